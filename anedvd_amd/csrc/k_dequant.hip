@@ -1,0 +1,374 @@
+// k_dequant.hip -- GGUF block dequantisation (bit-exact f32) and the repack of
+// GGUF expert tensors into the HBM tile layout the GEMV/GEMM kernels read.
+//
+// Every block routine follows the reference dequantiser named beside it
+// (gguf.zig:743-1071) in the same f32 operations.  Each product of a quant and
+// its scale is exact in f32 (see DESIGN.md's dequant note), so contraction could
+// not change a value; it is switched off anyway so the code says what it does.
+#pragma clang fp contract(off)
+
+#include "common.h"
+#include "kernels.h"
+
+namespace anedvd {
+
+__device__ inline uint16_t rd16(const uint8_t *b) { return (uint16_t)(b[0] | (b[1] << 8)); }
+__device__ inline uint32_t rd32(const uint8_t *b)
+{
+    return (uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) | ((uint32_t)b[3] << 24);
+}
+__device__ inline float h2f(const uint8_t *b) { return f16_bits_to_f32(rd16(b)); }
+__device__ inline float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// dequantQ4_0, gguf.zig:763-776
+__device__ void deq_q4_0(const uint8_t *blk, float *y)
+{
+    const float d = h2f(blk);
+    for (int j = 0; j < 16; j++) {
+        const uint8_t q = blk[2 + j];
+        y[j] = (float)((int)(q & 0x0F) - 8) * d;
+        y[j + 16] = (float)((int)(q >> 4) - 8) * d;
+    }
+}
+
+// dequantQ4_1, gguf.zig:778-793
+__device__ void deq_q4_1(const uint8_t *blk, float *y)
+{
+    const float d = h2f(blk), m = h2f(blk + 2);
+    for (int j = 0; j < 16; j++) {
+        const uint8_t q = blk[4 + j];
+        y[j] = (float)(q & 0x0F) * d + m;
+        y[j + 16] = (float)(q >> 4) * d + m;
+    }
+}
+
+// dequantQ5 (q5_0 / q5_1), gguf.zig:795-825
+__device__ void deq_q5(const uint8_t *blk, float *y, bool has_min)
+{
+    const int qh_off = has_min ? 4 : 2, qs_off = qh_off + 4, minus = has_min ? 0 : 16;
+    const float d = h2f(blk), m = has_min ? h2f(blk + 2) : 0.0f;
+    const uint32_t qh = rd32(blk + qh_off);
+    for (int j = 0; j < 16; j++) {
+        const uint8_t q = blk[qs_off + j];
+        const uint32_t xh0 = ((qh >> j) << 4) & 0x10u, xh1 = (qh >> (j + 12)) & 0x10u;
+        y[j] = (float)((int)((q & 0x0F) | xh0) - minus) * d + m;
+        y[j + 16] = (float)((int)((q >> 4) | xh1) - minus) * d + m;
+    }
+}
+
+// dequantQ8_0, gguf.zig:827-840
+__device__ void deq_q8_0(const uint8_t *blk, float *y)
+{
+    const float d = h2f(blk);
+    for (int j = 0; j < 32; j++) y[j] = d * (float)(int8_t)blk[2 + j];
+}
+
+// dequantQ8_1, gguf.zig:842-853
+__device__ void deq_q8_1(const uint8_t *blk, float *y)
+{
+    const float d = h2f(blk);
+    for (int j = 0; j < 32; j++) y[j] = (float)(int8_t)blk[4 + j] * d;
+}
+
+// dequantQ2K, gguf.zig:855-890
+__device__ void deq_q2_k(const uint8_t *blk, float *y)
+{
+    const float d = h2f(blk + 80), mn = h2f(blk + 82);
+    int q = 16, is = 0, o = 0;
+    for (int half = 0; half < 2; half++) {
+        int shift = 0;
+        for (int g = 0; g < 4; g++) {
+            for (int part = 0; part < 2; part++) {
+                const uint8_t sc = blk[is++];
+                const float dl = d * (float)(sc & 0x0F), ml = mn * (float)(sc >> 4);
+                for (int l = 0; l < 16; l++) y[o + l] = dl * (float)((blk[q + l + 16 * part] >> shift) & 3) - ml;
+                o += 16;
+            }
+            shift += 2;
+        }
+        q += 32;
+    }
+}
+
+// dequantQ3K, gguf.zig:892-946
+__device__ void deq_q3_k(const uint8_t *blk, float *y)
+{
+    const uint32_t kmask1 = 0x03030303u, kmask2 = 0x0f0f0f0fu;
+    const float d_all = h2f(blk + 108);
+    const uint8_t *hm = blk, *qs = blk + 32;
+    uint32_t aux[4] = { rd32(blk + 96), rd32(blk + 100), rd32(blk + 104), 0 };
+    const uint32_t tmp = aux[2];
+    aux[2] = ((aux[0] >> 4) & kmask2) | (((tmp >> 4) & kmask1) << 4);
+    aux[3] = ((aux[1] >> 4) & kmask2) | (((tmp >> 6) & kmask1) << 4);
+    aux[0] = (aux[0] & kmask2) | (((tmp >> 0) & kmask1) << 4);
+    aux[1] = (aux[1] & kmask2) | (((tmp >> 2) & kmask1) << 4);
+    uint8_t m = 1;
+    int is = 0, q = 0, o = 0;
+    for (int half = 0; half < 2; half++) {
+        int shift = 0;
+        for (int g = 0; g < 4; g++) {
+            for (int part = 0; part < 2; part++) {
+                const int8_t sc = (int8_t)(uint8_t)(aux[is >> 2] >> (8 * (is & 3)));
+                is++;
+                const float dl = d_all * (float)((int)sc - 32);
+                for (int l = 0; l < 16; l++) {
+                    const int low = (qs[q + l + 16 * part] >> shift) & 3;
+                    y[o + l] = dl * (float)(low - ((hm[l + 16 * part] & m) ? 0 : 4));
+                }
+                o += 16;
+            }
+            shift += 2;
+            m = (uint8_t)(m << 1);
+        }
+        q += 32;
+    }
+}
+
+// getScaleMinK4, gguf.zig:948-958
+__device__ inline void scale_min_k4(int j, const uint8_t *q, int &d, int &m)
+{
+    if (j < 4) {
+        d = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// dequantQ4K, gguf.zig:960-996
+__device__ void deq_q4_k(const uint8_t *blk, float *y)
+{
+    const float d = h2f(blk), mn = h2f(blk + 2);
+    const uint8_t *scales = blk + 4;
+    int q = 16;
+    for (int is = 0; is < 8; is += 2) {
+        int sd, sm;
+        scale_min_k4(is, scales, sd, sm);
+        const float d1 = d * (float)sd, m1 = mn * (float)sm;
+        scale_min_k4(is + 1, scales, sd, sm);
+        const float d2 = d * (float)sd, m2 = mn * (float)sm;
+        float *yy = y + (is / 2) * 64;
+        for (int l = 0; l < 32; l++) {
+            yy[l] = d1 * (float)(blk[q + l] & 0x0F) - m1;
+            yy[l + 32] = d2 * (float)(blk[q + l] >> 4) - m2;
+        }
+        q += 32;
+    }
+}
+
+// dequantQ5K, gguf.zig:998-1034
+__device__ void deq_q5_k(const uint8_t *blk, float *y)
+{
+    const float d = h2f(blk), mn = h2f(blk + 2);
+    const uint8_t *scales = blk + 4, *qh = blk + 16;
+    int ql = 48;
+    uint8_t mask1 = 1, mask2 = 2;
+    for (int is = 0; is < 8; is += 2) {
+        int sd, sm;
+        scale_min_k4(is, scales, sd, sm);
+        const float d1 = d * (float)sd, m1 = mn * (float)sm;
+        scale_min_k4(is + 1, scales, sd, sm);
+        const float d2 = d * (float)sd, m2 = mn * (float)sm;
+        float *yy = y + (is / 2) * 64;
+        for (int l = 0; l < 32; l++) yy[l] = d1 * (float)((blk[ql + l] & 0x0F) + ((qh[l] & mask1) ? 16 : 0)) - m1;
+        for (int l = 0; l < 32; l++) yy[l + 32] = d2 * (float)((blk[ql + l] >> 4) + ((qh[l] & mask2) ? 16 : 0)) - m2;
+        ql += 32;
+        mask1 = (uint8_t)(mask1 << 2);
+        mask2 = (uint8_t)(mask2 << 2);
+    }
+}
+
+// dequantQ6K, gguf.zig:1036-1059
+__device__ void deq_q6_k(const uint8_t *blk, float *y)
+{
+    const float d = h2f(blk + 208);
+    for (int half = 0; half < 2; half++) {
+        const uint8_t *ql = blk + half * 64, *qh = blk + 128 + half * 32, *sc = blk + 192 + half * 8;
+        float *yy = y + half * 128;
+        for (int l = 0; l < 32; l++) {
+            const int is = l / 16;
+            const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            yy[l] = d * (float)(int8_t)sc[is] * (float)q1;
+            yy[l + 32] = d * (float)(int8_t)sc[is + 2] * (float)q2;
+            yy[l + 64] = d * (float)(int8_t)sc[is + 4] * (float)q3;
+            yy[l + 96] = d * (float)(int8_t)sc[is + 6] * (float)q4;
+        }
+    }
+}
+
+// dequantQ8K, gguf.zig:1061-1071
+__device__ void deq_q8_k(const uint8_t *blk, float *y)
+{
+    const float d = u2f(rd32(blk));
+    for (int j = 0; j < 256; j++) y[j] = (float)(int8_t)blk[4 + j] * d;
+}
+
+__device__ void deq_block(int t, const uint8_t *blk, float *y)
+{
+    switch (t) {
+    case ANEDVD_F32: y[0] = u2f(rd32(blk)); break;
+    case ANEDVD_F16: y[0] = h2f(blk); break;
+    case ANEDVD_BF16: y[0] = u2f((uint32_t)rd16(blk) << 16); break;
+    case ANEDVD_Q4_0: deq_q4_0(blk, y); break;
+    case ANEDVD_Q4_1: deq_q4_1(blk, y); break;
+    case ANEDVD_Q5_0: deq_q5(blk, y, false); break;
+    case ANEDVD_Q5_1: deq_q5(blk, y, true); break;
+    case ANEDVD_Q8_0: deq_q8_0(blk, y); break;
+    case ANEDVD_Q8_1: deq_q8_1(blk, y); break;
+    case ANEDVD_Q2_K: deq_q2_k(blk, y); break;
+    case ANEDVD_Q3_K: deq_q3_k(blk, y); break;
+    case ANEDVD_Q4_K: deq_q4_k(blk, y); break;
+    case ANEDVD_Q5_K: deq_q5_k(blk, y); break;
+    case ANEDVD_Q6_K: deq_q6_k(blk, y); break;
+    case ANEDVD_Q8_K: deq_q8_k(blk, y); break;
+    default: break;
+    }
+}
+
+// One thread per GGUF block: src holds n_blocks whole blocks.
+__global__ void k_dequant_gguf(int t, const uint8_t *__restrict__ src, size_t n_blocks, float *__restrict__ out)
+{
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n_blocks) return;
+    const int epb = block_elems(t), bpb = block_bytes(t);
+    deq_block(t, src + b * bpb, out + b * epb);
+}
+
+// ------------------------------------------------------------------ repack
+
+// One thread per (matrix, row, unit): copies the unit's GGUF bytes into the tile
+// layout (common.h).  `src` is the stacked payload, matrices slowest.
+__global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
+{
+    const Fmt f = tile_fmt(m.type);
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t per_mat = (size_t)m.rows * m.units;
+    if (id >= per_mat * m.n) return;
+    const int mat = (int)(id / per_mat);
+    const int r = (int)((id % per_mat) / m.units), u = (int)(id % m.units);
+    const int rg = r / kRowGroup, lane = r % kRowGroup;
+    const int bpb = block_bytes(m.type), epb = block_elems(m.type);
+    const uint8_t *row = src + (size_t)mat * m.rows * ((size_t)m.cols / epb * bpb) + (size_t)r * ((size_t)m.cols / epb * bpb);
+    const uint8_t *unit = row + (size_t)u * (f.unit / epb) * bpb;
+    uint8_t *q = m.q + (size_t)mat * m.q_stride;
+    uint8_t *s = m.s ? m.s + (size_t)mat * m.s_stride : nullptr;
+    uint8_t qb[208];
+    int nq = 0;
+    switch (m.type) {
+    case ANEDVD_Q8_0:  // two blocks: [d][32 qs] x 2
+        for (int b = 0; b < 2; b++) {
+            for (int j = 0; j < 32; j++) qb[nq++] = unit[b * 34 + 2 + j];
+            s[tile_s_off(f, m.units, rg, u, lane) + 2 * b] = unit[b * 34];
+            s[tile_s_off(f, m.units, rg, u, lane) + 2 * b + 1] = unit[b * 34 + 1];
+        }
+        break;
+    case ANEDVD_Q4_0:  // two blocks: [d][16 qs] x 2
+        for (int b = 0; b < 2; b++) {
+            for (int j = 0; j < 16; j++) qb[nq++] = unit[b * 18 + 2 + j];
+            s[tile_s_off(f, m.units, rg, u, lane) + 2 * b] = unit[b * 18];
+            s[tile_s_off(f, m.units, rg, u, lane) + 2 * b + 1] = unit[b * 18 + 1];
+        }
+        break;
+    case ANEDVD_Q4_K:  // the 144-byte block as is
+        for (int j = 0; j < 144; j++) qb[nq++] = unit[j];
+        break;
+    case ANEDVD_Q6_K:  // ql, qh, scales as is; d to the scale plane
+        for (int j = 0; j < 208; j++) qb[nq++] = unit[j];
+        s[tile_s_off(f, m.units, rg, u, lane)] = unit[208];
+        s[tile_s_off(f, m.units, rg, u, lane) + 1] = unit[209];
+        break;
+    default:
+        return;
+    }
+    for (int c = 0; c < f.chunks; c++) {
+        uint8_t *dst = q + tile_q_off(f, m.units, rg, u, c, lane);
+        for (int j = 0; j < 16; j++) dst[j] = qb[c * 16 + j];
+    }
+}
+
+// Rebuilds the GGUF bytes of one unit from the tile layout.
+__device__ int unit_gguf_bytes(const QMat &m, int mat, int r, int u, uint8_t *blk)
+{
+    const Fmt f = tile_fmt(m.type);
+    const int rg = r / kRowGroup, lane = r % kRowGroup;
+    const uint8_t *q = m.q + (size_t)mat * m.q_stride;
+    const uint8_t *s = m.s ? m.s + (size_t)mat * m.s_stride : nullptr;
+    uint8_t qb[208];
+    for (int c = 0; c < f.chunks; c++) {
+        const uint8_t *src = q + tile_q_off(f, m.units, rg, u, c, lane);
+        for (int j = 0; j < 16; j++) qb[c * 16 + j] = src[j];
+    }
+    const uint8_t *sc = s ? s + tile_s_off(f, m.units, rg, u, lane) : nullptr;
+    switch (m.type) {
+    case ANEDVD_Q8_0:
+        for (int b = 0; b < 2; b++) {
+            blk[b * 34] = sc[2 * b];
+            blk[b * 34 + 1] = sc[2 * b + 1];
+            for (int j = 0; j < 32; j++) blk[b * 34 + 2 + j] = qb[b * 32 + j];
+        }
+        return 2;
+    case ANEDVD_Q4_0:
+        for (int b = 0; b < 2; b++) {
+            blk[b * 18] = sc[2 * b];
+            blk[b * 18 + 1] = sc[2 * b + 1];
+            for (int j = 0; j < 16; j++) blk[b * 18 + 2 + j] = qb[b * 16 + j];
+        }
+        return 2;
+    case ANEDVD_Q4_K:
+        for (int j = 0; j < 144; j++) blk[j] = qb[j];
+        return 1;
+    case ANEDVD_Q6_K:
+        for (int j = 0; j < 208; j++) blk[j] = qb[j];
+        blk[208] = sc[0];
+        blk[209] = sc[1];
+        return 1;
+    }
+    return 0;
+}
+
+// One thread per (row, unit) of matrix `mat`: out[rows][cols] f32, bit-exact.
+__global__ void k_dequant_tiles(QMat m, int mat, float *__restrict__ out)
+{
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (size_t)m.rows * m.units) return;
+    const int r = (int)(id / m.units), u = (int)(id % m.units);
+    const Fmt f = tile_fmt(m.type);
+    uint8_t blk[210 * 2];
+    const int nb = unit_gguf_bytes(m, mat, r, u, blk);
+    const int bpb = block_bytes(m.type), epb = block_elems(m.type);
+    float *y = out + (size_t)r * m.cols + (size_t)u * f.unit;
+    for (int b = 0; b < nb; b++) deq_block(m.type, blk + b * bpb, y + b * epb);
+}
+
+// ------------------------------------------------------------------ launchers
+
+int launch_dequant_gguf(int t, const uint8_t *d_src, size_t n_blocks, float *d_out, hipStream_t st)
+{
+    if (n_blocks == 0) return ANEDVD_OK;
+    const unsigned grid = (unsigned)((n_blocks + 255) / 256);
+    hipLaunchKernelGGL(k_dequant_gguf, dim3(grid), dim3(256), 0, st, t, d_src, n_blocks, d_out);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
+int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st)
+{
+    const size_t n = (size_t)m.n * m.rows * m.units;
+    hipLaunchKernelGGL(k_repack, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, d_src);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
+int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st)
+{
+    const size_t n = (size_t)m.rows * m.units;
+    hipLaunchKernelGGL(k_dequant_tiles, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, mat, d_out);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
+}  // namespace anedvd

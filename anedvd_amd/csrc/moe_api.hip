@@ -1,0 +1,802 @@
+// moe_api.hip -- the extern "C" boundary (include/anedvd_moe.h): contexts,
+// resident layers, and the forward pass as a stream-ordered chain of kernels
+//   router -> route -> dispatch -> expert gate/up -> expert down
+//   [-> shared gate/up -> shared down] -> combine
+// with no host synchronisation inside a forward.
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace anedvd {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+}  // namespace anedvd
+
+using namespace anedvd;
+
+// Device workspace of one context, carved from one allocation and grown on demand.
+struct Workspace {
+    void *base = nullptr;
+    size_t cap = 0;
+};
+
+struct anedvd_moe_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    Workspace ws;
+    Workspace io;  // staging for the host-pointer entry points
+};
+
+struct anedvd_moe_layer {
+    anedvd_moe_ctx *ctx = nullptr;
+    uint32_t H = 0, I = 0, E = 0, k = 0;
+    int norm = 0, gelu = 0;
+    QMat gate{}, up{}, down{};
+    uint16_t *router = nullptr;
+    uint32_t Is = 0;
+    QMat sgate{}, sup{}, sdown{};
+    uint16_t *sgate_lin = nullptr;
+    uint64_t device_bytes = 0;
+    double expert_bytes = 0, shared_bytes = 0;
+};
+
+namespace {
+
+struct Carve {
+    uint8_t *p;
+    template <class T>
+    T *take(size_t n)
+    {
+        T *r = (T *)p;
+        p += (n * sizeof(T) + 255) & ~(size_t)255;
+        return r;
+    }
+};
+
+int ensure(Workspace &w, size_t bytes, hipStream_t st)
+{
+    if (w.cap >= bytes) return ANEDVD_OK;
+    if (w.base) {
+        ANEDVD_HIP(hipStreamSynchronize(st));
+        ANEDVD_HIP(hipFree(w.base));
+        w.base = nullptr;
+        w.cap = 0;
+    }
+    const size_t want = std::max(bytes, (size_t)1 << 20);
+    ANEDVD_HIP(hipMalloc(&w.base, want));
+    w.cap = want;
+    return ANEDVD_OK;
+}
+
+bool tile_type(int t) { return tile_fmt(t).unit != 0; }
+
+int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, size_t bytes, hipStream_t st,
+              uint64_t &dev_bytes, const char *what)
+{
+    const Fmt f = tile_fmt(type);
+    if (!tile_type(type)) {
+        set_error("%s: ggml type %d is not supported by the GPU layout (q8_0, q4_0, q4_k, q6_k)", what, type);
+        return ANEDVD_E_UNSUPPORTED_TYPE;
+    }
+    if (rows % kRowGroup || cols % f.unit) {
+        set_error("%s: %d x %d is not a multiple of 64 rows x %d columns", what, rows, cols, f.unit);
+        return ANEDVD_E_INVALID_SHAPE;
+    }
+    const size_t per = (size_t)rows * cols / block_elems(type) * block_bytes(type);
+    if (bytes != per * n) {
+        set_error("%s: %zu bytes given, %d x %d x %d of type %d needs %zu", what, bytes, n, rows, cols, type, per * n);
+        return ANEDVD_E_DIMENSION;
+    }
+    m.type = type;
+    m.rows = rows;
+    m.cols = cols;
+    m.n = n;
+    m.units = cols / f.unit;
+    m.q_stride = (size_t)rows * m.units * f.chunks * 16;
+    m.s_stride = (size_t)rows * m.units * f.sbytes;
+    ANEDVD_HIP(hipMalloc(&m.q, m.q_stride * n));
+    if (m.s_stride) ANEDVD_HIP(hipMalloc(&m.s, m.s_stride * n));
+    dev_bytes += m.q_stride * n + m.s_stride * n;
+    uint8_t *staging = nullptr;
+    ANEDVD_HIP(hipMalloc(&staging, bytes));
+    hipError_t e = hipMemcpyAsync(staging, host, bytes, hipMemcpyHostToDevice, st);
+    int rc = e == hipSuccess ? launch_repack(m, staging, st) : ANEDVD_E_HIP;
+    if (e != hipSuccess) set_error("%s: upload failed: %s", what, hipGetErrorString(e));
+    hipError_t e2 = hipStreamSynchronize(st);
+    (void)hipFree(staging);
+    if (rc != ANEDVD_OK) return rc;
+    if (e2 != hipSuccess) {
+        set_error("%s: repack failed: %s", what, hipGetErrorString(e2));
+        return ANEDVD_E_HIP;
+    }
+    return ANEDVD_OK;
+}
+
+void free_qmat(QMat &m)
+{
+    if (m.q) (void)hipFree(m.q);
+    if (m.s) (void)hipFree(m.s);
+    m.q = nullptr;
+    m.s = nullptr;
+}
+
+// Splits the K axis over ks workgroups so that max_u * row_groups * ks reaches
+// about 1024 workgroups (4 per CU), keeping >= min_units units per workgroup.
+int choose_ks(int units, int row_groups, int max_u, int min_units)
+{
+    int best = 1;
+    for (int ks = 1; ks <= 16; ks++) {
+        if (units % ks || units / ks < min_units) continue;
+        best = ks;
+        if ((long)max_u * row_groups * ks >= 1024) break;
+    }
+    return best;
+}
+
+// All device scratch of one forward call of T tokens.
+struct Fwd {
+    float *logits, *probs, *part, *ypart, *sh_part, *sh_ypart, *sh_scale;
+    uint32_t *idx;
+    int32_t *offsets, *rows, *slots, *inv, *active, *meta;
+    int32_t *sh_offsets, *sh_rows, *sh_active, *sh_meta;
+    float *h_in, *l_in, *out;  // staging for host-pointer calls
+    int KSg, KSd, sKSg, sKSd, max_u;
+};
+
+size_t fwd_layout(const anedvd_moe_layer *L, int T, Fwd *f, uint8_t *base, bool with_io)
+{
+    const int H = L->H, I = L->I, E = L->E, k = L->k, P = T * k;
+    const int ug = gemv_unit_elems(L->gate.type), ud = gemv_unit_elems(L->down.type);
+    Fwd x{};
+    x.max_u = std::min(E, P);
+    x.KSg = ug ? choose_ks(H / ug, I / 64, x.max_u, 4) : 1;
+    x.KSd = ud ? choose_ks(I / ud, H / 64, x.max_u, 4) : 1;
+    if (L->Is) {
+        const int usg = gemv_unit_elems(L->sgate.type), usd = gemv_unit_elems(L->sdown.type);
+        x.sKSg = usg ? choose_ks(H / usg, L->Is / 64, 1, 4) : 1;
+        x.sKSd = usd ? choose_ks(L->Is / usd, H / 64, 1, 4) : 1;
+    }
+    Carve c{base};
+    x.logits = c.take<float>((size_t)T * E);
+    x.probs = c.take<float>(P);
+    x.idx = c.take<uint32_t>(P);
+    x.offsets = c.take<int32_t>(E + 1);
+    x.rows = c.take<int32_t>(P);
+    x.slots = c.take<int32_t>(P);
+    x.inv = c.take<int32_t>(P);
+    x.active = c.take<int32_t>(E);
+    x.meta = c.take<int32_t>(4);
+    x.part = c.take<float>((size_t)x.KSg * P * 2 * I);
+    x.ypart = c.take<float>((size_t)x.KSd * P * H);
+    if (L->Is) {
+        x.sh_part = c.take<float>((size_t)x.sKSg * T * 2 * L->Is);
+        x.sh_ypart = c.take<float>((size_t)x.sKSd * T * H);
+        x.sh_scale = c.take<float>(T);
+        x.sh_offsets = c.take<int32_t>(2);
+        x.sh_rows = c.take<int32_t>(T);
+        x.sh_active = c.take<int32_t>(1);
+        x.sh_meta = c.take<int32_t>(4);
+    }
+    if (with_io) {
+        x.h_in = c.take<float>((size_t)T * H);
+        x.l_in = c.take<float>((size_t)T * E);
+        x.out = c.take<float>((size_t)T * H);
+    }
+    if (f) *f = x;
+    return (size_t)(c.p - base);
+}
+
+// Fills the shared expert's one-expert dispatch (all T tokens, in order) and,
+// if it is gated, its per-token scale sigmoid(shared_gate_lin . h).
+__global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__restrict__ lin, int T, int H,
+                              int32_t *offsets, int32_t *rows, int32_t *active, int32_t *meta, float *scale)
+{
+    const int t = blockIdx.x;
+    if (t == 0 && threadIdx.x == 0) {
+        offsets[0] = 0;
+        offsets[1] = T;
+        active[0] = 0;
+        meta[0] = 1;
+        meta[1] = T;
+        meta[2] = 0;
+    }
+    if (threadIdx.x == 0) rows[t] = t;
+    if (!lin) return;
+    // one wavefront per token; sigmoid as cpu.sigmoid (cpu.zig:1223-1230)
+    float g = 0.0f;
+    for (int i = threadIdx.x; i < H; i += 64) g += f16_bits_to_f32(lin[i]) * h[(size_t)t * H + i];
+    for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o, 64);
+    if (threadIdx.x == 0) {
+        float s;
+        if (g >= 0) s = 1.0f / (1.0f + __expf(-fminf(g, 80.0f)));
+        else {
+            const float ex = __expf(fmaxf(g, -80.0f));
+            s = ex / (1.0f + ex);
+        }
+        scale[t] = s;
+    }
+}
+
+int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_logits, float *d_out, const Fwd &f,
+                   hipStream_t st, hipEvent_t *ev)
+{
+    const int H = L->H, I = L->I, E = L->E, k = L->k, P = T * k;
+    auto mark = [&](int i) {
+        if (ev) (void)hipEventRecord(ev[i], st);
+    };
+    mark(0);
+    const float *logits = d_logits;
+    if (!logits) {
+        ANEDVD_TRY(launch_router(L->router, d_h, T, E, H, f.logits, st));
+        logits = f.logits;
+    }
+    ANEDVD_TRY(launch_route(logits, T, E, k, L->norm, f.probs, f.idx, st));
+    ANEDVD_TRY(launch_dispatch(f.idx, T, k, E, f.offsets, f.rows, f.slots, f.inv, f.active, f.meta, st));
+    mark(1);
+    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, d_h, f.offsets, f.rows, f.active, f.meta, f.part, H, I, f.KSg, P,
+                                    f.max_u, st));
+    mark(2);
+    ANEDVD_TRY(launch_expert_down(L->down, f.part, f.offsets, f.active, f.meta, f.ypart, H, I, f.KSd, f.KSg, P, L->gelu,
+                                  f.max_u, st));
+    mark(3);
+    if (L->Is) {
+        hipLaunchKernelGGL(k_shared_prep, dim3(T), dim3(64), 0, st, d_h, L->sgate_lin, T, H, f.sh_offsets, f.sh_rows,
+                           f.sh_active, f.sh_meta, f.sh_scale);
+        ANEDVD_HIP(hipGetLastError());
+        ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, d_h, f.sh_offsets, f.sh_rows, f.sh_active, f.sh_meta,
+                                        f.sh_part, H, L->Is, f.sKSg, T, 1, st));
+        ANEDVD_TRY(launch_expert_down(L->sdown, f.sh_part, f.sh_offsets, f.sh_active, f.sh_meta, f.sh_ypart, H, L->Is,
+                                      f.sKSd, f.sKSg, T, L->gelu, 1, st));
+    }
+    mark(4);
+    ANEDVD_TRY(launch_combine(f.ypart, f.inv, f.probs, T, k, H, f.KSd, P, L->Is ? f.sh_ypart : nullptr,
+                              (L->Is && L->sgate_lin) ? f.sh_scale : nullptr, L->Is ? f.sKSd : 0, d_out, st));
+    mark(5);
+    return ANEDVD_OK;
+}
+
+int check_layer(const anedvd_moe_layer *L)
+{
+    if (!L || !L->ctx) {
+        set_error("null layer");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    return ANEDVD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *anedvd_moe_last_error(void) { return g_err; }
+
+int anedvd_moe_abi_version(void) { return ANEDVD_MOE_ABI_VERSION; }
+
+int anedvd_moe_open(int device, anedvd_moe_ctx **out)
+{
+    if (!out) {
+        set_error("anedvd_moe_open: out is null");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) {
+        set_error("anedvd_moe_open: device %d not present (%d HIP devices)", device, n);
+        return ANEDVD_E_NO_DEVICE;
+    }
+    hipDeviceProp_t prop;
+    ANEDVD_HIP(hipGetDeviceProperties(&prop, device));
+    if (!strstr(prop.gcnArchName, "gfx950")) {
+        set_error("anedvd_moe_open: device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+        return ANEDVD_E_NO_DEVICE;
+    }
+    ANEDVD_HIP(hipSetDevice(device));
+    anedvd_moe_ctx *c = new anedvd_moe_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        set_error("anedvd_moe_open: stream creation failed");
+        return ANEDVD_E_HIP;
+    }
+    *out = c;
+    return ANEDVD_OK;
+}
+
+void anedvd_moe_close(anedvd_moe_ctx *ctx)
+{
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws.base) (void)hipFree(ctx->ws.base);
+    if (ctx->io.base) (void)hipFree(ctx->io.base);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *d, anedvd_moe_layer **out)
+{
+    if (!ctx || !d || !out) {
+        set_error("anedvd_moe_layer_create: null argument");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    *out = nullptr;
+    if (!d->hidden || !d->inter || !d->n_experts || !d->k || d->k > d->n_experts || d->n_experts > 256 || d->k > 32 ||
+        !d->gate || !d->up || !d->down || !d->router) {
+        set_error("anedvd_moe_layer_create: bad shape H=%u I=%u E=%u k=%u (need 0 < k <= E <= 256, k <= 32) or missing tensor",
+                  d->hidden, d->inter, d->n_experts, d->k);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    if (d->hidden % 64) {
+        set_error("anedvd_moe_layer_create: hidden %u is not a multiple of 64", d->hidden);
+        return ANEDVD_E_INVALID_SHAPE;
+    }
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    anedvd_moe_layer *L = new anedvd_moe_layer();
+    L->ctx = ctx;
+    L->H = d->hidden;
+    L->I = d->inter;
+    L->E = d->n_experts;
+    L->k = d->k;
+    L->norm = d->norm_topk_prob != 0;
+    L->gelu = d->use_gelu != 0;
+    const int H = (int)d->hidden, I = (int)d->inter, E = (int)d->n_experts;
+    int rc = make_qmat(L->gate, d->gate_type, I, H, E, d->gate, d->gate_bytes, ctx->stream, L->device_bytes, "gate");
+    if (!rc) rc = make_qmat(L->up, d->up_type, I, H, E, d->up, d->up_bytes, ctx->stream, L->device_bytes, "up");
+    if (!rc) rc = make_qmat(L->down, d->down_type, H, I, E, d->down, d->down_bytes, ctx->stream, L->device_bytes, "down");
+    if (!rc) {
+        const size_t rb = (size_t)E * H * 2;
+        if (hipMalloc(&L->router, rb) != hipSuccess || hipMemcpy(L->router, d->router, rb, hipMemcpyHostToDevice) != hipSuccess) {
+            set_error("router upload failed");
+            rc = ANEDVD_E_HIP;
+        }
+        L->device_bytes += rb;
+    }
+    if (!rc && d->shared_inter) {
+        const int Is = (int)d->shared_inter;
+        L->Is = d->shared_inter;
+        rc = make_qmat(L->sgate, d->shared_type, Is, H, 1, d->shared_gate, d->shared_gate_bytes, ctx->stream,
+                       L->device_bytes, "shared gate");
+        if (!rc) rc = make_qmat(L->sup, d->shared_type, Is, H, 1, d->shared_up, d->shared_up_bytes, ctx->stream,
+                                L->device_bytes, "shared up");
+        if (!rc) rc = make_qmat(L->sdown, d->shared_type, H, Is, 1, d->shared_down, d->shared_down_bytes, ctx->stream,
+                                L->device_bytes, "shared down");
+        if (!rc && d->shared_gate_lin) {
+            if (hipMalloc(&L->sgate_lin, (size_t)H * 2) != hipSuccess ||
+                hipMemcpy(L->sgate_lin, d->shared_gate_lin, (size_t)H * 2, hipMemcpyHostToDevice) != hipSuccess) {
+                set_error("shared_gate_lin upload failed");
+                rc = ANEDVD_E_HIP;
+            }
+        }
+    }
+    if (rc) {
+        anedvd_moe_layer_free(L);
+        return rc;
+    }
+    auto bpw = [](int t) { return (double)block_bytes(t) / block_elems(t); };
+    L->expert_bytes = (double)I * H * (bpw(L->gate.type) + bpw(L->up.type) + bpw(L->down.type));
+    L->shared_bytes = L->Is ? 3.0 * H * L->Is * bpw(L->sgate.type) : 0.0;
+    *out = L;
+    return ANEDVD_OK;
+}
+
+void anedvd_moe_layer_free(anedvd_moe_layer *L)
+{
+    if (!L) return;
+    if (L->ctx) {
+        (void)hipSetDevice(L->ctx->device);
+        (void)hipStreamSynchronize(L->ctx->stream);
+    }
+    free_qmat(L->gate);
+    free_qmat(L->up);
+    free_qmat(L->down);
+    free_qmat(L->sgate);
+    free_qmat(L->sup);
+    free_qmat(L->sdown);
+    if (L->router) (void)hipFree(L->router);
+    if (L->sgate_lin) (void)hipFree(L->sgate_lin);
+    delete L;
+}
+
+uint64_t anedvd_moe_layer_device_bytes(const anedvd_moe_layer *L) { return L ? L->device_bytes : 0; }
+
+// ------------------------------------------------------------ op mirrors
+
+int anedvd_dequantize_range(anedvd_moe_ctx *ctx, int t, const void *src, size_t src_len, uint64_t elem_offset,
+                            float *out, size_t n)
+{
+    // The checks of dequantizeRange (gguf.zig:694-728), in its order.
+    const int epb = block_elems(t), bpb = block_bytes(t);
+    if (!epb || !bpb) {
+        set_error("dequantize_range: unsupported ggml type %d", t);
+        return ANEDVD_E_UNSUPPORTED_TYPE;
+    }
+    if (n == 0) return ANEDVD_OK;
+    if (n % epb || elem_offset % epb) {
+        set_error("dequantize_range: %zu elements at offset %llu are not whole blocks of %d", n,
+                  (unsigned long long)elem_offset, epb);
+        return ANEDVD_E_INVALID_SHAPE;
+    }
+    const uint64_t blocks_before = elem_offset / epb;
+    if (blocks_before > UINT64_MAX / bpb || blocks_before * bpb > src_len) {
+        set_error("dequantize_range: offset past the end of the data");
+        return ANEDVD_E_TRUNCATED;
+    }
+    const size_t start = (size_t)(blocks_before * bpb), blocks = n / epb;
+    if (src_len - start < blocks * (size_t)bpb) {
+        set_error("dequantize_range: %zu blocks need %zu bytes, %zu available", blocks, blocks * (size_t)bpb, src_len - start);
+        return ANEDVD_E_TRUNCATED;
+    }
+    if (!ctx || !src || !out) {
+        set_error("dequantize_range: null argument");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    const size_t in_b = blocks * bpb, out_b = n * sizeof(float);
+    ANEDVD_TRY(ensure(ctx->io, in_b + out_b + 512, ctx->stream));
+    uint8_t *d_in = (uint8_t *)ctx->io.base;
+    float *d_out = (float *)((uint8_t *)ctx->io.base + ((in_b + 255) & ~(size_t)255));
+    ANEDVD_HIP(hipMemcpyAsync(d_in, (const uint8_t *)src + start, in_b, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_TRY(launch_dequant_gguf(t, d_in, blocks, d_out, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(out, d_out, out_b, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_load_expert_f32(anedvd_moe_layer *L, int which, uint32_t expert, float *out, size_t n)
+{
+    ANEDVD_TRY(check_layer(L));
+    const QMat *m = which == 0 ? &L->gate : which == 1 ? &L->up : which == 2 ? &L->down : nullptr;
+    if (!m || !out) {
+        set_error("load_expert_f32: which must be 0 (gate), 1 (up) or 2 (down)");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    if (expert >= L->E) {
+        set_error("load_expert_f32: expert %u of %u", expert, L->E);
+        return ANEDVD_E_OUT_OF_RANGE;
+    }
+    if (n != (size_t)m->rows * m->cols) {
+        set_error("load_expert_f32: out holds %zu, expert has %d x %d", n, m->rows, m->cols);
+        return ANEDVD_E_DIMENSION;
+    }
+    anedvd_moe_ctx *ctx = L->ctx;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    ANEDVD_TRY(ensure(ctx->io, n * sizeof(float), ctx->stream));
+    ANEDVD_TRY(launch_dequant_tiles(*m, (int)expert, (float *)ctx->io.base, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(out, ctx->io.base, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+int anedvd_matmul_f16(anedvd_moe_ctx *ctx, float *out, const uint16_t *w, const float *x, size_t out_dim,
+                      size_t in_dim, size_t n_vec)
+{
+    if (!ctx || !out || !w || !x || !out_dim || !in_dim || out_dim > (1u << 30) || in_dim > (1u << 20)) {
+        set_error("matmul_f16: bad arguments");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    if (!n_vec) return ANEDVD_OK;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    const size_t wb = out_dim * in_dim * 2, xb = n_vec * in_dim * 4, ob = n_vec * out_dim * 4;
+    ANEDVD_TRY(ensure(ctx->io, wb + xb + ob + 1024, ctx->stream));
+    Carve c{(uint8_t *)ctx->io.base};
+    uint16_t *dw = c.take<uint16_t>(out_dim * in_dim);
+    float *dx = c.take<float>(n_vec * in_dim);
+    float *dout = c.take<float>(n_vec * out_dim);
+    ANEDVD_HIP(hipMemcpyAsync(dw, w, wb, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_TRY(launch_router(dw, dx, (int)n_vec, (int)out_dim, (int)in_dim, dout, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(out, dout, ob, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_route(anedvd_moe_ctx *ctx, const float *logits, size_t T, size_t E, size_t k, int norm, float *probs,
+                     uint32_t *idx)
+{
+    if (!ctx || !logits || !probs || !idx || T > (1u << 24)) {
+        set_error("moe_route: bad arguments");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    if (!T) return ANEDVD_OK;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    ANEDVD_TRY(ensure(ctx->io, T * E * 4 + T * k * 8 + 1024, ctx->stream));
+    Carve c{(uint8_t *)ctx->io.base};
+    float *dl = c.take<float>(T * E);
+    float *dp = c.take<float>(T * k);
+    uint32_t *di = c.take<uint32_t>(T * k);
+    ANEDVD_HIP(hipMemcpyAsync(dl, logits, T * E * 4, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, norm, dp, di, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(probs, dp, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(idx, di, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_dispatch(anedvd_moe_ctx *ctx, const uint32_t *idx, size_t T, size_t k, size_t E, int32_t *offsets,
+                        int32_t *rows, int32_t *slots)
+{
+    if (!ctx || !idx || !offsets || !rows || !slots || T > (1u << 24) || k > 64) {
+        set_error("moe_dispatch: bad arguments");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    if (!T) {
+        for (size_t e = 0; e <= E; e++) offsets[e] = 0;
+        return ANEDVD_OK;
+    }
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    const size_t P = T * k;
+    ANEDVD_TRY(ensure(ctx->io, P * 16 + E * 8 + 4096, ctx->stream));
+    Carve c{(uint8_t *)ctx->io.base};
+    uint32_t *di = c.take<uint32_t>(P);
+    int32_t *doff = c.take<int32_t>(E + 1);
+    int32_t *drows = c.take<int32_t>(P);
+    int32_t *dslots = c.take<int32_t>(P);
+    int32_t *dinv = c.take<int32_t>(P);
+    int32_t *dact = c.take<int32_t>(E);
+    int32_t *dmeta = c.take<int32_t>(4);
+    ANEDVD_HIP(hipMemcpyAsync(di, idx, P * 4, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_TRY(launch_dispatch(di, (int)T, (int)k, (int)E, doff, drows, dslots, dinv, dact, dmeta, ctx->stream));
+    int32_t meta[4];
+    ANEDVD_HIP(hipMemcpyAsync(offsets, doff, (E + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(rows, drows, P * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(slots, dslots, P * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(meta, dmeta, 16, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    if (meta[2]) {
+        set_error("moe_dispatch: %d expert ids >= %zu", meta[2], E);
+        return ANEDVD_E_OUT_OF_RANGE;
+    }
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h, float weight, float *out)
+{
+    ANEDVD_TRY(check_layer(L));
+    if (!h || !out || expert >= L->E) {
+        set_error("expert_accum: bad arguments (expert %u of %u)", expert, L->E);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    anedvd_moe_ctx *ctx = L->ctx;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    // One token routed to `expert` with probability `weight`: the same kernels as
+    // the forward, on a one-entry dispatch; out += the combined row.
+    const int H = (int)L->H, I = (int)L->I, E = (int)L->E;
+    const int ug = gemv_unit_elems(L->gate.type), ud = gemv_unit_elems(L->down.type);
+    if (!ug || !ud) {
+        set_error("expert_accum: no decode kernel for types %d/%d", L->gate.type, L->down.type);
+        return ANEDVD_E_UNSUPPORTED_TYPE;
+    }
+    const int KSg = choose_ks(H / ug, I / 64, 1, 4), KSd = choose_ks(I / ud, H / 64, 1, 4);
+    const size_t need = (size_t)H * 4 * 3 + (size_t)KSg * 2 * I * 4 + (size_t)KSd * H * 4 + (size_t)E * 8 + 8192;
+    ANEDVD_TRY(ensure(ctx->io, need, ctx->stream));
+    Carve c{(uint8_t *)ctx->io.base};
+    float *dh = c.take<float>(H);
+    float *dout = c.take<float>(H);
+    float *dpart = c.take<float>((size_t)KSg * 2 * I);
+    float *dy = c.take<float>((size_t)KSd * H);
+    int32_t *doff = c.take<int32_t>(E + 1);
+    int32_t *dmisc = c.take<int32_t>(8);  // rows[1], active[1], meta[4], inv[1]
+    float *dprob = c.take<float>(1);
+    std::vector<int32_t> off(E + 1);
+    for (int e = 0; e <= E; e++) off[e] = e > (int)expert ? 1 : 0;
+    const int32_t misc[8] = {0, (int32_t)expert, 1, 1, 0, 0, 0, 0};
+    ANEDVD_HIP(hipMemcpyAsync(dh, h, (size_t)H * 4, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(doff, off.data(), (size_t)(E + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(dmisc, misc, sizeof misc, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(dprob, &weight, 4, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, dh, doff, dmisc, dmisc + 1, dmisc + 2, dpart, H, I, KSg, 1, 1,
+                                    ctx->stream));
+    ANEDVD_TRY(launch_expert_down(L->down, dpart, doff, dmisc + 1, dmisc + 2, dy, H, I, KSd, KSg, 1, L->gelu, 1,
+                                  ctx->stream));
+    ANEDVD_TRY(launch_combine(dy, dmisc /* inv[0] = 0 */, dprob, 1, 1, H, KSd, 1, nullptr, nullptr, 0, dout,
+                              ctx->stream));
+    std::vector<float> y(H);
+    ANEDVD_HIP(hipMemcpyAsync(y.data(), dout, (size_t)H * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    for (int o = 0; o < H; o++) out[o] += y[o];  // `out[o] += weight * total` (cpu.zig:450)
+    return ANEDVD_OK;
+}
+
+// ------------------------------------------------------------------ layer
+
+int anedvd_moe_layer_route(anedvd_moe_layer *L, const float *h, size_t T, float *logits, float *probs, uint32_t *idx)
+{
+    ANEDVD_TRY(check_layer(L));
+    if (!h || !probs || !idx || T > (1u << 20)) {
+        set_error("layer_route: bad arguments");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    if (!T) return ANEDVD_OK;
+    anedvd_moe_ctx *ctx = L->ctx;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    const size_t H = L->H, E = L->E, k = L->k;
+    ANEDVD_TRY(ensure(ctx->io, T * H * 4 + T * E * 4 + T * k * 8 + 1024, ctx->stream));
+    Carve c{(uint8_t *)ctx->io.base};
+    float *dh = c.take<float>(T * H);
+    float *dl = c.take<float>(T * E);
+    float *dp = c.take<float>(T * k);
+    uint32_t *di = c.take<uint32_t>(T * k);
+    ANEDVD_HIP(hipMemcpyAsync(dh, h, T * H * 4, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_TRY(launch_router(L->router, dh, (int)T, (int)E, (int)H, dl, ctx->stream));
+    ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, L->norm, dp, di, ctx->stream));
+    if (logits) ANEDVD_HIP(hipMemcpyAsync(logits, dl, T * E * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(probs, dp, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(idx, di, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+static int prepare(anedvd_moe_layer *L, size_t T, bool io, Fwd &f)
+{
+    ANEDVD_TRY(check_layer(L));
+    if (T > (1u << 20)) {
+        set_error("forward: %zu tokens is more than this build handles per call", T);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    anedvd_moe_ctx *ctx = L->ctx;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    if (!gemv_unit_elems(L->gate.type) || !gemv_unit_elems(L->up.type) || !gemv_unit_elems(L->down.type) ||
+        L->gate.type != L->up.type || (L->Is && (!gemv_unit_elems(L->sgate.type)))) {
+        set_error("forward: no expert kernel for ggml types gate=%d up=%d down=%d yet", L->gate.type, L->up.type,
+                  L->down.type);
+        return ANEDVD_E_UNSUPPORTED_TYPE;
+    }
+    const size_t bytes = fwd_layout(L, (int)T, nullptr, (uint8_t *)0, io);
+    ANEDVD_TRY(ensure(ctx->ws, bytes + 4096, ctx->stream));
+    fwd_layout(L, (int)T, &f, (uint8_t *)ctx->ws.base, io);
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_layer_forward(anedvd_moe_layer *L, const float *h, size_t T, const float *logits, float *out,
+                             anedvd_moe_stats *stats)
+{
+    if (!h || !out) {
+        set_error("layer_forward: null h or out");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    Fwd f;
+    ANEDVD_TRY(prepare(L, T, true, f));
+    if (!T) return ANEDVD_OK;
+    hipStream_t st = L->ctx->stream;
+    ANEDVD_HIP(hipMemcpyAsync(f.h_in, h, T * L->H * 4, hipMemcpyHostToDevice, st));
+    if (logits) ANEDVD_HIP(hipMemcpyAsync(f.l_in, logits, T * L->E * 4, hipMemcpyHostToDevice, st));
+    ANEDVD_TRY(forward_device(L, f.h_in, (int)T, logits ? f.l_in : nullptr, f.out, f, st, nullptr));
+    int32_t meta[4] = {0, 0, 0, 0};
+    ANEDVD_HIP(hipMemcpyAsync(out, f.out, T * L->H * 4, hipMemcpyDeviceToHost, st));
+    ANEDVD_HIP(hipMemcpyAsync(meta, f.meta, 16, hipMemcpyDeviceToHost, st));
+    ANEDVD_HIP(hipStreamSynchronize(st));
+    if (stats) {
+        stats->n_tokens = (uint32_t)T;
+        stats->touched_experts = (uint32_t)meta[0];
+        stats->max_group = (uint32_t)meta[1];
+        stats->weight_bytes = (uint64_t)(meta[0] * L->expert_bytes + L->shared_bytes + (logits ? 0.0 : 2.0 * L->E * L->H));
+        stats->path = 0;
+    }
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_layer_forward_device(anedvd_moe_layer *L, const float *d_h, size_t T, const float *d_logits, float *d_out)
+{
+    if (!d_h || !d_out) {
+        set_error("layer_forward_device: null pointer");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    Fwd f;
+    ANEDVD_TRY(prepare(L, T, false, f));
+    if (!T) return ANEDVD_OK;
+    return forward_device(L, d_h, (int)T, d_logits, d_out, f, L->ctx->stream, nullptr);
+}
+
+// ------------------------------------------------------------ memory, timing
+
+int anedvd_moe_device_alloc(anedvd_moe_ctx *ctx, size_t bytes, void **p)
+{
+    if (!ctx || !p) return ANEDVD_E_INVALID_ARG;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    ANEDVD_HIP(hipMalloc(p, bytes));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_device_free(anedvd_moe_ctx *ctx, void *p)
+{
+    if (!ctx) return ANEDVD_E_INVALID_ARG;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    ANEDVD_HIP(hipFree(p));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_memcpy_h2d(anedvd_moe_ctx *ctx, void *d, const void *s, size_t n)
+{
+    if (!ctx) return ANEDVD_E_INVALID_ARG;
+    ANEDVD_HIP(hipMemcpyAsync(d, s, n, hipMemcpyHostToDevice, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_memcpy_d2h(anedvd_moe_ctx *ctx, void *d, const void *s, size_t n)
+{
+    if (!ctx) return ANEDVD_E_INVALID_ARG;
+    ANEDVD_HIP(hipMemcpyAsync(d, s, n, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_synchronize(anedvd_moe_ctx *ctx)
+{
+    if (!ctx) return ANEDVD_E_INVALID_ARG;
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, const float *d_h, size_t T,
+                            const float *d_logits, float *d_out, int warmup, int iters, float *ms, float *kernel_ms)
+{
+    if (!layers || !n_layers || !ms || iters <= 0 || warmup < 0) {
+        set_error("time_forward: bad arguments");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    anedvd_moe_ctx *ctx = layers[0]->ctx;
+    for (size_t i = 0; i < n_layers; i++)
+        if (!layers[i] || layers[i]->ctx != ctx || layers[i]->H != layers[0]->H || layers[i]->E != layers[0]->E) {
+            set_error("time_forward: layers must share a context and a shape");
+            return ANEDVD_E_INVALID_ARG;
+        }
+    hipStream_t st = ctx->stream;
+    Fwd f;
+    ANEDVD_TRY(prepare(layers[0], T, false, f));
+    for (int i = 0; i < warmup; i++)
+        ANEDVD_TRY(forward_device(layers[i % n_layers], d_h, (int)T, d_logits, d_out, f, st, nullptr));
+    hipEvent_t t0, t1;
+    ANEDVD_HIP(hipEventCreate(&t0));
+    ANEDVD_HIP(hipEventCreate(&t1));
+    ANEDVD_HIP(hipStreamSynchronize(st));
+    ANEDVD_HIP(hipEventRecord(t0, st));
+    for (int i = 0; i < iters; i++)
+        ANEDVD_TRY(forward_device(layers[i % n_layers], d_h, (int)T, d_logits, d_out, f, st, nullptr));
+    ANEDVD_HIP(hipEventRecord(t1, st));
+    ANEDVD_HIP(hipEventSynchronize(t1));
+    ANEDVD_HIP(hipEventElapsedTime(ms, t0, t1));
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    if (kernel_ms) {
+        std::vector<hipEvent_t> ev((size_t)iters * 6);
+        for (auto &e : ev) ANEDVD_HIP(hipEventCreate(&e));
+        for (int i = 0; i < iters; i++)
+            ANEDVD_TRY(forward_device(layers[i % n_layers], d_h, (int)T, d_logits, d_out, f, st, &ev[(size_t)i * 6]));
+        ANEDVD_HIP(hipStreamSynchronize(st));
+        double acc[6] = {0, 0, 0, 0, 0, 0};
+        for (int i = 0; i < iters; i++) {
+            hipEvent_t *e = &ev[(size_t)i * 6];
+            float x;
+            for (int s = 0; s < 5; s++) {
+                ANEDVD_HIP(hipEventElapsedTime(&x, e[s], e[s + 1]));
+                acc[s] += x;
+            }
+            ANEDVD_HIP(hipEventElapsedTime(&x, e[0], e[5]));
+            acc[5] += x;
+        }
+        // order: route, gate/up, down, shared, combine, total
+        for (int s = 0; s < 6; s++) kernel_ms[s] = (float)(acc[s] / iters);
+        for (auto &e : ev) (void)hipEventDestroy(e);
+    }
+    return ANEDVD_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,188 @@
+"""Seeded synthetic MoE layers and activations, reproducible on any host.
+
+Every random value is a pure function of (seed, stream, index): a SplitMix64
+finaliser over a counter, so the same bytes come out whether a whole tensor or
+one expert of it is generated, and whether on the build host or the GPU box.
+
+Quantised tensors are written in GGUF byte layout (the block structs of
+gguf.zig:763-1059), stacked `[E][rows][cols]` with the expert axis slowest, as
+`blk.N.ffn_*_exps.weight` is stored (gguf.zig:474-488).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import workloads as W
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+_GOLD = np.uint64(0x9E3779B97F4A7C15)
+
+
+def _mix(z: np.ndarray) -> np.ndarray:
+    z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def _key(seed: int, stream: int) -> np.uint64:
+    with np.errstate(over="ignore"):
+        s = np.array([(seed * 0x100000001B3 + stream * 0xC2B2AE3D27D4EB4F) & 0xFFFFFFFFFFFFFFFF], dtype=np.uint64)
+        return _mix(s + _GOLD)[0]
+
+
+def u64(seed: int, stream: int, n: int, offset: int = 0) -> np.ndarray:
+    """n uniform 64-bit words of stream `stream`, starting at counter `offset`."""
+    i = np.arange(offset, offset + n, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        return _mix(i * _GOLD + _key(seed, stream))
+
+
+def uniform(seed: int, stream: int, n: int, offset: int = 0) -> np.ndarray:
+    """Doubles in [0, 1)."""
+    return (u64(seed, stream, n, offset) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+
+
+def normal(seed: int, stream: int, n: int, offset: int = 0) -> np.ndarray:
+    """Standard normals (Box-Muller on two counters per value), float64."""
+    w = u64(seed, stream, 2 * n, 2 * offset)
+    u1 = ((w[0::2] >> np.uint64(11)).astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)
+    u2 = (w[1::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+    return np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+
+
+def rand_bytes(seed: int, stream: int, n: int, offset: int = 0) -> np.ndarray:
+    """n uniform bytes (8 per counter)."""
+    c0, c1 = offset // 8, (offset + n + 7) // 8
+    b = u64(seed, stream, c1 - c0, c0).view(np.uint8)
+    s = offset - c0 * 8
+    return b[s:s + n].copy()
+
+
+def _f16_abs_normal(seed, stream, n, sigma, offset=0, div=1.0):
+    return (np.abs(normal(seed, stream, n, offset)) * sigma / div).astype(np.float16)
+
+
+# ----------------------------------------------------------------- quant blocks
+
+def q8_0(seed: int, stream: int, n_blocks: int, sigma: float = 0.02, offset: int = 0) -> np.ndarray:
+    """Q8_0 blocks: d = f16(|N(0,sigma)|/127), qs uniform int8 in [-127, 127]."""
+    blk = np.empty((n_blocks, 34), dtype=np.uint8)
+    blk[:, 0:2] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset, 127.0).view(np.uint8).reshape(n_blocks, 2)
+    # 16-bit draws reduced mod 255 -> [-127, 127]
+    w = u64(seed, stream + 1, n_blocks * 8, offset * 8).view(np.uint16).astype(np.int32)
+    q = (w % 255 - 127).astype(np.int8)
+    blk[:, 2:] = q.view(np.uint8).reshape(n_blocks, 32)
+    return blk
+
+
+def q4_0(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q4_0 blocks: d = f16(|N(0,sigma)|), random nibbles."""
+    blk = np.empty((n_blocks, 18), dtype=np.uint8)
+    blk[:, 0:2] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 2:] = rand_bytes(seed, stream + 1, n_blocks * 16, offset * 16).reshape(n_blocks, 16)
+    return blk
+
+
+def q4_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q4_K super-blocks: d, dmin = f16(|N(0,sigma)|); random 12-byte packed 6-bit
+    scales/mins; random 4-bit quants."""
+    blk = np.empty((n_blocks, 144), dtype=np.uint8)
+    blk[:, 0:2] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 2:4] = _f16_abs_normal(seed, stream + 1, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 4:] = rand_bytes(seed, stream + 2, n_blocks * 140, offset * 140).reshape(n_blocks, 140)
+    return blk
+
+
+def q6_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q6_K super-blocks: random ql/qh, random int8 sub-block scales, d = f16(|N(0,sigma)|)."""
+    blk = np.empty((n_blocks, 210), dtype=np.uint8)
+    blk[:, 0:208] = rand_bytes(seed, stream + 1, n_blocks * 208, offset * 208).reshape(n_blocks, 208)
+    blk[:, 208:210] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    return blk
+
+
+_GEN = {W.Q8_0: q8_0, W.Q4_0: q4_0, W.Q4_K: q4_k, W.Q6_K: q6_k}
+
+
+def quant_matrix(t: int, seed: int, stream: int, n_elems: int, sigma: float, elem_offset: int = 0) -> np.ndarray:
+    epb, bpb = W.BLOCK[t]
+    assert n_elems % epb == 0 and elem_offset % epb == 0
+    return _GEN[t](seed, stream, n_elems // epb, sigma, elem_offset // epb).reshape(-1)
+
+
+# ------------------------------------------------------------------- layers
+
+_STREAM = {"gate": 100, "up": 200, "down": 300, "router": 400, "sh_gate": 500, "sh_up": 600,
+           "sh_down": 700, "sh_gate_lin": 800, "x": 900, "logits": 1000}
+
+
+def layer_seed(seed: int, layer: int) -> int:
+    return seed * 1000003 + layer
+
+
+def expert_tensor(spec: W.LayerSpec, which: str, seed: int, experts: range | None = None) -> np.ndarray:
+    """GGUF payload bytes of a stacked expert tensor, or of a contiguous range of
+    its experts (the bytes are identical to slicing the whole payload)."""
+    t = {"gate": spec.gate_type, "up": spec.up_type, "down": spec.down_type}[which]
+    per = spec.inter * spec.hidden
+    experts = experts if experts is not None else range(spec.n_experts)
+    sigma = spec.scale_sigma
+    return quant_matrix(t, seed, _STREAM[which], per * len(experts), sigma, per * experts.start)
+
+
+def router_f16(spec: W.LayerSpec, seed: int) -> np.ndarray:
+    """fp32 N(0, router_sigma) router, rounded to f16 as the loader does (loadLinear -> readF16)."""
+    r = (normal(seed, _STREAM["router"], spec.n_experts * spec.hidden) * spec.router_sigma).astype(np.float32)
+    return r.astype(np.float16).reshape(spec.n_experts, spec.hidden)
+
+
+def make_layer(spec: W.LayerSpec, seed: int = 0, layer: int = 0) -> dict:
+    s = layer_seed(seed, layer)
+    L = {
+        "gate": expert_tensor(spec, "gate", s),
+        "up": expert_tensor(spec, "up", s),
+        "down": expert_tensor(spec, "down", s),
+        "router": router_f16(spec, s),
+    }
+    if spec.shared_inter:
+        n = spec.shared_inter * spec.hidden
+        L["shared_gate"] = quant_matrix(spec.shared_type, s, _STREAM["sh_gate"], n, spec.scale_sigma)
+        L["shared_up"] = quant_matrix(spec.shared_type, s, _STREAM["sh_up"], n, spec.scale_sigma)
+        L["shared_down"] = quant_matrix(spec.shared_type, s, _STREAM["sh_down"], n, spec.scale_sigma)
+        if spec.shared_gated:
+            L["shared_gate_lin"] = (normal(s, _STREAM["sh_gate_lin"], spec.hidden) * 0.02).astype(np.float32).astype(np.float16)
+    return L
+
+
+def activations(spec: W.LayerSpec, n_tokens: int, seed: int = 0) -> np.ndarray:
+    """fp32 N(0,1) activations [T][H]; RMS-normalised with unit weight and eps 1e-5
+    (cpu.rmsnorm, cpu.zig:11-18) when the workload asks for it."""
+    x = normal(seed, _STREAM["x"], n_tokens * spec.hidden).astype(np.float32).reshape(n_tokens, spec.hidden)
+    if spec.rms_normalise_input:
+        ms = (x.astype(np.float64) ** 2).mean(axis=1, keepdims=True)
+        x = (x / np.sqrt(ms + 1e-5)).astype(np.float32)
+    return x
+
+
+def uniform_logits(spec: W.LayerSpec, n_tokens: int, seed: int = 0) -> np.ndarray:
+    """Router logits ~ U(0,1) i.i.d. (the decode workload's routing)."""
+    return uniform(seed, _STREAM["logits"], n_tokens * spec.n_experts).astype(np.float32).reshape(n_tokens, spec.n_experts)
+
+
+# Zipf-skewed prefill routing: logits = N(0,1) + alpha * log(p_e), p_e proportional to
+# rank^-1.1 over a seeded permutation of the experts.  alpha = 1.0 puts the busiest
+# expert at ~300 of 512 tokens with top-8 of 128 (measured by tests/test_workloads.py).
+ZIPF_S = 1.1
+ZIPF_ALPHA = 1.0
+
+
+def zipf_logits(spec: W.LayerSpec, n_tokens: int, seed: int = 0, alpha: float = ZIPF_ALPHA) -> np.ndarray:
+    E = spec.n_experts
+    perm = np.argsort(u64(seed, _STREAM["logits"] + 1, E))
+    rank = np.empty(E, dtype=np.float64)
+    rank[perm] = np.arange(1, E + 1)
+    p = rank ** -ZIPF_S
+    p /= p.sum()
+    bias = alpha * np.log(p)
+    z = normal(seed, _STREAM["logits"] + 2, n_tokens * E).reshape(n_tokens, E)
+    return (z + bias[None, :]).astype(np.float32)

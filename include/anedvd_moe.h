@@ -1,0 +1,182 @@
+/*
+ * anedvd_moe.h -- C ABI of the MI355X (gfx950) quantised mixture-of-experts FFN.
+ *
+ * Replaces, for ANEDVD's MoE block, the in-process Zig calls of src/cpu.zig and
+ * the expert reads of src/gguf.zig.  Conventions follow the reference's only
+ * foreign ABI, src/ane/shim.h:
+ *   - opaque handles;
+ *   - int status, 0 = ok, < 0 = error (shim.h:49-57);
+ *   - a thread-local, human-readable last error (shim.h:55-57);
+ *   - caller-owned buffers; nothing returned needs freeing except handles.
+ * Entry points taking `const float *h` etc. without a `_device` suffix take HOST
+ * pointers and are synchronous: results are in host memory on return.
+ *
+ * Threading: one caller thread per context (the engine is single-threaded,
+ * engine.zig:1-17); each context owns one HIP stream.
+ */
+#ifndef ANEDVD_MOE_H
+#define ANEDVD_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ANEDVD_MOE_ABI_VERSION 1
+
+/* ggml tensor type ids as stored in GGUF (gguf.zig:30-46). */
+enum anedvd_ggml_type {
+    ANEDVD_F32 = 0, ANEDVD_F16 = 1, ANEDVD_Q4_0 = 2, ANEDVD_Q4_1 = 3, ANEDVD_Q5_0 = 6,
+    ANEDVD_Q5_1 = 7, ANEDVD_Q8_0 = 8, ANEDVD_Q8_1 = 9, ANEDVD_Q2_K = 10, ANEDVD_Q3_K = 11,
+    ANEDVD_Q4_K = 12, ANEDVD_Q5_K = 13, ANEDVD_Q6_K = 14, ANEDVD_Q8_K = 15, ANEDVD_BF16 = 30
+};
+
+/* Status codes.  -1..-5 are the Zig errors of the replaced functions
+ * (gguf.zig:694-728, 533-552); the rest are this library's. */
+enum anedvd_status {
+    ANEDVD_OK = 0,
+    ANEDVD_E_UNSUPPORTED_TYPE = -1,  /* error.UnsupportedType */
+    ANEDVD_E_INVALID_SHAPE = -2,     /* error.InvalidTensorShape */
+    ANEDVD_E_TRUNCATED = -3,         /* error.TruncatedFile */
+    ANEDVD_E_DIMENSION = -4,         /* error.DimensionMismatch */
+    ANEDVD_E_OUT_OF_RANGE = -5,      /* error.TensorDataOutOfRange */
+    ANEDVD_E_INVALID_ARG = -6,
+    ANEDVD_E_HIP = -7,               /* a HIP runtime call failed; see last_error */
+    ANEDVD_E_NO_DEVICE = -8
+};
+
+typedef struct anedvd_moe_ctx anedvd_moe_ctx;
+typedef struct anedvd_moe_layer anedvd_moe_layer;
+
+/* One MoE layer, as ANEDVD's loaders hand it over (load_gguf.zig:767-826,
+ * model.zig:414-470).  Expert tensors are the GGUF payloads of
+ * blk.N.ffn_{gate,up,down}_exps.weight: E experts stacked on the slowest axis,
+ * each expert [out][in] row-major with quant blocks along `in`.  All pointers are
+ * host memory and may be freed once anedvd_moe_layer_create returns. */
+typedef struct {
+    uint32_t hidden;          /* H */
+    uint32_t inter;           /* I, one routed expert's width (Config.moe_inter) */
+    uint32_t n_experts;       /* E */
+    uint32_t k;               /* experts per token */
+    int32_t norm_topk_prob;   /* renormalise the top-k weights (Config.norm_topk_prob) */
+    int32_t use_gelu;         /* gelu(gate)*up instead of silu(gate)*up; must be 0 for now */
+    int32_t gate_type, up_type, down_type;
+    const void *gate; size_t gate_bytes;   /* [E][I][H] */
+    const void *up;   size_t up_bytes;     /* [E][I][H] */
+    const void *down; size_t down_bytes;   /* [E][H][I] */
+    const uint16_t *router;                /* [E][H] f16 bits (MoeWeights.router) */
+    uint32_t shared_inter;                 /* 0 = no shared expert */
+    int32_t shared_type;                   /* one type for the three shared tensors */
+    const void *shared_gate; size_t shared_gate_bytes;  /* [Is][H] */
+    const void *shared_up;   size_t shared_up_bytes;    /* [Is][H] */
+    const void *shared_down; size_t shared_down_bytes;  /* [H][Is] */
+    const uint16_t *shared_gate_lin;       /* [H] f16 bits, or NULL: shared scale 1.0 */
+} anedvd_moe_layer_desc;
+
+/* Filled by the forward calls when non-NULL. */
+typedef struct {
+    uint32_t n_tokens;
+    uint32_t touched_experts;      /* experts with >= 1 routed token in this call */
+    uint64_t weight_bytes;         /* expert + shared + router bytes the call had to read */
+    uint32_t max_group;            /* largest tokens-per-expert group */
+    uint32_t path;                 /* 0 = decode GEMV, 1 = prefill grouped GEMM */
+} anedvd_moe_stats;
+
+/* ------------------------------------------------------------------ lifetime */
+
+/* Human-readable description of the last failure on this thread (shim.h:55-57). */
+const char *anedvd_moe_last_error(void);
+int anedvd_moe_abi_version(void);
+
+/* Opens `device` and creates the context's stream (ane_shim_init, shim.h:49-53). */
+int anedvd_moe_open(int device, anedvd_moe_ctx **out);
+void anedvd_moe_close(anedvd_moe_ctx *ctx);
+
+/* Uploads one layer to HBM and repacks its quant blocks into the GPU tile layout,
+ * keeping every weight's bytes and dequantised value (loadMoeLayerStreaming,
+ * load_gguf.zig:767-826; MoeWeights, model.zig:414-470). */
+int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *desc,
+                            anedvd_moe_layer **out);
+void anedvd_moe_layer_free(anedvd_moe_layer *layer);
+/* Device bytes held by the layer's weights. */
+uint64_t anedvd_moe_layer_device_bytes(const anedvd_moe_layer *layer);
+
+/* ----------------------------------------------------- op-level mirrors of cpu.zig */
+
+/* gguf.dequantizeRange (gguf.zig:694-728): dequantise `n` elements of GGUF blocks
+ * starting at element `elem_offset`, bit-exact f32.  Same checks, same errors. */
+int anedvd_dequantize_range(anedvd_moe_ctx *ctx, int ggml_type, const void *src, size_t src_len,
+                            uint64_t elem_offset, float *out, size_t n);
+
+/* MoeWeights.loadExpertF32 / Gguf.readExpertF32 (model.zig:519-541, gguf.zig:533-552)
+ * from the resident layer: which 0 = gate, 1 = up, 2 = down; `out` holds
+ * rows*cols f32, bit-exact. */
+int anedvd_moe_load_expert_f32(anedvd_moe_layer *layer, int which, uint32_t expert, float *out, size_t n);
+
+/* cpu.matmulF16 (cpu.zig:461-475) over `n_vec` input vectors:
+ * out[v][o] = sum_i f32(w[o][i]) * x[v][i], in the reference's 8-lane order,
+ * bit-exact. */
+int anedvd_matmul_f16(anedvd_moe_ctx *ctx, float *out, const uint16_t *w, const float *x,
+                      size_t out_dim, size_t in_dim, size_t n_vec);
+
+/* cpu.moeRoute (cpu.zig:1236-1288) for `n_tokens` rows of logits:
+ * probs[t][k], idx[t][k].  Indices and probabilities are bit-exact. */
+int anedvd_moe_route(anedvd_moe_ctx *ctx, const float *logits, size_t n_tokens, size_t n_experts,
+                     size_t k, int norm_topk_prob, float *probs, uint32_t *idx);
+
+/* Token-to-expert dispatch (engine.zig:1204-1216, expertWeightFor engine.zig:825-830):
+ * offsets[E+1]; rows[T*k] = tokens grouped by expert, ascending within an expert;
+ * slots[T*k] = which of the token's k slots chose that expert. */
+int anedvd_moe_dispatch(anedvd_moe_ctx *ctx, const uint32_t *idx, size_t n_tokens, size_t k,
+                        size_t n_experts, int32_t *offsets, int32_t *rows, int32_t *slots);
+
+/* cpu.moeExpertAccumF32 (cpu.zig:416-452) for one token and one resident expert:
+ * out[H] += weight * down(silu(gate h) * up h). */
+int anedvd_moe_expert_accum(anedvd_moe_layer *layer, uint32_t expert, const float *h, float weight,
+                            float *out);
+
+/* ---------------------------------------------------------------- the layer */
+
+/* Router logits then moeRoute for T tokens (engine.zig:715-716, 1178-1179).
+ * `logits` may be NULL. */
+int anedvd_moe_layer_route(anedvd_moe_layer *layer, const float *h, size_t n_tokens,
+                           float *logits, float *probs, uint32_t *idx);
+
+/* The whole MoE block for T tokens (main.zig:488-520; engine.zig:705-779 decode,
+ * 1158-1268 prefill): out[t] = sum over slots of p * expert(h_t) + s * shared(h_t),
+ * s = sigmoid(shared_gate_lin . h_t) or 1.0.  `out` does not include the residual.
+ * If `logits` is non-NULL the router GEMV is skipped and those [T][E] logits are
+ * routed instead. */
+int anedvd_moe_layer_forward(anedvd_moe_layer *layer, const float *h, size_t n_tokens,
+                             const float *logits, float *out, anedvd_moe_stats *stats);
+
+/* Same with device pointers, stream-ordered on the context's stream, no host
+ * synchronisation (stats are not filled). */
+int anedvd_moe_layer_forward_device(anedvd_moe_layer *layer, const float *d_h, size_t n_tokens,
+                                    const float *d_logits, float *d_out);
+
+/* ------------------------------------------------- device memory and timing */
+
+int anedvd_moe_device_alloc(anedvd_moe_ctx *ctx, size_t bytes, void **d_ptr);
+int anedvd_moe_device_free(anedvd_moe_ctx *ctx, void *d_ptr);
+int anedvd_moe_memcpy_h2d(anedvd_moe_ctx *ctx, void *d_dst, const void *src, size_t bytes);
+int anedvd_moe_memcpy_d2h(anedvd_moe_ctx *ctx, void *dst, const void *d_src, size_t bytes);
+int anedvd_moe_synchronize(anedvd_moe_ctx *ctx);
+
+/* Runs `warmup` untimed then `iters` timed forward calls, call j using
+ * layers[j % n_layers], all inputs device-resident; the timed region is bracketed
+ * by HIP events on the context's stream.  *ms = total milliseconds of the timed
+ * region.  If `kernel_ms` is non-NULL, a second pass of `iters` calls records
+ * events around every stage and kernel_ms[0..5] receives the mean milliseconds per
+ * call of: route (router + route + dispatch), expert gate/up, expert down, shared
+ * expert, combine, and the whole call. */
+int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, const float *d_h,
+                            size_t n_tokens, const float *d_logits, float *d_out, int warmup,
+                            int iters, float *ms, float *kernel_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ANEDVD_MOE_H */

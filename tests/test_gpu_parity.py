@@ -1,0 +1,239 @@
+"""GPU parity: every entry point of the C ABI against the CPU oracle.
+
+Bit-exact: dequantised values (reference fixtures and resident experts), router
+logits, routing indices and probabilities, dispatch permutations.
+Tolerance: MoE layer outputs within rel-L2 <= 2e-3 of the oracle's f32
+composition (the bar the path is specified to), max-abs error printed.
+"""
+import dataclasses
+import os
+
+import numpy as np
+import pytest
+
+from anedvd_amd import moe, synth
+from anedvd_amd import workloads as W
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_TOL = 2e-3
+FIXTURES = ["f32", "f16", "bf16", "q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q8_1", "q2_k", "q3_k",
+            "q4_k", "q5_k", "q6_k", "q8_k"]
+TYPE = {n: t for t, n in W.TYPE_NAMES.items()}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = moe.MoeContext(0)
+    yield c
+    c.close()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_dequant_fixtures_bit_exact(ctx, golden_dir, name):
+    src = open(os.path.join(golden_dir, "dequant", name + ".bin"), "rb").read()
+    want = np.frombuffer(open(os.path.join(golden_dir, "dequant", name + ".f32"), "rb").read(), dtype=np.uint32)
+    got = ctx.dequantize(TYPE[name], src)
+    assert np.array_equal(bits(got), want)
+
+
+def test_dequant_range_errors_and_chunks(ctx, golden_dir):
+    src = open(os.path.join(golden_dir, "dequant", "q6_k.bin"), "rb").read()
+    want = np.frombuffer(open(os.path.join(golden_dir, "dequant", "q6_k.f32"), "rb").read(), dtype=np.uint32)
+    got = np.concatenate([ctx.dequantize_range(W.Q6_K, src, off, 256) for off in (0, 256)])
+    assert np.array_equal(bits(got), want)
+    for args, err in [((W.Q6_K, src, 64, 256), "InvalidTensorShape"), ((W.Q6_K, src[:300], 0, 512), "TruncatedFile"),
+                      ((99, src, 0, 256), "UnsupportedType")]:
+        with pytest.raises(moe.MoeError) as ei:
+            ctx.dequantize_range(*args)
+        assert ei.value.name == err
+
+
+@pytest.mark.parametrize("t", [W.Q8_0, W.Q4_0, W.Q4_K, W.Q6_K])
+def test_dequant_random_blocks_bit_exact(ctx, t):
+    src = synth.quant_matrix(t, 5, 9, 256 * 64, 0.3)
+    assert np.array_equal(bits(ctx.dequantize(t, src)), bits(O.dequantize(t, src)))
+
+
+@pytest.mark.parametrize("types", [(W.Q8_0, W.Q8_0, W.Q8_0), (W.Q4_K, W.Q4_K, W.Q6_K), (W.Q4_0, W.Q4_0, W.Q4_0)])
+def test_resident_experts_bit_exact(ctx, types):
+    """The tile repack keeps every dequantised weight: readExpertF32 of the
+    resident layer equals the oracle's on the GGUF payload, all three projections."""
+    spec = dataclasses.replace(W.TINY_Q8_0, hidden=512, inter=768, n_experts=4, gate_type=types[0], up_type=types[1],
+                               down_type=types[2])
+    L = synth.make_layer(spec, seed=3)
+    layer = moe.MoeLayer(ctx, spec, L)
+    n = spec.inter * spec.hidden
+    for which, (nm, t) in enumerate((("gate", types[0]), ("up", types[1]), ("down", types[2]))):
+        for e in (0, 3):
+            rc, want = O.read_expert_f32(t, L[nm], e, spec.n_experts, n)
+            assert rc == O.OK
+            assert np.array_equal(bits(layer.load_expert_f32(which, e)), bits(want)), (nm, e)
+    layer.free()
+
+
+# ------------------------------------------------------------------ routing
+
+@pytest.mark.parametrize("out_dim,in_dim,n", [(128, 2048, 1), (128, 2048, 64), (8, 512, 16), (64, 2048, 3),
+                                              (7, 300, 5), (8, 4096, 2)])
+def test_matmul_f16_bit_exact(ctx, out_dim, in_dim, n):
+    w = (synth.normal(1, out_dim, out_dim * in_dim) * 0.02).astype(np.float16).reshape(out_dim, in_dim)
+    x = synth.normal(2, in_dim, n * in_dim).astype(np.float32).reshape(n, in_dim)
+    got = ctx.matmul_f16(w, x)
+    want = np.stack([O.matmul_f16(w, x[i]) for i in range(n)])
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_moe_route_reference_kat(ctx):
+    vals = np.array([1.0, -2.0, -3.0, 5.0, -4.0, 0.5, -5.0, 3.0], dtype=np.float32)
+    p, idx = ctx.moe_route(vals, 4, False)
+    assert list(idx) == [3, 7, 0, 5]
+    op, _ = O.moe_route(vals, 4, False)
+    assert np.array_equal(bits(p), bits(op))
+    p, idx = ctx.moe_route(vals, 4, True)
+    assert abs(float(p.sum()) - 1.0) <= 1e-6
+    _, idx = ctx.moe_route(np.full(4, 2.0, np.float32), 4, False)
+    assert list(idx) == [0, 1, 2, 3]
+
+
+@pytest.mark.parametrize("E,k,norm,T", [(8, 2, True, 64), (128, 8, True, 512), (64, 6, False, 256),
+                                        (60, 4, False, 100), (256, 8, True, 64), (128, 1, False, 64)])
+def test_moe_route_bit_exact(ctx, E, k, norm, T):
+    lg = (synth.normal(7, E, T * E) * 2.0).astype(np.float32).reshape(T, E)
+    lg[::3] = np.round(lg[::3] * 4) / 4   # coarse logits: many exact ties
+    lg[1::7] = synth.uniform(8, E, lg[1::7].size).astype(np.float32).reshape(-1, E)
+    p, idx = ctx.moe_route(lg, k, norm)
+    for t in range(T):
+        op, oi = O.moe_route(lg[t], k, norm)
+        assert np.array_equal(idx[t], oi), t
+        assert np.array_equal(bits(p[t]), bits(op)), t
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (16, 8, 2), (64, 128, 8), (512, 128, 8), (2048, 8, 2), (1024, 64, 6)])
+def test_dispatch_bit_exact(ctx, T, E, k):
+    lg = synth.normal(11, T, T * E).astype(np.float32).reshape(T, E)
+    idx = np.stack([O.moe_route(lg[t], k, True)[1] for t in range(T)])
+    got = ctx.dispatch(idx, T, k, E)
+    want = O.dispatch(idx, T, k, E)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+
+
+def test_dispatch_rejects_bad_expert_ids(ctx):
+    with pytest.raises(moe.MoeError):
+        ctx.dispatch(np.array([[0, 9]], dtype=np.uint32), 1, 2, 8)
+
+
+@pytest.mark.parametrize("spec,T", [(W.TINY_Q8_0, 16), (W.QWEN3_30B_A3B_Q8_0, 64)])
+def test_layer_route_bit_exact(ctx, spec, T):
+    L = synth.make_layer(spec, seed=0)
+    h = synth.activations(spec, T, seed=0)
+    layer = moe.MoeLayer(ctx, spec, L)
+    logits, probs, idx = layer.route(h)
+    ol, op, oi = O.OracleLayer(spec, L).route(h, T)
+    assert np.array_equal(bits(logits), bits(ol))
+    assert np.array_equal(idx, oi)
+    assert np.array_equal(bits(probs), bits(op))
+    layer.free()
+
+
+# ------------------------------------------------------------------ experts
+
+def test_expert_accum_matches_oracle(ctx):
+    spec = W.TINY_Q8_0
+    L = synth.make_layer(spec, seed=2)
+    layer = moe.MoeLayer(ctx, spec, L)
+    h = synth.activations(spec, 1, seed=2)[0]
+    n = spec.inter * spec.hidden
+    g = O.read_expert_f32(W.Q8_0, L["gate"], 5, 8, n)[1]
+    u = O.read_expert_f32(W.Q8_0, L["up"], 5, 8, n)[1]
+    d = O.read_expert_f32(W.Q8_0, L["down"], 5, 8, n)[1]
+    want = O.moe_expert_accum_f32(np.zeros(spec.hidden, np.float32), h, g, u, d, spec.inter, spec.hidden, 0.75)
+    got = layer.expert_accum(np.zeros(spec.hidden, np.float32), 5, h, 0.75)
+    assert moe.rel_l2(got, want) <= REL_L2_TOL
+    # a second call accumulates (cpu.zig:1384-1387)
+    layer.expert_accum(got, 5, h, 1.5)
+    assert moe.rel_l2(got, 3 * want) <= REL_L2_TOL
+    layer.free()
+
+
+def _forward_case(ctx, spec, T, seed=0, logits=None, layer_arrays=None):
+    L = layer_arrays if layer_arrays is not None else synth.make_layer(spec, seed=seed)
+    h = synth.activations(spec, T, seed=seed)
+    layer = moe.MoeLayer(ctx, spec, L)
+    got, st = layer.forward(h, logits, stats=True)
+    want = O.OracleLayer(spec, L).forward(h, logits)
+    err = moe.rel_l2(got, want)
+    mabs = float(np.abs(got.astype(np.float64) - want).max())
+    print(f"\n{spec.name} T={T}: rel-L2 {err:.3e} max-abs {mabs:.3e} (|ref|max {np.abs(want).max():.3e}) "
+          f"touched {st['touched_experts']}")
+    layer.free()
+    return got, want, err, st
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_forward_tiny_q8_0(ctx, T):
+    _, _, err, _ = _forward_case(ctx, W.TINY_Q8_0, T)
+    assert err <= REL_L2_TOL
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 64])
+def test_forward_qwen3_30b_a3b_q8_0(ctx, T):
+    spec = W.QWEN3_30B_A3B_Q8_0
+    got, want, err, st = _forward_case(ctx, spec, T)
+    assert err <= REL_L2_TOL
+    _, oi = O.OracleLayer(spec, synth.make_layer(spec, 0)).route(synth.activations(spec, T, 0), T)[1:]
+    assert st["touched_experts"] == len(np.unique(oi))
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_forward_qwen3_uniform_logits(ctx, T):
+    """The decode workload routes i.i.d. U(0,1) logits instead of the router GEMV."""
+    spec = W.QWEN3_30B_A3B_Q8_0
+    lg = synth.uniform_logits(spec, T, seed=4)
+    _, _, err, _ = _forward_case(ctx, spec, T, seed=4, logits=lg)
+    assert err <= REL_L2_TOL
+
+
+def test_forward_shared_expert_deepseek_shape(ctx):
+    spec = W.DEEPSEEK_V2_LITE_Q8_0
+    _, _, err, _ = _forward_case(ctx, spec, 32)
+    assert err <= REL_L2_TOL
+
+
+def test_forward_gated_shared_expert(ctx):
+    spec = dataclasses.replace(W.TINY_Q8_0, shared_inter=1024, shared_gated=True)
+    _, _, err, _ = _forward_case(ctx, spec, 16, seed=6)
+    assert err <= REL_L2_TOL
+
+
+def test_forward_is_deterministic_and_order_equivariant(ctx):
+    """Size-independent properties at the full decode shape: two calls are bit
+    identical, and permuting the tokens permutes the outputs bit for bit (the
+    per-token combine is a fixed-order gather, not atomics)."""
+    spec = W.QWEN3_30B_A3B_Q8_0
+    L = synth.make_layer(spec, seed=1)
+    h = synth.activations(spec, 64, seed=1)
+    layer = moe.MoeLayer(ctx, spec, L)
+    a = layer.forward(h)
+    b = layer.forward(h)
+    assert np.array_equal(bits(a), bits(b))
+    perm = np.random.default_rng(0).permutation(64)
+    c = layer.forward(h[perm])
+    assert np.array_equal(bits(c), bits(a[perm]))
+    layer.free()
+
+
+def test_forward_zero_input_gives_zero(ctx):
+    spec = W.TINY_Q8_0
+    layer = moe.MoeLayer(ctx, spec, synth.make_layer(spec, seed=0))
+    out = layer.forward(np.zeros((3, spec.hidden), np.float32))
+    assert np.all(out == 0)
+    layer.free()
