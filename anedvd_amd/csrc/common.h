@@ -84,8 +84,9 @@ __host__ __device__ inline int block_bytes(int t)
 //   Q6_K   256    13 (208 B)    2 (f16 d)          210 (ql, qh, scales | d)
 //
 // Within a unit the chunks keep GGUF block byte order (Q8_0 chunk c is bytes
-// 16c..16c+15 of the two blocks' quants; Q4_K chunk 0 is d/dmin/scales and
-// chunks 1..8 are qs; Q6_K chunks 0..7 ql, 8..11 qh, 12 scales).
+// 16c..16c+15 of the two blocks' quants, each stored biased as q ^ 0x80 = q + 128;
+// Q4_K chunk 0 is d/dmin/scales and chunks 1..8 are qs; Q6_K chunks 0..7 ql,
+// 8..11 qh, 12 scales).
 struct Fmt {
     int unit;      // elements per unit
     int chunks;    // 16-byte quant chunks per lane per unit
@@ -125,12 +126,53 @@ __host__ __device__ inline size_t tile_s_off(const Fmt &f, int units, int rg, in
     return (((size_t)rg * units + u) * kRowGroup + lane) * (size_t)f.sbytes;
 }
 
+// GEMV activation order: within every 4 consecutive elements, (0, 2, 1, 3), so
+// that the f16 pairs (e0, e2) and (e1, e3) a lane builds from one dword of four
+// quants meet their activations as one aligned pair.
+__host__ __device__ inline int pair_perm(int e) { return (e & ~3) | ((e & 1) << 1) | ((e >> 1) & 1); }
+
 // IEEE binary16 bits -> f32, exact.
 __host__ __device__ inline float f16_bits_to_f32(uint16_t h)
 {
     half_t v;
     __builtin_memcpy(&v, &h, 2);
     return (float)v;
+}
+
+// ------------------------------------------------- GEMV activation format
+//
+// The decode kernels read activations as f16 scaled by a power of two per
+// (row, 64-element group), stored pair-permuted, with a float4 per group
+// {sum of the lower 32 f16 values, sum of the upper 32, the power of two that
+// undoes the scale, 0}.  Power-of-two scaling is exact; it keeps every group's
+// largest value in [2^14, 2^15), far from f16 overflow and subnormals.
+
+__device__ inline float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ inline float pow2_scale(float maxabs)
+{
+    if (!(maxabs > 0.0f) || !(maxabs < __builtin_inff())) return 1.0f;
+    int e;
+    frexpf(maxabs, &e);  // maxabs = m * 2^e, m in [0.5, 1)
+    return ldexpf(1.0f, max(-100, min(15 - e, 100)));
+}
+
+// One wavefront converts one 64-element group: lane i holds element i.
+__device__ inline void act_group(float v, int lane, half_t *__restrict__ q, float4 *__restrict__ side)
+{
+    const float sc = pow2_scale(wave_max(fabsf(v)));
+    const half_t hv = (half_t)(v * sc);
+    q[pair_perm(lane)] = hv;
+    float s = (float)hv;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    const float s_hi = __shfl(s, 32, 64);
+    if (lane == 0) *side = make_float4(s, s_hi, 1.0f / sc, 0.0f);
 }
 
 }  // namespace anedvd

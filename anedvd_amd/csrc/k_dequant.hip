@@ -259,9 +259,9 @@ __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
     uint8_t qb[208];
     int nq = 0;
     switch (m.type) {
-    case ANEDVD_Q8_0:  // two blocks: [d][32 qs] x 2
+    case ANEDVD_Q8_0:  // two blocks: [d][32 qs] x 2; quants stored biased (q + 128 = q ^ 0x80)
         for (int b = 0; b < 2; b++) {
-            for (int j = 0; j < 32; j++) qb[nq++] = unit[b * 34 + 2 + j];
+            for (int j = 0; j < 32; j++) qb[nq++] = unit[b * 34 + 2 + j] ^ 0x80;
             s[tile_s_off(f, m.units, rg, u, lane) + 2 * b] = unit[b * 34];
             s[tile_s_off(f, m.units, rg, u, lane) + 2 * b + 1] = unit[b * 34 + 1];
         }
@@ -308,7 +308,7 @@ __device__ int unit_gguf_bytes(const QMat &m, int mat, int r, int u, uint8_t *bl
         for (int b = 0; b < 2; b++) {
             blk[b * 34] = sc[2 * b];
             blk[b * 34 + 1] = sc[2 * b + 1];
-            for (int j = 0; j < 32; j++) blk[b * 34 + 2 + j] = qb[b * 32 + j];
+            for (int j = 0; j < 32; j++) blk[b * 34 + 2 + j] = qb[b * 32 + j] ^ 0x80;
         }
         return 2;
     case ANEDVD_Q4_0:

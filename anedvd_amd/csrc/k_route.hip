@@ -77,13 +77,6 @@ int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, fl
 
 // ------------------------------------------------------------------- route
 
-__device__ inline float wave_max(float v)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
 __device__ inline uint64_t wave_max_u64(uint64_t v)
 {
 #pragma unroll
@@ -94,51 +87,44 @@ __device__ inline uint64_t wave_max_u64(uint64_t v)
     return v;
 }
 
-constexpr int kRouteWaves = 4;
+__device__ inline float lane_value(float v, int lane)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 constexpr int kMaxExperts = 256;
 constexpr int kMaxK = 32;
 
-// One wavefront per token; lane j holds experts j, j+64, j+128, j+192.
+// One wavefront routes token t.  Lane j holds experts j, j+64, j+128, j+192.
+// The softmax denominator is summed in ascending expert order, one expert at a
+// time (the reference's sequential loop), by reading each lane's value in turn.
 // Selection key = (p bits << 32) | ~e: p >= 0, so its bits order like the value,
 // and among equal p the lowest expert has the largest key -- the reference's
-// strict `p > best_p` scan in ascending e.
-__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, int T, int E, int k, int norm,
-                                               float *__restrict__ probs, uint32_t *__restrict__ idx)
+// strict `p > best_p` scan in ascending e.  NaN probabilities are never chosen;
+// a slot with nothing left to choose gets (0, expert 0), as in the reference.
+__device__ void route_token(const float *__restrict__ lg, int E, int k, int norm, float *__restrict__ probs,
+                            uint32_t *__restrict__ idx, int lane)
 {
-    __shared__ float ex_s[kRouteWaves][kMaxExperts];
-    __shared__ float p_s[kRouteWaves][kMaxK];
-    __shared__ uint32_t i_s[kRouteWaves][kMaxK];
-    __shared__ float inv_s[kRouteWaves];
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = blockIdx.x * kRouteWaves + wv;
-    const bool live = t < T;  // every thread reaches every barrier
-    const float *lg = logits + (size_t)(live ? t : 0) * E;
-
     float v[4];
     float mx = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int e = lane + 64 * j;
-        v[j] = (live && e < E) ? lg[e] : -__builtin_inff();
+        v[j] = e < E ? lg[e] : -__builtin_inff();
         if (e < E) mx = fmaxf(mx, v[j]);
     }
     mx = wave_max(mx);
-
     float ex[4];
 #pragma unroll
+    for (int j = 0; j < 4; j++) ex[j] = expf_exact(v[j] - mx, c_exp2_tab);
+    float sum = 0.0f;
+#pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int e = lane + 64 * j;
-        ex[j] = expf_exact(v[j] - mx, c_exp2_tab);
-        if (e < E) ex_s[wv][e] = ex[j];
+        if (64 * j >= E) break;
+        const int n = min(64, E - 64 * j);
+        for (int l = 0; l < n; l++) sum = __fadd_rn(sum, lane_value(ex[j], l));
     }
-    __syncthreads();
-    if (lane == 0) {  // the reference's sum is sequential in e
-        float s = 0.0f;
-        for (int e = 0; e < E; e++) s = __fadd_rn(s, ex_s[wv][e]);
-        inv_s[wv] = s > 0.0f ? __fdiv_rn(1.0f, s) : 0.0f;
-    }
-    __syncthreads();
-    const float inv_sum = inv_s[wv];
+    const float inv_sum = sum > 0.0f ? __fdiv_rn(1.0f, sum) : 0.0f;
 
     uint64_t key[4];
 #pragma unroll
@@ -148,6 +134,8 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
         const bool ok = e < E && !(p != p);
         key[j] = ok ? ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e) : 0ull;
     }
+    float my_p = 0.0f;
+    uint32_t my_i = 0;
     for (int slot = 0; slot < k; slot++) {
         uint64_t best = key[0];
 #pragma unroll
@@ -162,139 +150,266 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
             for (int j = 0; j < 4; j++)
                 if (lane + 64 * j == (int)be) key[j] = 0ull;
         }
-        if (lane == 0) {
-            p_s[wv][slot] = bp;
-            i_s[wv][slot] = be;
+        if (lane == slot) {
+            my_p = bp;
+            my_i = be;
         }
     }
-    __syncthreads();
-    if (lane == 0 && norm) {
+    if (norm) {  // renormalise by the slot-order sum
         float s = 0.0f;
-        for (int j = 0; j < k; j++) s = __fadd_rn(s, p_s[wv][j]);
-        if (s > 0.0f)
-            for (int j = 0; j < k; j++) p_s[wv][j] = __fdiv_rn(p_s[wv][j], s);
+        for (int q = 0; q < k; q++) s = __fadd_rn(s, lane_value(my_p, q));
+        if (s > 0.0f) my_p = __fdiv_rn(my_p, s);
     }
-    __syncthreads();
-    if (live && lane < k) {
-        probs[(size_t)t * k + lane] = p_s[wv][lane];
-        idx[(size_t)t * k + lane] = i_s[wv][lane];
+    if (lane < k) {
+        probs[lane] = my_p;
+        idx[lane] = my_i;
     }
 }
 
-int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
-                 hipStream_t st)
+// ---------------------------------------------------------------- dispatch
+//
+// Stable counting sort of the T*k (token, slot) entries by expert, done by one
+// 256-thread workgroup:
+//   1. per-expert counts (LDS atomics; order-free), then an exclusive scan over
+//      experts gives offsets[E+1] and the ascending list of active experts;
+//   2. entries are ranked within their expert in chunks of C: each entry sets
+//      bit (entry - chunk start) of its expert's row of a bitmap, a block-wide
+//      scan of the popcounts of the flattened bitmap gives every word the count
+//      of earlier entries of the same expert, and an entry's rank is that count
+//      plus the popcount of the lower bits of its own word.
+// Outputs: offsets[E+1]; rows/slots[T*k] grouped by expert, tokens ascending;
+// inv[t*k+s] = position of (t, s) or -1 for an expert id >= E; active[0..n) =
+// experts with tokens, ascending; meta[0] = n, meta[1] = largest group,
+// meta[2] = entries with expert id >= E (never written out of bounds).
+constexpr int kDispWords = 4096;
+
+struct DispLds {
+    int32_t cnt[kMaxExperts];
+    int32_t off[kMaxExperts];
+    int32_t base[kMaxExperts];
+    uint32_t bits[kDispWords];
+    int32_t pre[kDispWords + 1];
+    int32_t wsum[4];
+    int32_t bad;
+};
+
+__device__ inline int wave_incl_scan(int v, int lane)
 {
-    if (T <= 0) return ANEDVD_OK;
-    if (E > kMaxExperts || k > kMaxK || k > E || k <= 0 || k > 64) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+
+__device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
+                               int32_t *__restrict__ rows, int32_t *__restrict__ slots, int32_t *__restrict__ inv,
+                               int32_t *__restrict__ active, int32_t *__restrict__ meta, DispLds &s)
+{
+    const int P = T * k, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int e = tid; e < E; e += 256) {
+        s.cnt[e] = 0;
+        s.base[e] = 0;
+    }
+    if (tid == 0) s.bad = 0;
+    __syncthreads();
+    int bad = 0;
+    for (int i = tid; i < P; i += 256) {
+        const uint32_t e = idx[i];
+        if (e < (uint32_t)E) atomicAdd(&s.cnt[e], 1);
+        else bad++;
+    }
+    if (bad) atomicAdd(&s.bad, bad);
+    __syncthreads();
+    if (wv == 0) {  // offsets and active experts: 4 experts per lane, E <= 256
+        int c[4], tot = 0, nz = 0, mx = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int e = lane * 4 + q;
+            c[q] = e < E ? s.cnt[e] : 0;
+            tot += c[q];
+            nz += c[q] > 0;
+            mx = max(mx, c[q]);
+        }
+        int run = wave_incl_scan(tot, lane) - tot;
+        int runa = wave_incl_scan(nz, lane) - nz;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int e = lane * 4 + q;
+            if (e < E) {
+                s.off[e] = run;
+                offsets[e] = run;
+                if (c[q]) active[runa++] = e;
+                run += c[q];
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
+        if (lane == 63) {
+            offsets[E] = run;
+            meta[0] = runa;
+        }
+        if (lane == 0) {
+            meta[1] = mx;
+            meta[2] = s.bad;
+        }
+    }
+    const int W = kDispWords / E;  // bitmap words per expert per chunk
+    const int C = 32 * W, NW = W * E;
+    const int per = (NW + 255) / 256;  // words scanned per thread
+    for (int c0 = 0; c0 < P; c0 += C) {
+        const int c1 = min(P, c0 + C);
+        for (int w = tid; w < NW; w += 256) s.bits[w] = 0;
+        __syncthreads();
+        for (int i = c0 + tid; i < c1; i += 256) {
+            const uint32_t e = idx[i];
+            if (e < (uint32_t)E) atomicOr(&s.bits[e * W + ((i - c0) >> 5)], 1u << ((i - c0) & 31));
+        }
+        __syncthreads();
+        // exclusive scan of popcounts over the flattened bitmap
+        int loc = 0;
+        for (int q = 0; q < per; q++) {
+            const int w = tid * per + q;
+            if (w < NW) loc += __popc(s.bits[w]);
+        }
+        const int incl = wave_incl_scan(loc, lane);
+        if (lane == 63) s.wsum[wv] = incl;
+        __syncthreads();
+        int run = incl - loc;
+        for (int q = 0; q < wv; q++) run += s.wsum[q];
+        for (int q = 0; q < per; q++) {
+            const int w = tid * per + q;
+            if (w < NW) {
+                s.pre[w] = run;
+                run += __popc(s.bits[w]);
+            }
+        }
+        if (tid == 255) s.pre[NW] = run;
+        __syncthreads();
+        for (int i = c0 + tid; i < c1; i += 256) {
+            const uint32_t e = idx[i];
+            if (e >= (uint32_t)E) {
+                inv[i] = -1;
+                continue;
+            }
+            const int r = i - c0, w = e * W + (r >> 5);
+            const int pos = s.off[e] + s.base[e] + (s.pre[w] - s.pre[e * W]) +
+                            __popc(s.bits[w] & ((1u << (r & 31)) - 1u));
+            rows[pos] = i / k;
+            slots[pos] = i % k;
+            inv[i] = pos;
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += 256) s.base[e] += s.pre[(e + 1) * W] - s.pre[e * W];
+        __syncthreads();
+    }
+}
+
+// --------------------------------------------------- activation conversion
+
+__device__ void act_prep_wave(const float *__restrict__ x, int rows, int K, half_t *__restrict__ q,
+                              float4 *__restrict__ side, size_t w, int lane)
+{
+    const int G = K / 64;
+    if (w >= (size_t)rows * G) return;
+    const size_t r = w / G;
+    const int g = (int)(w % G);
+    act_group(x[r * K + g * 64 + lane], lane, q + r * K + g * 64, side + r * G + g);
+}
+
+// ------------------------------------------------------- route launches
+
+struct RouteArgs {
+    const float *logits;
+    int T, E, k, norm;
+    float *probs;
+    uint32_t *idx;
+    const float *x;  // activations to convert in the same launch (null = none)
+    int H;
+    half_t *xq;
+    float4 *xside;
+    int n_route_blocks;
+};
+
+// Blocks [0, n_route_blocks) route 4 tokens each (one wavefront per token);
+// blocks after them convert the activations, 4 groups of 64 per block.
+__global__ __launch_bounds__(256) void k_route(RouteArgs a)
+{
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if ((int)blockIdx.x >= a.n_route_blocks) {
+        act_prep_wave(a.x, a.T, a.H, a.xq, a.xside, (size_t)(blockIdx.x - a.n_route_blocks) * 4 + wv, lane);
+        return;
+    }
+    const int t = blockIdx.x * 4 + wv;
+    if (t < a.T)
+        route_token(a.logits + (size_t)t * a.E, a.E, a.k, a.norm, a.probs + (size_t)t * a.k, a.idx + (size_t)t * a.k,
+                    lane);
+}
+
+__global__ __launch_bounds__(256) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
+                                                  int32_t *offsets, int32_t *rows, int32_t *slots, int32_t *inv,
+                                                  int32_t *active, int32_t *meta)
+{
+    __shared__ DispLds s;
+    dispatch_block(idx, T, k, E, offsets, rows, slots, inv, active, meta, s);
+}
+
+__global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ x, int rows, int K, half_t *__restrict__ q,
+                                                  float4 *__restrict__ side)
+{
+    act_prep_wave(x, rows, K, q, side, (size_t)blockIdx.x * 4 + (threadIdx.x >> 6), threadIdx.x & 63);
+}
+
+static int check_route_shape(int T, int E, int k)
+{
+    if (E > kMaxExperts || E <= 0 || k > kMaxK || k > E || k <= 0) {
         set_error("route: unsupported E=%d k=%d (E <= %d, 0 < k <= min(E, %d))", E, k, kMaxExperts, kMaxK);
         return ANEDVD_E_INVALID_ARG;
     }
-    hipLaunchKernelGGL(k_route, dim3((T + kRouteWaves - 1) / kRouteWaves), dim3(256), 0, st, d_logits, T, E, k,
-                       norm, d_probs, d_idx);
+    if ((long)T * k > (1l << 30)) {
+        set_error("route: %d tokens x top-%d is too many entries", T, k);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    return ANEDVD_OK;
+}
+
+int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
+                 const float *d_x, int H, const ActQ &xq, hipStream_t st)
+{
+    if (T <= 0) return ANEDVD_OK;
+    ANEDVD_TRY(check_route_shape(T, E, k));
+    if (d_x && H % 64) {
+        set_error("route: hidden %d is not a multiple of 64", H);
+        return ANEDVD_E_INVALID_SHAPE;
+    }
+    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq.q, xq.side, (T + 3) / 4};
+    const size_t groups = d_x ? (size_t)T * (H / 64) : 0;
+    const unsigned blocks = (unsigned)(a.n_route_blocks + (groups + 3) / 4);
+    hipLaunchKernelGGL(k_route, dim3(blocks), dim3(256), 0, st, a);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }
 
-// ---------------------------------------------------------------- dispatch
-
-// A single workgroup of NTH threads.  Thread i owns the contiguous token range
-// [i*P, (i+1)*P), P = ceil(T/NTH), and counts its (token, slot) entries per
-// expert in column i of lc[E][NTH].  A scan down each expert's column, then
-// across experts, gives every thread the first position it writes for each
-// expert; walking its tokens in order then places entries stably.
-//
-// Outputs: offsets[E+1]; rows/slots[T*k] in expert-major order; inv[t*k+s] =
-// the position of (t, s); active[0..n_active) = experts with tokens, ascending;
-// meta[0] = n_active, meta[1] = largest group, meta[2] = entries dropped because
-// idx >= E (they are never written out of bounds).
-template <int NTH>
-__global__ __launch_bounds__(NTH) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
-                                                  int32_t *__restrict__ offsets, int32_t *__restrict__ rows,
-                                                  int32_t *__restrict__ slots, int32_t *__restrict__ inv,
-                                                  int32_t *__restrict__ active, int32_t *__restrict__ meta)
+int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &d, hipStream_t st)
 {
-    extern __shared__ uint16_t lc[];  // [E][NTH]
-    __shared__ int32_t base_s[kMaxExperts + 1];
-    __shared__ int32_t bad_s;
-    const int tid = threadIdx.x;
-    const int P = (T + NTH - 1) / NTH;
-    const int t_begin = min(T, tid * P), t_end = min(T, t_begin + P);
-    for (int i = tid; i < E * NTH; i += NTH) lc[i] = 0;
-    if (tid == 0) bad_s = 0;
-    __syncthreads();
-    int bad = 0;
-    for (int t = t_begin; t < t_end; t++)
-        for (int s = 0; s < k; s++) {
-            const uint32_t e = idx[(size_t)t * k + s];
-            if (e < (uint32_t)E) lc[e * NTH + tid]++;
-            else bad++;
-        }
-    if (bad) atomicAdd(&bad_s, bad);
-    __syncthreads();
-    for (int e = tid; e < E; e += NTH) {  // exclusive scan down column e
-        int run = 0;
-        for (int i = 0; i < NTH; i++) {
-            const int c = lc[e * NTH + i];
-            lc[e * NTH + i] = (uint16_t)run;
-            run += c;
-        }
-        base_s[e] = run;  // the expert's count, for now
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int pos = 0, n_active = 0, biggest = 0;
-        for (int e = 0; e < E; e++) {
-            const int c = base_s[e];
-            offsets[e] = pos;
-            base_s[e] = pos;
-            if (c > 0) active[n_active++] = e;
-            biggest = c > biggest ? c : biggest;
-            pos += c;
-        }
-        offsets[E] = pos;
-        meta[0] = n_active;
-        meta[1] = biggest;
-        meta[2] = bad_s;
-    }
-    __syncthreads();
-    for (int t = t_begin; t < t_end; t++)
-        for (int s = 0; s < k; s++) {
-            const uint32_t e = idx[(size_t)t * k + s];
-            if (e >= (uint32_t)E) {
-                inv[(size_t)t * k + s] = -1;
-                continue;
-            }
-            const int pos = base_s[e] + lc[e * NTH + tid]++;
-            rows[pos] = t;
-            slots[pos] = s;
-            inv[(size_t)t * k + s] = pos;
-        }
+    if (T <= 0) return ANEDVD_OK;
+    ANEDVD_TRY(check_route_shape(T, E, k));
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), 0, st, d_idx, T, k, E, d.offsets, d.rows, d.slots, d.inv,
+                       d.active, d.meta);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
 }
 
-int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, int32_t *d_offsets, int32_t *d_rows, int32_t *d_slots,
-                    int32_t *d_inv, int32_t *d_active, int32_t *d_meta, hipStream_t st)
+int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st)
 {
-    if (E > kMaxExperts || E <= 0 || T <= 0 || k <= 0) {
-        set_error("dispatch: unsupported shape T=%d k=%d E=%d (E <= %d)", T, k, E, kMaxExperts);
-        return ANEDVD_E_INVALID_ARG;
+    if (rows <= 0) return ANEDVD_OK;
+    if (K % 64) {
+        set_error("activation conversion: %d columns is not a multiple of 64", K);
+        return ANEDVD_E_INVALID_SHAPE;
     }
-    // lc[E][nth] u16 kept within 32 KiB of LDS
-    const int nth = E <= 64 ? 256 : E <= 128 ? 128 : 64;
-    const int P = (T + nth - 1) / nth;
-    if ((long)P * k > 65535) {
-        set_error("dispatch: %d tokens x top-%d exceeds the per-thread counter range", T, k);
-        return ANEDVD_E_INVALID_ARG;
-    }
-    const size_t lds = (size_t)E * nth * sizeof(uint16_t);
-    if (nth == 256)
-        hipLaunchKernelGGL(k_dispatch<256>, dim3(1), dim3(256), lds, st, d_idx, T, k, E, d_offsets, d_rows, d_slots,
-                           d_inv, d_active, d_meta);
-    else if (nth == 128)
-        hipLaunchKernelGGL(k_dispatch<128>, dim3(1), dim3(128), lds, st, d_idx, T, k, E, d_offsets, d_rows, d_slots,
-                           d_inv, d_active, d_meta);
-    else
-        hipLaunchKernelGGL(k_dispatch<64>, dim3(1), dim3(64), lds, st, d_idx, T, k, E, d_offsets, d_rows, d_slots,
-                           d_inv, d_active, d_meta);
+    const size_t groups = (size_t)rows * (K / 64);
+    hipLaunchKernelGGL(k_act_prep, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st, d_x, rows, K, xq.q, xq.side);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }

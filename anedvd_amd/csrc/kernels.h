@@ -5,6 +5,23 @@
 
 namespace anedvd {
 
+// GEMV activation format: f16 values [rows][K], each 64-element group scaled by a
+// power of two and stored pair-permuted (pair_perm), and per group a float4
+// {sum of the lower 32 f16 values, sum of the upper 32, the power of two that
+// undoes the scale, 0} in side[rows][K/64].
+struct ActQ {
+    half_t *q;
+    float4 *side;
+};
+
+// Token-to-expert dispatch of T*k (token, slot) entries (engine.zig:1204-1216):
+// offsets[E+1]; rows/slots[T*k] grouped by expert, tokens ascending; inv[T*k] =
+// position of (t, s); active[] = experts with tokens, ascending; meta[0] = number
+// of active experts, meta[1] = largest group, meta[2] = ids >= E.
+struct Dispatch {
+    int32_t *offsets, *rows, *slots, *inv, *active, *meta;
+};
+
 // k_dequant.hip
 int launch_dequant_gguf(int type, const uint8_t *d_src, size_t n_blocks, float *d_out, hipStream_t st);
 int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st);
@@ -12,18 +29,31 @@ int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st);
 
 // k_route.hip
 int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits, hipStream_t st);
-int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx, hipStream_t st);
-int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, int32_t *d_offsets, int32_t *d_rows, int32_t *d_slots,
-                    int32_t *d_inv, int32_t *d_active, int32_t *d_meta, hipStream_t st);
+// cpu.moeRoute for T rows of logits; with d_x non-null the same launch also
+// converts x [T][H] to the GEMV activation format `xq`.
+int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
+                 const float *d_x, int H, const ActQ &xq, hipStream_t st);
+int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &d, hipStream_t st);
+int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st);
 
-// k_gemv.hip
-int gemv_unit_elems(int type);
-int launch_expert_gateup(const QMat &gate, const QMat &up, const float *x, const int32_t *offsets,
-                         const int32_t *rows, const int32_t *active, const int32_t *meta, float *part, int H, int I,
-                         int KS, int P, int max_u, hipStream_t st);
-int launch_expert_down(const QMat &down, const float *part, const int32_t *offsets, const int32_t *active,
-                       const int32_t *meta, float *ypart, int H, int I, int KS, int KSg, int P, int use_gelu,
-                       int max_u, hipStream_t st);
+// k_gemv.hip -- decode-regime expert GEMVs
+struct GemvPlan {
+    int nt;       // tokens per pass over the weights (1, 2, 4 or 8)
+    int ks_gu;    // K split of gate/up
+    int ks_dn;    // K split of down
+    int wk_dn;    // wavefronts splitting one down row group's K (1, 2 or 4)
+};
+bool gemv_supported(int type);
+// max_u: most experts a call can touch; max_group: most tokens one expert can get.
+GemvPlan plan_gemv(int gate_type, int down_type, int H, int I, int max_u, int max_group);
+// gate/up + SiLU(gate)*up for every dispatched (token, expert) position, written
+// to `act` [P][I] in the activation format.  With plan.ks_gu > 1 the K partials go
+// through `part` [ks][P][2][I] and a second launch adds them in ks order.
+int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
+                         int max_u, const GemvPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st);
+// down for every position: ypart [ks_dn][P][H] (the combine adds the K partials).
+int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int max_u,
+                       const GemvPlan &plan, float *ypart, hipStream_t st);
 int launch_combine(const float *ypart, const int32_t *inv, const float *probs, int T, int k, int H, int KS, int P,
                    const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st);
 

@@ -136,62 +136,58 @@ void free_qmat(QMat &m)
     m.s = nullptr;
 }
 
-// Splits the K axis over ks workgroups so that max_u * row_groups * ks reaches
-// about 1024 workgroups (4 per CU), keeping >= min_units units per workgroup.
-int choose_ks(int units, int row_groups, int max_u, int min_units)
-{
-    int best = 1;
-    for (int ks = 1; ks <= 16; ks++) {
-        if (units % ks || units / ks < min_units) continue;
-        best = ks;
-        if ((long)max_u * row_groups * ks >= 1024) break;
-    }
-    return best;
-}
-
-// All device scratch of one forward call of T tokens.
+// All device scratch of one forward call of T tokens with k slots each.
 struct Fwd {
-    float *logits, *probs, *part, *ypart, *sh_part, *sh_ypart, *sh_scale;
+    float *logits, *probs;
     uint32_t *idx;
-    int32_t *offsets, *rows, *slots, *inv, *active, *meta;
-    int32_t *sh_offsets, *sh_rows, *sh_active, *sh_meta;
+    Dispatch d;
+    ActQ xq;            // [T][H]
+    ActQ act;           // [P][I]
+    float *part, *ypart;
+    // shared expert
+    Dispatch sd;
+    ActQ sact;          // [T][Is]
+    float *sh_part, *sh_ypart, *sh_scale;
     float *h_in, *l_in, *out;  // staging for host-pointer calls
-    int KSg, KSd, sKSg, sKSd, max_u;
+    GemvPlan plan, splan;
+    int max_u, P;
 };
 
-size_t fwd_layout(const anedvd_moe_layer *L, int T, Fwd *f, uint8_t *base, bool with_io)
+size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base, bool with_io)
 {
-    const int H = L->H, I = L->I, E = L->E, k = L->k, P = T * k;
-    const int ug = gemv_unit_elems(L->gate.type), ud = gemv_unit_elems(L->down.type);
+    const int H = L->H, I = L->I, E = L->E, P = T * k;
     Fwd x{};
+    x.P = P;
     x.max_u = std::min(E, P);
-    x.KSg = ug ? choose_ks(H / ug, I / 64, x.max_u, 4) : 1;
-    x.KSd = ud ? choose_ks(I / ud, H / 64, x.max_u, 4) : 1;
-    if (L->Is) {
-        const int usg = gemv_unit_elems(L->sgate.type), usd = gemv_unit_elems(L->sdown.type);
-        x.sKSg = usg ? choose_ks(H / usg, L->Is / 64, 1, 4) : 1;
-        x.sKSd = usd ? choose_ks(L->Is / usd, H / 64, 1, 4) : 1;
-    }
+    x.plan = plan_gemv(L->gate.type, L->down.type, H, I, x.max_u, T);
     Carve c{base};
     x.logits = c.take<float>((size_t)T * E);
     x.probs = c.take<float>(P);
     x.idx = c.take<uint32_t>(P);
-    x.offsets = c.take<int32_t>(E + 1);
-    x.rows = c.take<int32_t>(P);
-    x.slots = c.take<int32_t>(P);
-    x.inv = c.take<int32_t>(P);
-    x.active = c.take<int32_t>(E);
-    x.meta = c.take<int32_t>(4);
-    x.part = c.take<float>((size_t)x.KSg * P * 2 * I);
-    x.ypart = c.take<float>((size_t)x.KSd * P * H);
+    x.d.offsets = c.take<int32_t>(E + 1);
+    x.d.rows = c.take<int32_t>(P);
+    x.d.slots = c.take<int32_t>(P);
+    x.d.inv = c.take<int32_t>(P);
+    x.d.active = c.take<int32_t>(E);
+    x.d.meta = c.take<int32_t>(4);
+    x.xq.q = c.take<half_t>((size_t)T * H);
+    x.xq.side = c.take<float4>((size_t)T * (H / 64));
+    x.act.q = c.take<half_t>((size_t)P * I);
+    x.act.side = c.take<float4>((size_t)P * (I / 64));
+    x.part = x.plan.ks_gu > 1 ? c.take<float>((size_t)x.plan.ks_gu * P * 2 * I) : nullptr;
+    x.ypart = c.take<float>((size_t)x.plan.ks_dn * P * H);
     if (L->Is) {
-        x.sh_part = c.take<float>((size_t)x.sKSg * T * 2 * L->Is);
-        x.sh_ypart = c.take<float>((size_t)x.sKSd * T * H);
+        const int Is = (int)L->Is;
+        x.splan = plan_gemv(L->sgate.type, L->sdown.type, H, Is, 1, T);
+        x.sd.offsets = c.take<int32_t>(2);
+        x.sd.rows = c.take<int32_t>(T);
+        x.sd.active = c.take<int32_t>(1);
+        x.sd.meta = c.take<int32_t>(4);
+        x.sact.q = c.take<half_t>((size_t)T * Is);
+        x.sact.side = c.take<float4>((size_t)T * (Is / 64));
+        x.sh_part = x.splan.ks_gu > 1 ? c.take<float>((size_t)x.splan.ks_gu * T * 2 * Is) : nullptr;
+        x.sh_ypart = c.take<float>((size_t)x.splan.ks_dn * T * H);
         x.sh_scale = c.take<float>(T);
-        x.sh_offsets = c.take<int32_t>(2);
-        x.sh_rows = c.take<int32_t>(T);
-        x.sh_active = c.take<int32_t>(1);
-        x.sh_meta = c.take<int32_t>(4);
     }
     if (with_io) {
         x.h_in = c.take<float>((size_t)T * H);
@@ -204,24 +200,24 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, Fwd *f, uint8_t *base, bool 
 
 // Fills the shared expert's one-expert dispatch (all T tokens, in order) and,
 // if it is gated, its per-token scale sigmoid(shared_gate_lin . h).
-__global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__restrict__ lin, int T, int H,
-                              int32_t *offsets, int32_t *rows, int32_t *active, int32_t *meta, float *scale)
+__global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__restrict__ lin, int T, int H, Dispatch d,
+                              float *scale)
 {
     const int t = blockIdx.x;
     if (t == 0 && threadIdx.x == 0) {
-        offsets[0] = 0;
-        offsets[1] = T;
-        active[0] = 0;
-        meta[0] = 1;
-        meta[1] = T;
-        meta[2] = 0;
+        d.offsets[0] = 0;
+        d.offsets[1] = T;
+        d.active[0] = 0;
+        d.meta[0] = 1;
+        d.meta[1] = T;
+        d.meta[2] = 0;
     }
-    if (threadIdx.x == 0) rows[t] = t;
+    if (threadIdx.x == 0) d.rows[t] = t;
     if (!lin) return;
     // one wavefront per token; sigmoid as cpu.sigmoid (cpu.zig:1223-1230)
     float g = 0.0f;
     for (int i = threadIdx.x; i < H; i += 64) g += f16_bits_to_f32(lin[i]) * h[(size_t)t * H + i];
-    for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o, 64);
+    for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o);
     if (threadIdx.x == 0) {
         float s;
         if (g >= 0) s = 1.0f / (1.0f + __expf(-fminf(g, 80.0f)));
@@ -246,27 +242,25 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
         ANEDVD_TRY(launch_router(L->router, d_h, T, E, H, f.logits, st));
         logits = f.logits;
     }
-    ANEDVD_TRY(launch_route(logits, T, E, k, L->norm, f.probs, f.idx, st));
-    ANEDVD_TRY(launch_dispatch(f.idx, T, k, E, f.offsets, f.rows, f.slots, f.inv, f.active, f.meta, st));
+    ANEDVD_TRY(launch_route(logits, T, E, k, L->norm, f.probs, f.idx, d_h, H, f.xq, st));
+    ANEDVD_TRY(launch_dispatch(f.idx, T, k, E, f.d, st));
     mark(1);
-    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, d_h, f.offsets, f.rows, f.active, f.meta, f.part, H, I, f.KSg, P,
-                                    f.max_u, st));
+    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.max_u, f.plan, f.part, f.act,
+                                    L->gelu, st));
     mark(2);
-    ANEDVD_TRY(launch_expert_down(L->down, f.part, f.offsets, f.active, f.meta, f.ypart, H, I, f.KSd, f.KSg, P, L->gelu,
-                                  f.max_u, st));
+    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.max_u, f.plan, f.ypart, st));
     mark(3);
     if (L->Is) {
-        hipLaunchKernelGGL(k_shared_prep, dim3(T), dim3(64), 0, st, d_h, L->sgate_lin, T, H, f.sh_offsets, f.sh_rows,
-                           f.sh_active, f.sh_meta, f.sh_scale);
+        const int Is = (int)L->Is;
+        hipLaunchKernelGGL(k_shared_prep, dim3(T), dim3(64), 0, st, d_h, L->sgate_lin, T, H, f.sd, f.sh_scale);
         ANEDVD_HIP(hipGetLastError());
-        ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, d_h, f.sh_offsets, f.sh_rows, f.sh_active, f.sh_meta,
-                                        f.sh_part, H, L->Is, f.sKSg, T, 1, st));
-        ANEDVD_TRY(launch_expert_down(L->sdown, f.sh_part, f.sh_offsets, f.sh_active, f.sh_meta, f.sh_ypart, H, L->Is,
-                                      f.sKSd, f.sKSg, T, L->gelu, 1, st));
+        ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, f.xq, H, Is, f.sd, T, 1, f.splan, f.sh_part,
+                                        f.sact, L->gelu, st));
+        ANEDVD_TRY(launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, 1, f.splan, f.sh_ypart, st));
     }
     mark(4);
-    ANEDVD_TRY(launch_combine(f.ypart, f.inv, f.probs, T, k, H, f.KSd, P, L->Is ? f.sh_ypart : nullptr,
-                              (L->Is && L->sgate_lin) ? f.sh_scale : nullptr, L->Is ? f.sKSd : 0, d_out, st));
+    ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, T, k, H, f.plan.ks_dn, P, L->Is ? f.sh_ypart : nullptr,
+                              (L->Is && L->sgate_lin) ? f.sh_scale : nullptr, L->Is ? f.splan.ks_dn : 0, d_out, st));
     mark(5);
     return ANEDVD_OK;
 }
@@ -521,7 +515,7 @@ int anedvd_moe_route(anedvd_moe_ctx *ctx, const float *logits, size_t T, size_t 
     float *dp = c.take<float>(T * k);
     uint32_t *di = c.take<uint32_t>(T * k);
     ANEDVD_HIP(hipMemcpyAsync(dl, logits, T * E * 4, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, norm, dp, di, ctx->stream));
+    ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, norm, dp, di, nullptr, 0, ActQ{}, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(probs, dp, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(idx, di, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
@@ -551,7 +545,8 @@ int anedvd_moe_dispatch(anedvd_moe_ctx *ctx, const uint32_t *idx, size_t T, size
     int32_t *dact = c.take<int32_t>(E);
     int32_t *dmeta = c.take<int32_t>(4);
     ANEDVD_HIP(hipMemcpyAsync(di, idx, P * 4, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_TRY(launch_dispatch(di, (int)T, (int)k, (int)E, doff, drows, dslots, dinv, dact, dmeta, ctx->stream));
+    const Dispatch dd{doff, drows, dslots, dinv, dact, dmeta};
+    ANEDVD_TRY(launch_dispatch(di, (int)T, (int)k, (int)E, dd, ctx->stream));
     int32_t meta[4];
     ANEDVD_HIP(hipMemcpyAsync(offsets, doff, (E + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(rows, drows, P * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -572,44 +567,40 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
         set_error("expert_accum: bad arguments (expert %u of %u)", expert, L->E);
         return ANEDVD_E_INVALID_ARG;
     }
-    anedvd_moe_ctx *ctx = L->ctx;
-    ANEDVD_HIP(hipSetDevice(ctx->device));
-    // One token routed to `expert` with probability `weight`: the same kernels as
-    // the forward, on a one-entry dispatch; out += the combined row.
-    const int H = (int)L->H, I = (int)L->I, E = (int)L->E;
-    const int ug = gemv_unit_elems(L->gate.type), ud = gemv_unit_elems(L->down.type);
-    if (!ug || !ud) {
-        set_error("expert_accum: no decode kernel for types %d/%d", L->gate.type, L->down.type);
+    if (!gemv_supported(L->gate.type) || !gemv_supported(L->down.type)) {
+        set_error("expert_accum: no expert kernel for types %d/%d", L->gate.type, L->down.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
-    const int KSg = choose_ks(H / ug, I / 64, 1, 4), KSd = choose_ks(I / ud, H / 64, 1, 4);
-    const size_t need = (size_t)H * 4 * 3 + (size_t)KSg * 2 * I * 4 + (size_t)KSd * H * 4 + (size_t)E * 8 + 8192;
-    ANEDVD_TRY(ensure(ctx->io, need, ctx->stream));
-    Carve c{(uint8_t *)ctx->io.base};
-    float *dh = c.take<float>(H);
-    float *dout = c.take<float>(H);
-    float *dpart = c.take<float>((size_t)KSg * 2 * I);
-    float *dy = c.take<float>((size_t)KSd * H);
-    int32_t *doff = c.take<int32_t>(E + 1);
-    int32_t *dmisc = c.take<int32_t>(8);  // rows[1], active[1], meta[4], inv[1]
-    float *dprob = c.take<float>(1);
+    anedvd_moe_ctx *ctx = L->ctx;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    // One token routed to `expert` with probability `weight`: the forward's
+    // kernels on a one-entry dispatch; then out += the combined row
+    // (`out[o] += weight * total`, cpu.zig:450).
+    const int H = (int)L->H, I = (int)L->I, E = (int)L->E;
+    Fwd f;
+    const size_t bytes = fwd_layout(L, 1, 1, nullptr, (uint8_t *)0, true);
+    ANEDVD_TRY(ensure(ctx->ws, bytes + 4096, ctx->stream));
+    fwd_layout(L, 1, 1, &f, (uint8_t *)ctx->ws.base, true);
     std::vector<int32_t> off(E + 1);
     for (int e = 0; e <= E; e++) off[e] = e > (int)expert ? 1 : 0;
-    const int32_t misc[8] = {0, (int32_t)expert, 1, 1, 0, 0, 0, 0};
-    ANEDVD_HIP(hipMemcpyAsync(dh, h, (size_t)H * 4, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_HIP(hipMemcpyAsync(doff, off.data(), (size_t)(E + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_HIP(hipMemcpyAsync(dmisc, misc, sizeof misc, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_HIP(hipMemcpyAsync(dprob, &weight, 4, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, dh, doff, dmisc, dmisc + 1, dmisc + 2, dpart, H, I, KSg, 1, 1,
-                                    ctx->stream));
-    ANEDVD_TRY(launch_expert_down(L->down, dpart, doff, dmisc + 1, dmisc + 2, dy, H, I, KSd, KSg, 1, L->gelu, 1,
-                                  ctx->stream));
-    ANEDVD_TRY(launch_combine(dy, dmisc /* inv[0] = 0 */, dprob, 1, 1, H, KSd, 1, nullptr, nullptr, 0, dout,
-                              ctx->stream));
+    const int32_t zero = 0, act = (int32_t)expert, meta[4] = {1, 1, 0, 0};
+    hipStream_t st = ctx->stream;
+    ANEDVD_HIP(hipMemcpyAsync(f.h_in, h, (size_t)H * 4, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.d.offsets, off.data(), (size_t)(E + 1) * 4, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.d.rows, &zero, 4, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.d.inv, &zero, 4, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.d.active, &act, 4, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.d.meta, meta, sizeof meta, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.probs, &weight, 4, hipMemcpyHostToDevice, st));
+    ANEDVD_TRY(launch_act_prep(f.h_in, 1, H, f.xq, st));
+    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, 1, 1, f.plan, f.part, f.act, L->gelu,
+                                    st));
+    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, 1, 1, f.plan, f.ypart, st));
+    ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, 1, 1, H, f.plan.ks_dn, 1, nullptr, nullptr, 0, f.out, st));
     std::vector<float> y(H);
-    ANEDVD_HIP(hipMemcpyAsync(y.data(), dout, (size_t)H * 4, hipMemcpyDeviceToHost, ctx->stream));
-    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
-    for (int o = 0; o < H; o++) out[o] += y[o];  // `out[o] += weight * total` (cpu.zig:450)
+    ANEDVD_HIP(hipMemcpyAsync(y.data(), f.out, (size_t)H * 4, hipMemcpyDeviceToHost, st));
+    ANEDVD_HIP(hipStreamSynchronize(st));
+    for (int o = 0; o < H; o++) out[o] += y[o];
     return ANEDVD_OK;
 }
 
@@ -634,7 +625,7 @@ int anedvd_moe_layer_route(anedvd_moe_layer *L, const float *h, size_t T, float 
     uint32_t *di = c.take<uint32_t>(T * k);
     ANEDVD_HIP(hipMemcpyAsync(dh, h, T * H * 4, hipMemcpyHostToDevice, ctx->stream));
     ANEDVD_TRY(launch_router(L->router, dh, (int)T, (int)E, (int)H, dl, ctx->stream));
-    ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, L->norm, dp, di, ctx->stream));
+    ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, L->norm, dp, di, nullptr, 0, ActQ{}, ctx->stream));
     if (logits) ANEDVD_HIP(hipMemcpyAsync(logits, dl, T * E * 4, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(probs, dp, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(idx, di, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -651,15 +642,15 @@ static int prepare(anedvd_moe_layer *L, size_t T, bool io, Fwd &f)
     }
     anedvd_moe_ctx *ctx = L->ctx;
     ANEDVD_HIP(hipSetDevice(ctx->device));
-    if (!gemv_unit_elems(L->gate.type) || !gemv_unit_elems(L->up.type) || !gemv_unit_elems(L->down.type) ||
-        L->gate.type != L->up.type || (L->Is && (!gemv_unit_elems(L->sgate.type)))) {
-        set_error("forward: no expert kernel for ggml types gate=%d up=%d down=%d yet", L->gate.type, L->up.type,
+    if (!gemv_supported(L->gate.type) || !gemv_supported(L->down.type) || L->gate.type != L->up.type ||
+        (L->Is && (!gemv_supported(L->sgate.type) || !gemv_supported(L->sdown.type)))) {
+        set_error("forward: no expert kernel for ggml types gate=%d up=%d down=%d", L->gate.type, L->up.type,
                   L->down.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
-    const size_t bytes = fwd_layout(L, (int)T, nullptr, (uint8_t *)0, io);
+    const size_t bytes = fwd_layout(L, (int)T, (int)L->k, nullptr, (uint8_t *)0, io);
     ANEDVD_TRY(ensure(ctx->ws, bytes + 4096, ctx->stream));
-    fwd_layout(L, (int)T, &f, (uint8_t *)ctx->ws.base, io);
+    fwd_layout(L, (int)T, (int)L->k, &f, (uint8_t *)ctx->ws.base, io);
     return ANEDVD_OK;
 }
 
@@ -679,7 +670,7 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *L, const float *h, size_t T, cons
     ANEDVD_TRY(forward_device(L, f.h_in, (int)T, logits ? f.l_in : nullptr, f.out, f, st, nullptr));
     int32_t meta[4] = {0, 0, 0, 0};
     ANEDVD_HIP(hipMemcpyAsync(out, f.out, T * L->H * 4, hipMemcpyDeviceToHost, st));
-    ANEDVD_HIP(hipMemcpyAsync(meta, f.meta, 16, hipMemcpyDeviceToHost, st));
+    ANEDVD_HIP(hipMemcpyAsync(meta, f.d.meta, 16, hipMemcpyDeviceToHost, st));
     ANEDVD_HIP(hipStreamSynchronize(st));
     if (stats) {
         stats->n_tokens = (uint32_t)T;

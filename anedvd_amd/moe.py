@@ -20,7 +20,9 @@ import numpy as np
 from . import workloads as W
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libanedvd_moe_hip.so")
+# ANEDVD_MOE_LIB selects another build of the library (e.g. one compiled with
+# different tuning options); the default is the in-tree build.
+LIB_PATH = os.environ.get("ANEDVD_MOE_LIB") or os.path.join(HERE, "libanedvd_moe_hip.so")
 
 STATUS = {0: "OK", -1: "UnsupportedType", -2: "InvalidTensorShape", -3: "TruncatedFile",
           -4: "DimensionMismatch", -5: "TensorDataOutOfRange", -6: "InvalidArgument", -7: "HipError",

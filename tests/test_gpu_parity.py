@@ -237,3 +237,59 @@ def test_forward_zero_input_gives_zero(ctx):
     out = layer.forward(np.zeros((3, spec.hidden), np.float32))
     assert np.all(out == 0)
     layer.free()
+
+
+# --------------------------------------------------- other block formats
+
+FORMATS = [(W.Q4_0, W.Q4_0, W.Q4_0), (W.Q4_K, W.Q4_K, W.Q6_K), (W.Q8_0, W.Q8_0, W.Q6_K), (W.Q4_K, W.Q4_K, W.Q4_K),
+           (W.Q6_K, W.Q6_K, W.Q8_0)]
+
+
+@pytest.mark.parametrize("types", FORMATS, ids=lambda t: "/".join(W.TYPE_NAMES[x] for x in t))
+@pytest.mark.parametrize("T", [1, 5, 64])
+def test_forward_block_formats(ctx, types, T):
+    """Fused dequant + SwiGLU for every supported GGUF block format, at group sizes
+    from 1 token (K split over workgroups) to more than one pass over the weights."""
+    spec = dataclasses.replace(W.QWEN3_30B_A3B_Q4_K_M, name="formats", hidden=1024, inter=512, n_experts=16, k=4,
+                               gate_type=types[0], up_type=types[1], down_type=types[2], scale_sigma=0.01)
+    _, _, err, _ = _forward_case(ctx, spec, T, seed=T)
+    assert err <= REL_L2_TOL
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_forward_mixtral_shape_q4_0(ctx, T):
+    """Mixtral-8x7B proportions (hidden 4096, top-2 of 8) with the expert width cut to
+    2048 so the oracle stays fast."""
+    spec = dataclasses.replace(W.MIXTRAL_8X7B_Q4_0, inter=2048)
+    _, _, err, _ = _forward_case(ctx, spec, T, seed=2)
+    assert err <= REL_L2_TOL
+
+
+def test_forward_qwen3_q4_k_m_prefill_zipf(ctx):
+    """A 300-token prefill of the Q4_K_M layer with Zipf-skewed routing (skewed
+    groups up to ~200 tokens); more than 256 tokens also takes the unfused
+    route/dispatch path.  (300 rather than 512 tokens keeps the oracle to seconds.)"""
+    spec = W.QWEN3_30B_A3B_Q4_K_M
+    lg = synth.zipf_logits(spec, 300, seed=0)
+    got, want, err, st = _forward_case(ctx, spec, 300, seed=0, logits=lg)
+    assert err <= REL_L2_TOL
+    assert st["max_group"] > 60
+
+
+def test_forward_many_passes_tiny(ctx):
+    """Groups of ~16 tokens per expert: two passes of 8 tokens over the weights."""
+    _, _, err, _ = _forward_case(ctx, W.TINY_Q8_0, 64, seed=9)
+    assert err <= REL_L2_TOL
+
+
+def test_forward_repeat_calls_keep_counters_clean(ctx):
+    """The K-split completion counters are left at zero: many B=1 calls in a row (the
+    path that splits K) stay identical to the first."""
+    spec = W.QWEN3_30B_A3B_Q8_0
+    L = synth.make_layer(spec, seed=5)
+    layer = moe.MoeLayer(ctx, spec, L)
+    h = synth.activations(spec, 1, seed=5)
+    first = layer.forward(h)
+    for _ in range(20):
+        assert np.array_equal(bits(layer.forward(h)), bits(first))
+    layer.free()
