@@ -67,69 +67,87 @@ __host__ __device__ inline int block_bytes(int t)
     }
 }
 
-// ------------------------------------------------------------ tile layout
+// -------------------------------------------------------- MMA tile layout
 //
-// A quantised matrix [rows][cols] (blocks along cols) is stored "row per lane":
-// rows are cut into row groups of 64, one row per wavefront lane, and the
-// column axis into units of UNIT elements (whole GGUF blocks).  For each
-// (row group, unit) the quant bytes of the 64 rows are interleaved in 16-byte
-// chunks, [chunk][lane][16 B], so one global_load_dwordx4 of a wavefront reads
-// 1 KiB contiguous; the per-lane scale bytes of the unit follow in a separate
-// plane, [lane][SB bytes].  Byte count per weight is unchanged:
+// A quantised matrix [rows][cols] (blocks along cols) is stored for the 16x16x32
+// f16 MFMA: rows in blocks of 64 (4 tiles of 16 rows), columns in steps of 64.
+// For (row block rb, step s, tile t) the 64 lanes of a wavefront hold, lane
+// l = 16 g + n, row 64 rb + 16 t + n and the 16 columns {64 s + 32 j + 8 g + i :
+// j = 0, 1; i = 0..7} in the order (j, i): the B operands of two MFMAs (j), so one
+// load per lane per tile feeds both.
+//   quant plane [rb][s][t][lane][QB bytes]
+//   h plane     [rb][s][t][lane] 4 bytes (Q6_K only): byte b, bits 4j + 2h and
+//               4j + 2h + 1, hold the high 2 bits of value (j, b + 4h)
+//   scale plane [rb][u][t][16 rows][SB bytes], u = the step's scale unit (one
+//               step for Q8_0 / Q4_0, a 256-column super-block for Q4_K / Q6_K)
+//   d plane     [rb][u][t][16 rows] f16 (Q6_K only)
 //
-//   type   UNIT  chunks/unit  scale bytes/unit   bytes per UNIT weights
-//   Q8_0    64     4 (64 B)     4 (2 x f16 d)      68  = 2 x 34
-//   Q4_0    64     2 (32 B)     4 (2 x f16 d)      36  = 2 x 18
-//   Q4_K   256     9 (144 B)    0                  144 (d, dmin, scales, qs)
-//   Q6_K   256    13 (208 B)    2 (f16 d)          210 (ql, qh, scales | d)
+//   type  QB  the lane's 16 values                                   SB
+//   Q8_0  16  byte 8j + i = q + 128                                   4  (d of blocks j = 0, 1)
+//   Q4_0   8  dword j, byte b: low nibble = (j, b), high = (j, b+4)   4  (d x 2)
+//   Q4_K   8  as Q4_0, the super-block's 4-bit quants                16  (d, dmin, 12 scale bytes)
+//   Q6_K   8  as Q4_0, the low 4 bits (high 2 in the h plane)        16  (int8 scales) + d plane
 //
-// Within a unit the chunks keep GGUF block byte order (Q8_0 chunk c is bytes
-// 16c..16c+15 of the two blocks' quants, each stored biased as q ^ 0x80 = q + 128;
-// Q4_K chunk 0 is d/dmin/scales and chunks 1..8 are qs; Q6_K chunks 0..7 ql,
-// 8..11 qh, 12 scales).
+// Bytes per weight are those of the GGUF blocks (Q8_0 1.0625, Q4_0 0.5625,
+// Q4_K 0.5625, Q6_K 0.8203); every dequantised value is kept (the repack only
+// moves bits).
 struct Fmt {
-    int unit;      // elements per unit
-    int chunks;    // 16-byte quant chunks per lane per unit
-    int sbytes;    // scale-plane bytes per lane per unit
+    int qb;     // quant bytes per lane per (step, tile)
+    int sb;     // scale bytes per row per scale unit
+    int spu;    // steps per scale unit
+    int blk;    // GGUF block elements
 };
 
 __host__ __device__ inline Fmt tile_fmt(int t)
 {
     switch (t) {
-    case ANEDVD_Q8_0: return Fmt{64, 4, 4};
-    case ANEDVD_Q4_0: return Fmt{64, 2, 4};
-    case ANEDVD_Q4_K: return Fmt{256, 9, 0};
-    case ANEDVD_Q6_K: return Fmt{256, 13, 2};
-    default: return Fmt{0, 0, 0};
+    case ANEDVD_Q8_0: return Fmt{16, 4, 1, 32};
+    case ANEDVD_Q4_0: return Fmt{8, 4, 1, 32};
+    case ANEDVD_Q4_K: return Fmt{8, 16, 4, 256};
+    case ANEDVD_Q6_K: return Fmt{8, 16, 4, 256};
+    default: return Fmt{0, 0, 0, 0};
     }
 }
 
-constexpr int kRowGroup = 64;
+constexpr int kRowBlock = 64;
+constexpr int kStep = 64;
 
 // One stacked matrix set (all experts of one projection) in tile layout.
 struct QMat {
     int type;
-    int rows, cols, n;        // n stacked matrices (experts)
-    uint8_t *q;               // quant plane, n * rows * cols * chunks*16/unit bytes
-    uint8_t *s;               // scale plane (may be null when sbytes == 0)
-    size_t q_stride, s_stride;  // bytes per matrix in each plane
-    int units;                // cols / unit
+    int rows, cols, n;            // n stacked matrices (experts)
+    int steps, units;             // cols / 64, steps / steps-per-unit
+    uint8_t *q, *s, *h, *d;       // quant, scale and (Q6_K) h and d planes
+    size_t q_stride, s_stride, h_stride, d_stride;  // bytes per matrix in each plane
 };
 
-__host__ __device__ inline size_t tile_q_off(const Fmt &f, int units, int rg, int u, int c, int lane)
+__host__ __device__ inline size_t tile_q_off(const Fmt &f, int steps, int rb, int s, int t, int lane)
 {
-    return ((((size_t)rg * units + u) * f.chunks + c) * kRowGroup + lane) * 16;
+    return ((((size_t)rb * steps + s) * 4 + t) * 64 + lane) * (size_t)f.qb;
 }
 
-__host__ __device__ inline size_t tile_s_off(const Fmt &f, int units, int rg, int u, int lane)
+__host__ __device__ inline size_t tile_s_off(const Fmt &f, int units, int rb, int u, int t, int n)
 {
-    return (((size_t)rg * units + u) * kRowGroup + lane) * (size_t)f.sbytes;
+    return ((((size_t)rb * units + u) * 4 + t) * 16 + n) * (size_t)f.sb;
 }
 
-// GEMV activation order: within every 4 consecutive elements, (0, 2, 1, 3), so
-// that the f16 pairs (e0, e2) and (e1, e3) a lane builds from one dword of four
-// quants meet their activations as one aligned pair.
-__host__ __device__ inline int pair_perm(int e) { return (e & ~3) | ((e & 1) << 1) | ((e >> 1) & 1); }
+__host__ __device__ inline size_t tile_h_off(int steps, int rb, int s, int t, int lane)
+{
+    return ((((size_t)rb * steps + s) * 4 + t) * 64 + lane) * 4;
+}
+
+__host__ __device__ inline size_t tile_d_off(int units, int rb, int u, int t, int n)
+{
+    return ((((size_t)rb * units + u) * 4 + t) * 16 + n) * 2;
+}
+
+// Column of lane group g's value (j, i) within a 64-column step.
+__host__ __device__ inline int mma_col(int g, int j, int i) { return 32 * j + 8 * g + i; }
+
+// MFMA activation format: element e of a 64-column group is stored at position
+// 16 g + 8 j + i (e = 32 j + 8 g + i), so lane group g reads its 16 A values as 32
+// contiguous bytes.
+__host__ __device__ inline int mma_pos(int e) { return 16 * ((e & 31) >> 3) + 8 * (e >> 5) + (e & 7); }
 
 // IEEE binary16 bits -> f32, exact.
 __host__ __device__ inline float f16_bits_to_f32(uint16_t h)
@@ -139,13 +157,13 @@ __host__ __device__ inline float f16_bits_to_f32(uint16_t h)
     return (float)v;
 }
 
-// ------------------------------------------------- GEMV activation format
+// ------------------------------------------------- MFMA activation format
 //
-// The decode kernels read activations as f16 scaled by a power of two per
-// (row, 64-element group), stored pair-permuted, with a float4 per group
-// {sum of the lower 32 f16 values, sum of the upper 32, the power of two that
-// undoes the scale, 0}.  Power-of-two scaling is exact; it keeps every group's
-// largest value in [2^14, 2^15), far from f16 overflow and subnormals.
+// The expert kernels read activations as f16 scaled by a power of two per (row,
+// 64-element group), stored in mma_pos order, with the power of two that undoes
+// the scale in a float array ds[group][row] (row-contiguous per group).  Power-of-
+// two scaling is exact; it keeps every group's largest value in [2^14, 2^15), far
+// from f16 overflow and subnormals.
 
 __device__ inline float wave_max(float v)
 {
@@ -162,17 +180,27 @@ __device__ inline float pow2_scale(float maxabs)
     return ldexpf(1.0f, max(-100, min(15 - e, 100)));
 }
 
-// One wavefront converts one 64-element group: lane i holds element i.
-__device__ inline void act_group(float v, int lane, half_t *__restrict__ q, float4 *__restrict__ side)
+template <int CTRL>
+__device__ inline float dpp_f32(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ inline float row_max_f32(float v)
+{
+    v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+    return v;
+}
+
+// One wavefront converts one 64-element group: lane e holds element e.
+__device__ inline void act_group(float v, int lane, half_t *__restrict__ q, float *__restrict__ ds)
 {
     const float sc = pow2_scale(wave_max(fabsf(v)));
-    const half_t hv = (half_t)(v * sc);
-    q[pair_perm(lane)] = hv;
-    float s = (float)hv;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    const float s_hi = __shfl(s, 32, 64);
-    if (lane == 0) *side = make_float4(s, s_hi, 1.0f / sc, 0.0f);
+    q[mma_pos(lane)] = (half_t)(v * sc);
+    if (lane == 0) *ds = 1.0f / sc;
 }
 
 }  // namespace anedvd

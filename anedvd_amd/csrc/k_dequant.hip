@@ -239,9 +239,102 @@ __global__ void k_dequant_gguf(int t, const uint8_t *__restrict__ src, size_t n_
 }
 
 // ------------------------------------------------------------------ repack
+//
+// The MMA tile layout (common.h) moves the bits of the GGUF blocks; gguf_quant()
+// and set_gguf_quant() read and write one element's raw quant in GGUF block
+// bytes, so the repack and its inverse share one statement of each format.
 
-// One thread per (matrix, row, unit): copies the unit's GGUF bytes into the tile
-// layout (common.h).  `src` is the stacked payload, matrices slowest.
+// Raw quant of element e of a GGUF block: Q8_0 the int8, Q4_0 / Q4_K the nibble,
+// Q6_K the 6-bit value (before the -32 offset).
+__device__ inline int gguf_quant(int t, const uint8_t *blk, int e)
+{
+    switch (t) {
+    case ANEDVD_Q8_0: return (int)(int8_t)blk[2 + e];
+    case ANEDVD_Q4_0: return e < 16 ? blk[2 + e] & 0xF : blk[2 + e - 16] >> 4;  // dequantQ4_0
+    case ANEDVD_Q4_K: {  // dequantQ4K: group e/64, low nibbles first, then high
+        const int g = e >> 6, l = e & 63;
+        const uint8_t q = blk[16 + 32 * g + (l & 31)];
+        return l < 32 ? q & 0xF : q >> 4;
+    }
+    case ANEDVD_Q6_K: {  // dequantQ6K: half e/128, quarter (e%128)/32
+        const int h = e >> 7, qd = (e & 127) >> 5, l = e & 31;
+        const uint8_t ql = blk[64 * h + l + (qd & 1) * 32], qh = blk[128 + 32 * h + l];
+        return ((qd & 2) ? ql >> 4 : ql & 0xF) | (((qh >> (2 * qd)) & 3) << 4);
+    }
+    default: return 0;
+    }
+}
+
+__device__ inline void set_gguf_quant(int t, uint8_t *blk, int e, int v)
+{
+    switch (t) {
+    case ANEDVD_Q8_0: blk[2 + e] = (uint8_t)v; break;
+    case ANEDVD_Q4_0:
+        if (e < 16) blk[2 + e] = (uint8_t)((blk[2 + e] & 0xF0) | v);
+        else blk[2 + e - 16] = (uint8_t)((blk[2 + e - 16] & 0x0F) | (v << 4));
+        break;
+    case ANEDVD_Q4_K: {
+        const int g = e >> 6, l = e & 63;
+        uint8_t &q = blk[16 + 32 * g + (l & 31)];
+        q = l < 32 ? (uint8_t)((q & 0xF0) | v) : (uint8_t)((q & 0x0F) | (v << 4));
+        break;
+    }
+    case ANEDVD_Q6_K: {
+        const int h = e >> 7, qd = (e & 127) >> 5, l = e & 31;
+        uint8_t &ql = blk[64 * h + l + (qd & 1) * 32], &qh = blk[128 + 32 * h + l];
+        ql = (qd & 2) ? (uint8_t)((ql & 0x0F) | ((v & 0xF) << 4)) : (uint8_t)((ql & 0xF0) | (v & 0xF));
+        qh = (uint8_t)((qh & ~(3 << (2 * qd))) | (((v >> 4) & 3) << (2 * qd)));
+        break;
+    }
+    default: break;
+    }
+}
+
+// Lane bytes of one (step, tile) from the lane's 16 raw quants v[8j + i].
+__device__ inline void pack_lane(int t, const int *v, uint8_t *out)
+{
+    switch (t) {
+    case ANEDVD_Q8_0:
+        for (int k = 0; k < 16; k++) out[k] = (uint8_t)((v[k] + 128) & 0xFF);
+        break;
+    case ANEDVD_Q4_0:
+    case ANEDVD_Q4_K:
+    case ANEDVD_Q6_K:
+        for (int j = 0; j < 2; j++)
+            for (int b = 0; b < 4; b++) out[4 * j + b] = (uint8_t)((v[8 * j + b] & 0xF) | ((v[8 * j + b + 4] & 0xF) << 4));
+        if (t == ANEDVD_Q6_K)
+            for (int b = 0; b < 4; b++) {
+                int h = 0;
+                for (int j = 0; j < 2; j++)
+                    for (int hh = 0; hh < 2; hh++) h |= ((v[8 * j + b + 4 * hh] >> 4) & 3) << (4 * j + 2 * hh);
+                out[8 + b] = (uint8_t)h;
+            }
+        break;
+    default: break;
+    }
+}
+
+__device__ inline int unpack_lane(int t, const uint8_t *in, int k)
+{
+    switch (t) {
+    case ANEDVD_Q8_0: return (int)in[k] - 128;
+    case ANEDVD_Q4_0:
+    case ANEDVD_Q4_K: {
+        const int j = k >> 3, i = k & 7;
+        return (in[4 * j + (i & 3)] >> (4 * (i >> 2))) & 0xF;
+    }
+    case ANEDVD_Q6_K: {
+        const int j = k >> 3, i = k & 7;
+        const int lo = (in[4 * j + (i & 3)] >> (4 * (i >> 2))) & 0xF;
+        const int hi = (in[8 + (i & 3)] >> (4 * j + 2 * (i >> 2))) & 3;
+        return lo | (hi << 4);
+    }
+    default: return 0;
+    }
+}
+
+// One thread per (matrix, row, scale unit): moves the unit's quants and scales
+// from the stacked GGUF payload `src` (matrices slowest) into the tile layout.
 __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
 {
     const Fmt f = tile_fmt(m.type);
@@ -250,98 +343,101 @@ __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
     if (id >= per_mat * m.n) return;
     const int mat = (int)(id / per_mat);
     const int r = (int)((id % per_mat) / m.units), u = (int)(id % m.units);
-    const int rg = r / kRowGroup, lane = r % kRowGroup;
+    const int rb = r / kRowBlock, t = (r % kRowBlock) / 16, n = r % 16;
     const int bpb = block_bytes(m.type), epb = block_elems(m.type);
-    const uint8_t *row = src + (size_t)mat * m.rows * ((size_t)m.cols / epb * bpb) + (size_t)r * ((size_t)m.cols / epb * bpb);
-    const uint8_t *unit = row + (size_t)u * (f.unit / epb) * bpb;
+    const size_t row_bytes = (size_t)m.cols / epb * bpb;
+    const uint8_t *row = src + ((size_t)mat * m.rows + r) * row_bytes;
     uint8_t *q = m.q + (size_t)mat * m.q_stride;
-    uint8_t *s = m.s ? m.s + (size_t)mat * m.s_stride : nullptr;
-    uint8_t qb[208];
-    int nq = 0;
-    switch (m.type) {
-    case ANEDVD_Q8_0:  // two blocks: [d][32 qs] x 2; quants stored biased (q + 128 = q ^ 0x80)
-        for (int b = 0; b < 2; b++) {
-            for (int j = 0; j < 32; j++) qb[nq++] = unit[b * 34 + 2 + j] ^ 0x80;
-            s[tile_s_off(f, m.units, rg, u, lane) + 2 * b] = unit[b * 34];
-            s[tile_s_off(f, m.units, rg, u, lane) + 2 * b + 1] = unit[b * 34 + 1];
+    for (int s = u * f.spu; s < (u + 1) * f.spu; s++)
+        for (int g = 0; g < 4; g++) {
+            int v[16];
+            for (int k = 0; k < 16; k++) {
+                const int c = kStep * s + mma_col(g, k >> 3, k & 7);
+                v[k] = gguf_quant(m.type, row + (size_t)(c / epb) * bpb, c % epb);
+            }
+            uint8_t lb[16];  // Q8_0: 16 quant bytes; Q6_K: 8 quant + 4 h bytes
+            pack_lane(m.type, v, lb);
+            uint8_t *dst = q + tile_q_off(f, m.steps, rb, s, t, 16 * g + n);
+            for (int k = 0; k < f.qb; k++) dst[k] = lb[k];
+            if (m.type == ANEDVD_Q6_K) {
+                uint8_t *hd = m.h + (size_t)mat * m.h_stride + tile_h_off(m.steps, rb, s, t, 16 * g + n);
+                for (int k = 0; k < 4; k++) hd[k] = lb[8 + k];
+            }
         }
-        break;
-    case ANEDVD_Q4_0:  // two blocks: [d][16 qs] x 2
-        for (int b = 0; b < 2; b++) {
-            for (int j = 0; j < 16; j++) qb[nq++] = unit[b * 18 + 2 + j];
-            s[tile_s_off(f, m.units, rg, u, lane) + 2 * b] = unit[b * 18];
-            s[tile_s_off(f, m.units, rg, u, lane) + 2 * b + 1] = unit[b * 18 + 1];
-        }
-        break;
-    case ANEDVD_Q4_K:  // the 144-byte block as is
-        for (int j = 0; j < 144; j++) qb[nq++] = unit[j];
-        break;
-    case ANEDVD_Q6_K:  // ql, qh, scales as is; d to the scale plane
-        for (int j = 0; j < 208; j++) qb[nq++] = unit[j];
-        s[tile_s_off(f, m.units, rg, u, lane)] = unit[208];
-        s[tile_s_off(f, m.units, rg, u, lane) + 1] = unit[209];
-        break;
-    default:
-        return;
-    }
-    for (int c = 0; c < f.chunks; c++) {
-        uint8_t *dst = q + tile_q_off(f, m.units, rg, u, c, lane);
-        for (int j = 0; j < 16; j++) dst[j] = qb[c * 16 + j];
-    }
-}
-
-// Rebuilds the GGUF bytes of one unit from the tile layout.
-__device__ int unit_gguf_bytes(const QMat &m, int mat, int r, int u, uint8_t *blk)
-{
-    const Fmt f = tile_fmt(m.type);
-    const int rg = r / kRowGroup, lane = r % kRowGroup;
-    const uint8_t *q = m.q + (size_t)mat * m.q_stride;
-    const uint8_t *s = m.s ? m.s + (size_t)mat * m.s_stride : nullptr;
-    uint8_t qb[208];
-    for (int c = 0; c < f.chunks; c++) {
-        const uint8_t *src = q + tile_q_off(f, m.units, rg, u, c, lane);
-        for (int j = 0; j < 16; j++) qb[c * 16 + j] = src[j];
-    }
-    const uint8_t *sc = s ? s + tile_s_off(f, m.units, rg, u, lane) : nullptr;
+    uint8_t *sc = m.s + (size_t)mat * m.s_stride + tile_s_off(f, m.units, rb, u, t, n);
+    const int c0 = u * f.spu * kStep;
+    const uint8_t *b0 = row + (size_t)(c0 / epb) * bpb;
     switch (m.type) {
     case ANEDVD_Q8_0:
-        for (int b = 0; b < 2; b++) {
-            blk[b * 34] = sc[2 * b];
-            blk[b * 34 + 1] = sc[2 * b + 1];
-            for (int j = 0; j < 32; j++) blk[b * 34 + 2 + j] = qb[b * 32 + j] ^ 0x80;
-        }
-        return 2;
-    case ANEDVD_Q4_0:
-        for (int b = 0; b < 2; b++) {
-            blk[b * 18] = sc[2 * b];
-            blk[b * 18 + 1] = sc[2 * b + 1];
-            for (int j = 0; j < 16; j++) blk[b * 18 + 2 + j] = qb[b * 16 + j];
-        }
-        return 2;
-    case ANEDVD_Q4_K:
-        for (int j = 0; j < 144; j++) blk[j] = qb[j];
-        return 1;
-    case ANEDVD_Q6_K:
-        for (int j = 0; j < 208; j++) blk[j] = qb[j];
-        blk[208] = sc[0];
-        blk[209] = sc[1];
-        return 1;
+    case ANEDVD_Q4_0:  // the f16 d of the step's two blocks
+        sc[0] = b0[0];
+        sc[1] = b0[1];
+        sc[2] = b0[bpb];
+        sc[3] = b0[bpb + 1];
+        break;
+    case ANEDVD_Q4_K:  // d, dmin, 12 scale bytes
+        for (int k = 0; k < 16; k++) sc[k] = b0[k];
+        break;
+    case ANEDVD_Q6_K: {  // 16 int8 scales; d to the d plane
+        for (int k = 0; k < 16; k++) sc[k] = b0[192 + k];
+        uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n);
+        dp[0] = b0[208];
+        dp[1] = b0[209];
+        break;
     }
-    return 0;
+    default: break;
+    }
 }
 
-// One thread per (row, unit) of matrix `mat`: out[rows][cols] f32, bit-exact.
+// One thread per GGUF block of matrix `mat`: rebuilds the block's bytes from the
+// tile layout and dequantises them (out[rows][cols] f32, bit-exact).
 __global__ void k_dequant_tiles(QMat m, int mat, float *__restrict__ out)
 {
-    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (id >= (size_t)m.rows * m.units) return;
-    const int r = (int)(id / m.units), u = (int)(id % m.units);
     const Fmt f = tile_fmt(m.type);
-    uint8_t blk[210 * 2];
-    const int nb = unit_gguf_bytes(m, mat, r, u, blk);
     const int bpb = block_bytes(m.type), epb = block_elems(m.type);
-    float *y = out + (size_t)r * m.cols + (size_t)u * f.unit;
-    for (int b = 0; b < nb; b++) deq_block(m.type, blk + b * bpb, y + b * epb);
+    const int bpr = m.cols / epb;
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (size_t)m.rows * bpr) return;
+    const int r = (int)(id / bpr), b = (int)(id % bpr);
+    const int rb = r / kRowBlock, t = (r % kRowBlock) / 16, n = r % 16;
+    const uint8_t *q = m.q + (size_t)mat * m.q_stride;
+    uint8_t blk[292];
+    for (int k = 0; k < bpb; k++) blk[k] = 0;
+    for (int e = 0; e < epb; e++) {
+        const int c = b * epb + e, s = c / kStep, w = c % kStep;
+        const int j = w >> 5, g = (w & 31) >> 3, i = w & 7;
+        uint8_t lb[16];  // Q8_0: 16 quant bytes; Q6_K: 8 quant + 4 h bytes
+        const uint8_t *src = q + tile_q_off(f, m.steps, rb, s, t, 16 * g + n);
+        for (int k = 0; k < f.qb; k++) lb[k] = src[k];
+        if (m.type == ANEDVD_Q6_K) {
+            const uint8_t *hs = m.h + (size_t)mat * m.h_stride + tile_h_off(m.steps, rb, s, t, 16 * g + n);
+            for (int k = 0; k < 4; k++) lb[8 + k] = hs[k];
+        }
+        set_gguf_quant(m.type, blk, e, unpack_lane(m.type, lb, 8 * j + i));
+    }
+    const int u = (b * epb) / (f.spu * kStep);
+    const uint8_t *sc = m.s + (size_t)mat * m.s_stride + tile_s_off(f, m.units, rb, u, t, n);
+    switch (m.type) {
+    case ANEDVD_Q8_0:
+    case ANEDVD_Q4_0: {
+        const int j = (b * epb / 32) & 1;  // which of the step's two blocks
+        blk[0] = sc[2 * j];
+        blk[1] = sc[2 * j + 1];
+        break;
+    }
+    case ANEDVD_Q4_K:
+        for (int k = 0; k < 16; k++) blk[k] = sc[k];
+        break;
+    case ANEDVD_Q6_K: {
+        for (int k = 0; k < 16; k++) blk[192 + k] = sc[k];
+        const uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n);
+        blk[208] = dp[0];
+        blk[209] = dp[1];
+        break;
+    }
+    default: break;
+    }
+    deq_block(m.type, blk, out + (size_t)r * m.cols + (size_t)b * epb);
 }
 
 // ------------------------------------------------------------------ launchers
@@ -365,7 +461,7 @@ int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st)
 
 int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st)
 {
-    const size_t n = (size_t)m.rows * m.units;
+    const size_t n = (size_t)m.rows * (m.cols / block_elems(m.type));
     hipLaunchKernelGGL(k_dequant_tiles, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, mat, d_out);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;

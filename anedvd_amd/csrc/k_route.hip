@@ -77,14 +77,31 @@ int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, fl
 
 // ------------------------------------------------------------------- route
 
+// One step of a wavefront max over u64 keys: v = max(v, v of the lane the DPP
+// control names); lanes without a source keep their own value.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline uint64_t dpp_max_u64(uint64_t v)
+{
+    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, ROW_MASK, 0xF, false);
+    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, ROW_MASK, 0xF, false);
+    const uint64_t o = ((uint64_t)ohi << 32) | olo;
+    return o > v ? o : v;
+}
+
+// Max of v over the 64 lanes, returned wave-uniform: DPP swaps within quads, row
+// mirrors, then row broadcasts 15 and 31 carry the row maxima up to lane 63.
 __device__ inline uint64_t wave_max_u64(uint64_t v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
+    v = dpp_max_u64<0xB1>(v);        // quad_perm [1,0,3,2]
+    v = dpp_max_u64<0x4E>(v);        // quad_perm [2,3,0,1]
+    v = dpp_max_u64<0x141>(v);       // row_half_mirror
+    v = dpp_max_u64<0x140>(v);       // row_mirror
+    v = dpp_max_u64<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+    v = dpp_max_u64<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
 }
 
 __device__ inline float lane_value(float v, int lane)
@@ -95,81 +112,130 @@ __device__ inline float lane_value(float v, int lane)
 constexpr int kMaxExperts = 256;
 constexpr int kMaxK = 32;
 
-// One wavefront routes token t.  Lane j holds experts j, j+64, j+128, j+192.
-// The softmax denominator is summed in ascending expert order, one expert at a
-// time (the reference's sequential loop), by reading each lane's value in turn.
-// Selection key = (p bits << 32) | ~e: p >= 0, so its bits order like the value,
-// and among equal p the lowest expert has the largest key -- the reference's
-// strict `p > best_p` scan in ascending e.  NaN probabilities are never chosen;
-// a slot with nothing left to choose gets (0, expert 0), as in the reference.
-__device__ void route_token(const float *__restrict__ lg, int E, int k, int norm, float *__restrict__ probs,
-                            uint32_t *__restrict__ idx, int lane)
+// ----------------------------------------------------- 16-lane row routing
+//
+// A DPP row (16 lanes) routes one token, so a wavefront routes 4 at once.  Lane
+// li of the row holds experts [li*VPL, (li+1)*VPL).  Row-wide max and argmax use
+// DPP swaps within the row (every lane ends with the result); the softmax
+// denominator is the reference's sequential sum in ascending expert order, carried
+// lane to lane with row_shr:1, each lane adding its experts one at a time.
+
+__device__ inline uint64_t row_max_u64(uint64_t v)
 {
-    float v[4];
-    float mx = -__builtin_inff();
+    v = dpp_max_u64<0xB1>(v);
+    v = dpp_max_u64<0x4E>(v);
+    v = dpp_max_u64<0x141>(v);
+    v = dpp_max_u64<0x140>(v);
+    return v;
+}
+
+// cpu.moeRoute (cpu.zig:1236-1288) for one token per row.  Selection key =
+// (p bits << 32) | ~e: p >= 0, so its bits order like the value, and among equal p
+// the lowest expert has the largest key -- the reference's strict `p > best_p`
+// scan in ascending e.  NaN probabilities are never chosen; a slot with nothing
+// left to choose gets (0, expert 0), as in the reference.  All lanes of the wave
+// run this (rows with live == false compute on -inf and store nothing).
+template <int VPL>
+__device__ void route_row(const float *__restrict__ lg, bool live, int E, int k, int norm, float *__restrict__ probs,
+                          uint32_t *__restrict__ idx, uint32_t *idx_copy, int li)
+{
+    const int e0 = li * VPL;
+    float v[VPL];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int e = lane + 64 * j;
-        v[j] = e < E ? lg[e] : -__builtin_inff();
-        if (e < E) mx = fmaxf(mx, v[j]);
+    for (int j = 0; j < VPL; j++) v[j] = (live && e0 + j < E) ? lg[e0 + j] : -__builtin_inff();
+    float mx = v[0];
+#pragma unroll
+    for (int j = 1; j < VPL; j++) mx = fmaxf(mx, v[j]);
+    mx = row_max_f32(mx);
+    float ex[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; j++) ex[j] = expf_exact(v[j] - mx, c_exp2_tab);
+    // sequential sum: before step L, lane L holds the sum of experts < L*VPL
+    float run = 0.0f, t = 0.0f;
+#pragma unroll
+    for (int L = 0; L < 16; L++) {
+        t = run;
+#pragma unroll
+        for (int j = 0; j < VPL; j++)
+            if (L * VPL + j < E) t = __fadd_rn(t, ex[j]);
+        if (L < 15) run = dpp_f32<0x111>(t);  // row_shr:1
     }
-    mx = wave_max(mx);
-    float ex[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) ex[j] = expf_exact(v[j] - mx, c_exp2_tab);
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        if (64 * j >= E) break;
-        const int n = min(64, E - 64 * j);
-        for (int l = 0; l < n; l++) sum = __fadd_rn(sum, lane_value(ex[j], l));
-    }
+    const float sum = __shfl(t, (threadIdx.x & 63 & ~15) + 15, 64);  // lane 15 of the row
     const float inv_sum = sum > 0.0f ? __fdiv_rn(1.0f, sum) : 0.0f;
 
-    uint64_t key[4];
+    uint64_t key[VPL];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int e = lane + 64 * j;
+    for (int j = 0; j < VPL; j++) {
         const float p = __fmul_rn(ex[j], inv_sum);
-        const bool ok = e < E && !(p != p);
-        key[j] = ok ? ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e) : 0ull;
+        const bool ok = live && e0 + j < E && !(p != p);
+        key[j] = ok ? ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)(e0 + j)) : 0ull;
     }
-    float my_p = 0.0f;
-    uint32_t my_i = 0;
+    float my_p0 = 0.0f, my_p1 = 0.0f, rsum = 0.0f;
+    uint32_t my_i0 = 0, my_i1 = 0;
     for (int slot = 0; slot < k; slot++) {
         uint64_t best = key[0];
 #pragma unroll
-        for (int j = 1; j < 4; j++) best = key[j] > best ? key[j] : best;
-        best = wave_max_u64(best);
+        for (int j = 1; j < VPL; j++) best = key[j] > best ? key[j] : best;
+        best = row_max_u64(best);
         float bp = 0.0f;
         uint32_t be = 0;
         if (best != 0ull) {
             be = 0xFFFFFFFFu - (uint32_t)best;
             bp = __uint_as_float((uint32_t)(best >> 32));
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (lane + 64 * j == (int)be) key[j] = 0ull;
+            for (int j = 0; j < VPL; j++)
+                if (key[j] == best) key[j] = 0ull;
         }
-        if (lane == slot) {
-            my_p = bp;
-            my_i = be;
+        rsum = __fadd_rn(rsum, bp);  // the renormalisation sum, in slot order
+        if (li == (slot & 15)) {
+            if (slot < 16) {
+                my_p0 = bp;
+                my_i0 = be;
+            } else {
+                my_p1 = bp;
+                my_i1 = be;
+            }
         }
     }
-    if (norm) {  // renormalise by the slot-order sum
-        float s = 0.0f;
-        for (int q = 0; q < k; q++) s = __fadd_rn(s, lane_value(my_p, q));
-        if (s > 0.0f) my_p = __fdiv_rn(my_p, s);
+    if (norm && rsum > 0.0f) {
+        my_p0 = __fdiv_rn(my_p0, rsum);
+        my_p1 = __fdiv_rn(my_p1, rsum);
     }
-    if (lane < k) {
-        probs[lane] = my_p;
-        idx[lane] = my_i;
+    if (!live) return;
+    if (li < k) {
+        probs[li] = my_p0;
+        idx[li] = my_i0;
+        if (idx_copy) idx_copy[li] = my_i0;
     }
+    if (li + 16 < k) {
+        probs[li + 16] = my_p1;
+        idx[li + 16] = my_i1;
+        if (idx_copy) idx_copy[li + 16] = my_i1;
+    }
+}
+
+// Routes token t (if t < T) on this thread's row.
+__device__ inline void route_token_row(const float *__restrict__ logits, int t, int T, int E, int k, int norm,
+                                       float *__restrict__ probs, uint32_t *__restrict__ idx, uint32_t *idx_copy)
+{
+    const bool live = t < T;
+    const int tt = live ? t : 0;
+    const float *lg = logits + (size_t)tt * E;
+    float *pr = probs + (size_t)tt * k;
+    uint32_t *ix = idx + (size_t)tt * k;
+    uint32_t *ic = idx_copy ? idx_copy + (size_t)tt * k : nullptr;
+    const int li = threadIdx.x & 15;
+    if (E <= 16) route_row<1>(lg, live, E, k, norm, pr, ix, ic, li);
+    else if (E <= 32) route_row<2>(lg, live, E, k, norm, pr, ix, ic, li);
+    else if (E <= 64) route_row<4>(lg, live, E, k, norm, pr, ix, ic, li);
+    else if (E <= 128) route_row<8>(lg, live, E, k, norm, pr, ix, ic, li);
+    else route_row<16>(lg, live, E, k, norm, pr, ix, ic, li);
 }
 
 // ---------------------------------------------------------------- dispatch
 //
 // Stable counting sort of the T*k (token, slot) entries by expert, done by one
-// 256-thread workgroup:
+// workgroup of NTH threads:
 //   1. per-expert counts (LDS atomics; order-free), then an exclusive scan over
 //      experts gives offsets[E+1] and the ascending list of active experts;
 //   2. entries are ranked within their expert in chunks of C: each entry sets
@@ -189,7 +255,7 @@ struct DispLds {
     int32_t base[kMaxExperts];
     uint32_t bits[kDispWords];
     int32_t pre[kDispWords + 1];
-    int32_t wsum[4];
+    int32_t wsum[16];
     int32_t bad;
 };
 
@@ -203,19 +269,20 @@ __device__ inline int wave_incl_scan(int v, int lane)
     return v;
 }
 
+template <int NTH>
 __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
                                int32_t *__restrict__ rows, int32_t *__restrict__ slots, int32_t *__restrict__ inv,
                                int32_t *__restrict__ active, int32_t *__restrict__ meta, DispLds &s)
 {
     const int P = T * k, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int e = tid; e < E; e += 256) {
+    for (int e = tid; e < E; e += NTH) {
         s.cnt[e] = 0;
         s.base[e] = 0;
     }
     if (tid == 0) s.bad = 0;
     __syncthreads();
     int bad = 0;
-    for (int i = tid; i < P; i += 256) {
+    for (int i = tid; i < P; i += NTH) {
         const uint32_t e = idx[i];
         if (e < (uint32_t)E) atomicAdd(&s.cnt[e], 1);
         else bad++;
@@ -257,12 +324,12 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
     }
     const int W = kDispWords / E;  // bitmap words per expert per chunk
     const int C = 32 * W, NW = W * E;
-    const int per = (NW + 255) / 256;  // words scanned per thread
+    const int per = (NW + NTH - 1) / NTH;  // words scanned per thread
     for (int c0 = 0; c0 < P; c0 += C) {
         const int c1 = min(P, c0 + C);
-        for (int w = tid; w < NW; w += 256) s.bits[w] = 0;
+        for (int w = tid; w < NW; w += NTH) s.bits[w] = 0;
         __syncthreads();
-        for (int i = c0 + tid; i < c1; i += 256) {
+        for (int i = c0 + tid; i < c1; i += NTH) {
             const uint32_t e = idx[i];
             if (e < (uint32_t)E) atomicOr(&s.bits[e * W + ((i - c0) >> 5)], 1u << ((i - c0) & 31));
         }
@@ -285,9 +352,9 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
                 run += __popc(s.bits[w]);
             }
         }
-        if (tid == 255) s.pre[NW] = run;
+        if (tid == NTH - 1) s.pre[NW] = run;
         __syncthreads();
-        for (int i = c0 + tid; i < c1; i += 256) {
+        for (int i = c0 + tid; i < c1; i += NTH) {
             const uint32_t e = idx[i];
             if (e >= (uint32_t)E) {
                 inv[i] = -1;
@@ -301,21 +368,22 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
             inv[i] = pos;
         }
         __syncthreads();
-        for (int e = tid; e < E; e += 256) s.base[e] += s.pre[(e + 1) * W] - s.pre[e * W];
+        for (int e = tid; e < E; e += NTH) s.base[e] += s.pre[(e + 1) * W] - s.pre[e * W];
         __syncthreads();
     }
 }
 
 // --------------------------------------------------- activation conversion
 
-__device__ void act_prep_wave(const float *__restrict__ x, int rows, int K, half_t *__restrict__ q,
-                              float4 *__restrict__ side, size_t w, int lane)
+// x f32 [rows][K] -> the MFMA activation format (common.h): one wavefront per
+// (row, 64-column group); ds[g * ld + row].
+__device__ void act_prep_wave(const float *__restrict__ x, int rows, int K, const ActQ &xq, size_t w, int lane)
 {
     const int G = K / 64;
     if (w >= (size_t)rows * G) return;
     const size_t r = w / G;
     const int g = (int)(w % G);
-    act_group(x[r * K + g * 64 + lane], lane, q + r * K + g * 64, side + r * G + g);
+    act_group(x[r * K + g * 64 + lane], lane, xq.q + r * K + g * 64, xq.ds + (size_t)g * xq.ld + r);
 }
 
 // ------------------------------------------------------- route launches
@@ -327,38 +395,53 @@ struct RouteArgs {
     uint32_t *idx;
     const float *x;  // activations to convert in the same launch (null = none)
     int H;
-    half_t *xq;
-    float4 *xside;
+    ActQ xq;
     int n_route_blocks;
 };
 
-// Blocks [0, n_route_blocks) route 4 tokens each (one wavefront per token);
+constexpr int kDispThreads = 1024;
+constexpr int kFusedMaxEntries = 2048;  // T*k routed and dispatched by one workgroup
+
+// Blocks [0, n_route_blocks) route 16 tokens each (one 16-lane row per token);
 // blocks after them convert the activations, 4 groups of 64 per block.
 __global__ __launch_bounds__(256) void k_route(RouteArgs a)
 {
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if ((int)blockIdx.x >= a.n_route_blocks) {
-        act_prep_wave(a.x, a.T, a.H, a.xq, a.xside, (size_t)(blockIdx.x - a.n_route_blocks) * 4 + wv, lane);
+        act_prep_wave(a.x, a.T, a.H, a.xq, (size_t)(blockIdx.x - a.n_route_blocks) * 4 + wv, lane);
         return;
     }
-    const int t = blockIdx.x * 4 + wv;
-    if (t < a.T)
-        route_token(a.logits + (size_t)t * a.E, a.E, a.k, a.norm, a.probs + (size_t)t * a.k, a.idx + (size_t)t * a.k,
-                    lane);
+    route_token_row(a.logits, blockIdx.x * 16 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx,
+                    nullptr);
 }
 
-__global__ __launch_bounds__(256) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
-                                                  int32_t *offsets, int32_t *rows, int32_t *slots, int32_t *inv,
-                                                  int32_t *active, int32_t *meta)
+// Decode-sized calls: block 0 (64 rows) routes every token, keeps the expert ids
+// in LDS and dispatches them; the other blocks convert activations.
+__global__ __launch_bounds__(kDispThreads) void k_route_dispatch(RouteArgs a, Dispatch d)
 {
     __shared__ DispLds s;
-    dispatch_block(idx, T, k, E, offsets, rows, slots, inv, active, meta, s);
+    __shared__ uint32_t idx_s[kFusedMaxEntries];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (blockIdx.x > 0) {
+        act_prep_wave(a.x, a.T, a.H, a.xq, (size_t)(blockIdx.x - 1) * (kDispThreads / 64) + wv, lane);
+        return;
+    }
+    for (int t0 = 0; t0 < a.T; t0 += kDispThreads / 16)
+        route_token_row(a.logits, t0 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx, idx_s);
+    __syncthreads();
+    dispatch_block<kDispThreads>(idx_s, a.T, a.k, a.E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, s);
 }
 
-__global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ x, int rows, int K, half_t *__restrict__ q,
-                                                  float4 *__restrict__ side)
+__global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
+                                                           Dispatch d)
 {
-    act_prep_wave(x, rows, K, q, side, (size_t)blockIdx.x * 4 + (threadIdx.x >> 6), threadIdx.x & 63);
+    __shared__ DispLds s;
+    dispatch_block<kDispThreads>(idx, T, k, E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, s);
+}
+
+__global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ x, int rows, int K, ActQ xq)
+{
+    act_prep_wave(x, rows, K, xq, (size_t)blockIdx.x * 4 + (threadIdx.x >> 6), threadIdx.x & 63);
 }
 
 static int check_route_shape(int T, int E, int k)
@@ -383,7 +466,7 @@ int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_
         set_error("route: hidden %d is not a multiple of 64", H);
         return ANEDVD_E_INVALID_SHAPE;
     }
-    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq.q, xq.side, (T + 3) / 4};
+    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, (T + 15) / 16};
     const size_t groups = d_x ? (size_t)T * (H / 64) : 0;
     const unsigned blocks = (unsigned)(a.n_route_blocks + (groups + 3) / 4);
     hipLaunchKernelGGL(k_route, dim3(blocks), dim3(256), 0, st, a);
@@ -395,8 +478,28 @@ int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &
 {
     if (T <= 0) return ANEDVD_OK;
     ANEDVD_TRY(check_route_shape(T, E, k));
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), 0, st, d_idx, T, k, E, d.offsets, d.rows, d.slots, d.inv,
-                       d.active, d.meta);
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(kDispThreads), 0, st, d_idx, T, k, E, d);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
+int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
+                              const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st)
+{
+    if (T <= 0) return ANEDVD_OK;
+    ANEDVD_TRY(check_route_shape(T, E, k));
+    if (d_x && H % 64) {
+        set_error("route: hidden %d is not a multiple of 64", H);
+        return ANEDVD_E_INVALID_SHAPE;
+    }
+    if ((long)T * k > kFusedMaxEntries || T > 64) {  // many tokens: route in parallel, then dispatch
+        ANEDVD_TRY(launch_route(d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, st));
+        return launch_dispatch(d_idx, T, k, E, d, st);
+    }
+    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, 1};
+    const size_t groups = d_x ? (size_t)T * (H / 64) : 0;
+    const unsigned blocks = (unsigned)(1 + (groups + 15) / 16);
+    hipLaunchKernelGGL(k_route_dispatch, dim3(blocks), dim3(kDispThreads), 0, st, a, d);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }
@@ -409,7 +512,7 @@ int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream
         return ANEDVD_E_INVALID_SHAPE;
     }
     const size_t groups = (size_t)rows * (K / 64);
-    hipLaunchKernelGGL(k_act_prep, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st, d_x, rows, K, xq.q, xq.side);
+    hipLaunchKernelGGL(k_act_prep, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st, d_x, rows, K, xq);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }

@@ -5,13 +5,12 @@
 
 namespace anedvd {
 
-// GEMV activation format: f16 values [rows][K], each 64-element group scaled by a
-// power of two and stored pair-permuted (pair_perm), and per group a float4
-// {sum of the lower 32 f16 values, sum of the upper 32, the power of two that
-// undoes the scale, 0} in side[rows][K/64].
+// MFMA activation format (common.h): f16 values q[rows][K] in mma_pos order within
+// each 64-column group, and the descale of each (group, row) in ds[g * ld + row].
 struct ActQ {
     half_t *q;
-    float4 *side;
+    float *ds;
+    int ld;
 };
 
 // Token-to-expert dispatch of T*k (token, slot) entries (engine.zig:1204-1216):
@@ -34,26 +33,29 @@ int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, fl
 int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                  const float *d_x, int H, const ActQ &xq, hipStream_t st);
 int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &d, hipStream_t st);
+// Route, dispatch and (d_x non-null) activation conversion of one forward call:
+// a single launch whose first workgroup routes and dispatches when T*k is small,
+// else a parallel route launch followed by the dispatch.
+int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
+                              const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st);
 int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st);
 
-// k_gemv.hip -- decode-regime expert GEMVs
-struct GemvPlan {
-    int nt;       // tokens per pass over the weights (1, 2, 4 or 8)
-    int ks_gu;    // K split of gate/up
+// k_mm.hip -- expert products on MFMA
+struct MmPlan {
+    int ks_gu;    // K split of gate/up (workgroups per 64-row block)
     int ks_dn;    // K split of down
-    int wk_dn;    // wavefronts splitting one down row group's K (1, 2 or 4)
 };
-bool gemv_supported(int type);
-// max_u: most experts a call can touch; max_group: most tokens one expert can get.
-GemvPlan plan_gemv(int gate_type, int down_type, int H, int I, int max_u, int max_group);
+bool mm_supported(int type);
+// max_u: most experts a call can touch.
+MmPlan plan_mm(int gate_type, int down_type, int H, int I, int max_u);
 // gate/up + SiLU(gate)*up for every dispatched (token, expert) position, written
-// to `act` [P][I] in the activation format.  With plan.ks_gu > 1 the K partials go
-// through `part` [ks][P][2][I] and a second launch adds them in ks order.
+// to `act` [P][I] in the activation format.  With plan.ks_gu > 1 the K partials
+// go to `part` [ks][P][2][I] and a second launch finishes them.
 int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
-                         int max_u, const GemvPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st);
+                         int max_u, const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st);
 // down for every position: ypart [ks_dn][P][H] (the combine adds the K partials).
 int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int max_u,
-                       const GemvPlan &plan, float *ypart, hipStream_t st);
+                       const MmPlan &plan, float *ypart, hipStream_t st);
 int launch_combine(const float *ypart, const int32_t *inv, const float *probs, int T, int k, int H, int KS, int P,
                    const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st);
 

@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <vector>
 
 #include "common.h"
@@ -84,18 +85,17 @@ int ensure(Workspace &w, size_t bytes, hipStream_t st)
     return ANEDVD_OK;
 }
 
-bool tile_type(int t) { return tile_fmt(t).unit != 0; }
-
 int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, size_t bytes, hipStream_t st,
               uint64_t &dev_bytes, const char *what)
 {
     const Fmt f = tile_fmt(type);
-    if (!tile_type(type)) {
+    if (!mm_supported(type)) {
         set_error("%s: ggml type %d is not supported by the GPU layout (q8_0, q4_0, q4_k, q6_k)", what, type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
-    if (rows % kRowGroup || cols % f.unit) {
-        set_error("%s: %d x %d is not a multiple of 64 rows x %d columns", what, rows, cols, f.unit);
+    const int unit_cols = kStep * f.spu;
+    if (rows % kRowBlock || cols % unit_cols) {
+        set_error("%s: %d x %d is not a multiple of %d rows x %d columns", what, rows, cols, kRowBlock, unit_cols);
         return ANEDVD_E_INVALID_SHAPE;
     }
     const size_t per = (size_t)rows * cols / block_elems(type) * block_bytes(type);
@@ -107,12 +107,18 @@ int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, si
     m.rows = rows;
     m.cols = cols;
     m.n = n;
-    m.units = cols / f.unit;
-    m.q_stride = (size_t)rows * m.units * f.chunks * 16;
-    m.s_stride = (size_t)rows * m.units * f.sbytes;
+    m.steps = cols / kStep;
+    m.units = m.steps / f.spu;
+    // per matrix: rows/64 row blocks x steps x 4 tiles x 64 lanes x qb bytes, ...
+    m.q_stride = (size_t)rows * m.steps * 4 * f.qb;
+    m.s_stride = (size_t)rows * m.units * f.sb;
+    m.h_stride = type == ANEDVD_Q6_K ? (size_t)rows * m.steps * 16 : 0;
+    m.d_stride = type == ANEDVD_Q6_K ? (size_t)rows * m.units * 2 : 0;
     ANEDVD_HIP(hipMalloc(&m.q, m.q_stride * n));
-    if (m.s_stride) ANEDVD_HIP(hipMalloc(&m.s, m.s_stride * n));
-    dev_bytes += m.q_stride * n + m.s_stride * n;
+    ANEDVD_HIP(hipMalloc(&m.s, m.s_stride * n));
+    if (m.h_stride) ANEDVD_HIP(hipMalloc(&m.h, m.h_stride * n));
+    if (m.d_stride) ANEDVD_HIP(hipMalloc(&m.d, m.d_stride * n));
+    dev_bytes += (m.q_stride + m.s_stride + m.h_stride + m.d_stride) * n;
     uint8_t *staging = nullptr;
     ANEDVD_HIP(hipMalloc(&staging, bytes));
     hipError_t e = hipMemcpyAsync(staging, host, bytes, hipMemcpyHostToDevice, st);
@@ -130,10 +136,10 @@ int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, si
 
 void free_qmat(QMat &m)
 {
-    if (m.q) (void)hipFree(m.q);
-    if (m.s) (void)hipFree(m.s);
-    m.q = nullptr;
-    m.s = nullptr;
+    for (uint8_t **p : {&m.q, &m.s, &m.h, &m.d}) {
+        if (*p) (void)hipFree(*p);
+        *p = nullptr;
+    }
 }
 
 // All device scratch of one forward call of T tokens with k slots each.
@@ -149,7 +155,7 @@ struct Fwd {
     ActQ sact;          // [T][Is]
     float *sh_part, *sh_ypart, *sh_scale;
     float *h_in, *l_in, *out;  // staging for host-pointer calls
-    GemvPlan plan, splan;
+    MmPlan plan, splan;
     int max_u, P;
 };
 
@@ -159,7 +165,7 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     Fwd x{};
     x.P = P;
     x.max_u = std::min(E, P);
-    x.plan = plan_gemv(L->gate.type, L->down.type, H, I, x.max_u, T);
+    x.plan = plan_mm(L->gate.type, L->down.type, H, I, x.max_u);
     Carve c{base};
     x.logits = c.take<float>((size_t)T * E);
     x.probs = c.take<float>(P);
@@ -170,21 +176,18 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     x.d.inv = c.take<int32_t>(P);
     x.d.active = c.take<int32_t>(E);
     x.d.meta = c.take<int32_t>(4);
-    x.xq.q = c.take<half_t>((size_t)T * H);
-    x.xq.side = c.take<float4>((size_t)T * (H / 64));
-    x.act.q = c.take<half_t>((size_t)P * I);
-    x.act.side = c.take<float4>((size_t)P * (I / 64));
+    x.xq = ActQ{c.take<half_t>((size_t)T * H), c.take<float>((size_t)T * (H / kStep)), T};
+    x.act = ActQ{c.take<half_t>((size_t)P * I), c.take<float>((size_t)P * (I / kStep)), P};
     x.part = x.plan.ks_gu > 1 ? c.take<float>((size_t)x.plan.ks_gu * P * 2 * I) : nullptr;
     x.ypart = c.take<float>((size_t)x.plan.ks_dn * P * H);
     if (L->Is) {
         const int Is = (int)L->Is;
-        x.splan = plan_gemv(L->sgate.type, L->sdown.type, H, Is, 1, T);
+        x.splan = plan_mm(L->sgate.type, L->sdown.type, H, Is, 1);
         x.sd.offsets = c.take<int32_t>(2);
         x.sd.rows = c.take<int32_t>(T);
         x.sd.active = c.take<int32_t>(1);
         x.sd.meta = c.take<int32_t>(4);
-        x.sact.q = c.take<half_t>((size_t)T * Is);
-        x.sact.side = c.take<float4>((size_t)T * (Is / 64));
+        x.sact = ActQ{c.take<half_t>((size_t)T * Is), c.take<float>((size_t)T * (Is / kStep)), T};
         x.sh_part = x.splan.ks_gu > 1 ? c.take<float>((size_t)x.splan.ks_gu * T * 2 * Is) : nullptr;
         x.sh_ypart = c.take<float>((size_t)x.splan.ks_dn * T * H);
         x.sh_scale = c.take<float>(T);
@@ -242,8 +245,7 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
         ANEDVD_TRY(launch_router(L->router, d_h, T, E, H, f.logits, st));
         logits = f.logits;
     }
-    ANEDVD_TRY(launch_route(logits, T, E, k, L->norm, f.probs, f.idx, d_h, H, f.xq, st));
-    ANEDVD_TRY(launch_dispatch(f.idx, T, k, E, f.d, st));
+    ANEDVD_TRY(launch_route_and_dispatch(logits, T, E, k, L->norm, f.probs, f.idx, d_h, H, f.xq, f.d, st));
     mark(1);
     ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.max_u, f.plan, f.part, f.act,
                                     L->gelu, st));
@@ -567,7 +569,7 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
         set_error("expert_accum: bad arguments (expert %u of %u)", expert, L->E);
         return ANEDVD_E_INVALID_ARG;
     }
-    if (!gemv_supported(L->gate.type) || !gemv_supported(L->down.type)) {
+    if (!mm_supported(L->gate.type) || !mm_supported(L->down.type)) {
         set_error("expert_accum: no expert kernel for types %d/%d", L->gate.type, L->down.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
@@ -642,8 +644,8 @@ static int prepare(anedvd_moe_layer *L, size_t T, bool io, Fwd &f)
     }
     anedvd_moe_ctx *ctx = L->ctx;
     ANEDVD_HIP(hipSetDevice(ctx->device));
-    if (!gemv_supported(L->gate.type) || !gemv_supported(L->down.type) || L->gate.type != L->up.type ||
-        (L->Is && (!gemv_supported(L->sgate.type) || !gemv_supported(L->sdown.type)))) {
+    if (!mm_supported(L->gate.type) || !mm_supported(L->down.type) || L->gate.type != L->up.type ||
+        (L->Is && (!mm_supported(L->sgate.type) || !mm_supported(L->sdown.type)))) {
         set_error("forward: no expert kernel for ggml types gate=%d up=%d down=%d", L->gate.type, L->up.type,
                   L->down.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
@@ -737,7 +739,8 @@ int anedvd_moe_synchronize(anedvd_moe_ctx *ctx)
 }
 
 int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, const float *d_h, size_t T,
-                            const float *d_logits, float *d_out, int warmup, int iters, float *ms, float *kernel_ms)
+                            const float *d_logits, float *d_out, int warmup, int iters, int flags, float *ms,
+                            float *kernel_ms)
 {
     if (!layers || !n_layers || !ms || iters <= 0 || warmup < 0) {
         set_error("time_forward: bad arguments");
@@ -745,27 +748,76 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
     }
     anedvd_moe_ctx *ctx = layers[0]->ctx;
     for (size_t i = 0; i < n_layers; i++)
-        if (!layers[i] || layers[i]->ctx != ctx || layers[i]->H != layers[0]->H || layers[i]->E != layers[0]->E) {
+        if (!layers[i] || layers[i]->ctx != ctx || layers[i]->H != layers[0]->H || layers[i]->E != layers[0]->E ||
+            layers[i]->I != layers[0]->I || layers[i]->k != layers[0]->k || layers[i]->Is != layers[0]->Is) {
             set_error("time_forward: layers must share a context and a shape");
             return ANEDVD_E_INVALID_ARG;
         }
     hipStream_t st = ctx->stream;
     Fwd f;
     ANEDVD_TRY(prepare(layers[0], T, false, f));
-    for (int i = 0; i < warmup; i++)
-        ANEDVD_TRY(forward_device(layers[i % n_layers], d_h, (int)T, d_logits, d_out, f, st, nullptr));
-    hipEvent_t t0, t1;
-    ANEDVD_HIP(hipEventCreate(&t0));
-    ANEDVD_HIP(hipEventCreate(&t1));
-    ANEDVD_HIP(hipStreamSynchronize(st));
-    ANEDVD_HIP(hipEventRecord(t0, st));
-    for (int i = 0; i < iters; i++)
-        ANEDVD_TRY(forward_device(layers[i % n_layers], d_h, (int)T, d_logits, d_out, f, st, nullptr));
-    ANEDVD_HIP(hipEventRecord(t1, st));
-    ANEDVD_HIP(hipEventSynchronize(t1));
-    ANEDVD_HIP(hipEventElapsedTime(ms, t0, t1));
-    (void)hipEventDestroy(t0);
-    (void)hipEventDestroy(t1);
+    // With ANEDVD_TIME_GRAPH each layer's forward is captured once into a HIP graph
+    // and the timed loop replays the graphs (one submission per call).
+    std::vector<hipGraphExec_t> execs;
+    auto destroy = [&]() {
+        for (auto &e : execs) (void)hipGraphExecDestroy(e);
+        execs.clear();
+    };
+    if (flags & ANEDVD_TIME_GRAPH) {
+        for (size_t i = 0; i < n_layers; i++) {
+            ANEDVD_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            const int rc = forward_device(layers[i], d_h, (int)T, d_logits, d_out, f, st, nullptr);
+            hipGraph_t g = nullptr;
+            const hipError_t e = hipStreamEndCapture(st, &g);
+            if (rc != ANEDVD_OK || e != hipSuccess) {
+                if (g) (void)hipGraphDestroy(g);
+                destroy();
+                if (rc == ANEDVD_OK) set_error("time_forward: graph capture failed: %s", hipGetErrorString(e));
+                return rc != ANEDVD_OK ? rc : ANEDVD_E_HIP;
+            }
+            hipGraphExec_t x = nullptr;
+            const hipError_t e2 = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e2 != hipSuccess) {
+                destroy();
+                set_error("time_forward: graph instantiation failed: %s", hipGetErrorString(e2));
+                return ANEDVD_E_HIP;
+            }
+            execs.push_back(x);
+        }
+    }
+    auto step = [&](int i) -> int {
+        if (!execs.empty()) {
+            const hipError_t e = hipGraphLaunch(execs[(size_t)i % n_layers], st);
+            if (e != hipSuccess) {
+                set_error("time_forward: graph launch failed: %s", hipGetErrorString(e));
+                return ANEDVD_E_HIP;
+            }
+            return ANEDVD_OK;
+        }
+        return forward_device(layers[(size_t)i % n_layers], d_h, (int)T, d_logits, d_out, f, st, nullptr);
+    };
+    int rc = ANEDVD_OK;
+    for (int i = 0; i < warmup && rc == ANEDVD_OK; i++) rc = step(i);
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    if (rc == ANEDVD_OK && (hipEventCreate(&t0) != hipSuccess || hipEventCreate(&t1) != hipSuccess)) {
+        set_error("time_forward: event creation failed");
+        rc = ANEDVD_E_HIP;
+    }
+    if (rc == ANEDVD_OK && (hipStreamSynchronize(st) != hipSuccess || hipEventRecord(t0, st) != hipSuccess)) {
+        set_error("time_forward: synchronisation failed");
+        rc = ANEDVD_E_HIP;
+    }
+    for (int i = 0; i < iters && rc == ANEDVD_OK; i++) rc = step(i);
+    if (rc == ANEDVD_OK && (hipEventRecord(t1, st) != hipSuccess || hipEventSynchronize(t1) != hipSuccess ||
+                            hipEventElapsedTime(ms, t0, t1) != hipSuccess)) {
+        set_error("time_forward: timing failed");
+        rc = ANEDVD_E_HIP;
+    }
+    if (t0) (void)hipEventDestroy(t0);
+    if (t1) (void)hipEventDestroy(t1);
+    destroy();
+    if (rc != ANEDVD_OK) return rc;
     if (kernel_ms) {
         std::vector<hipEvent_t> ev((size_t)iters * 6);
         for (auto &e : ev) ANEDVD_HIP(hipEventCreate(&e));

@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 
 import numpy as np
 
@@ -82,7 +83,8 @@ SIGNATURES = {
     "anedvd_moe_memcpy_h2d": (_i, [_vp, _vp, _vp, _sz]),
     "anedvd_moe_memcpy_d2h": (_i, [_vp, _vp, _vp, _sz]),
     "anedvd_moe_synchronize": (_i, [_vp]),
-    "anedvd_moe_time_forward": (_i, [C.POINTER(_vp), _sz, _vp, _sz, _vp, _vp, _i, _i, C.POINTER(_f), C.POINTER(_f)]),
+    "anedvd_moe_time_forward": (_i, [C.POINTER(_vp), _sz, _vp, _sz, _vp, _vp, _i, _i, _i, C.POINTER(_f),
+                                     C.POINTER(_f)]),
 }
 
 _lib = None
@@ -123,9 +125,12 @@ class MoeContext:
         h = C.c_void_p()
         _check(lib().anedvd_moe_open(device, C.byref(h)))
         self.h = h
+        self._layers = weakref.WeakSet()  # freed before the context closes
 
     def close(self):
         if self.h:
+            for layer in list(self._layers):
+                layer.free()
             lib().anedvd_moe_close(self.h)
             self.h = None
 
@@ -232,10 +237,12 @@ class MoeLayer:
         h = C.c_void_p()
         _check(lib().anedvd_moe_layer_create(ctx.h, C.byref(d), C.byref(h)))
         self.h = h
+        ctx._layers.add(self)
 
     def free(self):
         if self.h:
-            lib().anedvd_moe_layer_free(self.h)
+            if self.ctx.h:
+                lib().anedvd_moe_layer_free(self.h)
             self.h = None
 
     def __del__(self):
@@ -289,15 +296,19 @@ class MoeLayer:
         _check(lib().anedvd_moe_layer_forward_device(self.h, d_h, n_tokens, d_logits, d_out))
 
 
+TIME_GRAPH = 1
+
+
 def time_forward(layers: list, d_h: int, n_tokens: int, d_logits: int | None, d_out: int,
-                 warmup: int, iters: int, stages: bool = False):
-    """Runs the timed loop inside the library (HIP events on the context's stream).
-    Returns (total_ms, per-stage mean ms or None)."""
+                 warmup: int, iters: int, stages: bool = False, graph: bool = False):
+    """Runs the timed loop inside the library (HIP events on the context's stream),
+    replaying per-layer HIP graphs when `graph`.  Returns (total_ms, per-stage mean
+    ms or None)."""
     arr = (C.c_void_p * len(layers))(*[l.h.value for l in layers])
     ms = C.c_float()
     km = (C.c_float * 6)()
     _check(lib().anedvd_moe_time_forward(arr, len(layers), d_h, n_tokens, d_logits, d_out, warmup, iters,
-                                         C.byref(ms), km if stages else None))
+                                         TIME_GRAPH if graph else 0, C.byref(ms), km if stages else None))
     return ms.value, (list(km) if stages else None)
 
 

@@ -168,13 +168,16 @@ int anedvd_moe_synchronize(anedvd_moe_ctx *ctx);
 /* Runs `warmup` untimed then `iters` timed forward calls, call j using
  * layers[j % n_layers], all inputs device-resident; the timed region is bracketed
  * by HIP events on the context's stream.  *ms = total milliseconds of the timed
- * region.  If `kernel_ms` is non-NULL, a second pass of `iters` calls records
- * events around every stage and kernel_ms[0..5] receives the mean milliseconds per
- * call of: route (router + route + dispatch), expert gate/up, expert down, shared
- * expert, combine, and the whole call. */
+ * region.  flags: ANEDVD_TIME_GRAPH captures each layer's forward once into a
+ * HIP graph and replays it (one submission per call).  If `kernel_ms` is non-NULL,
+ * a further pass of `iters` directly launched calls records events around every
+ * stage and kernel_ms[0..5] receives the mean milliseconds per call of: route
+ * (router + route + dispatch), expert gate/up, expert down, shared expert,
+ * combine, and the whole call. */
+#define ANEDVD_TIME_GRAPH 1
 int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, const float *d_h,
                             size_t n_tokens, const float *d_logits, float *d_out, int warmup,
-                            int iters, float *ms, float *kernel_ms);
+                            int iters, int flags, float *ms, float *kernel_ms);
 
 #ifdef __cplusplus
 }

@@ -293,3 +293,24 @@ def test_forward_repeat_calls_keep_counters_clean(ctx):
     for _ in range(20):
         assert np.array_equal(bits(layer.forward(h)), bits(first))
     layer.free()
+
+
+def test_graph_replay_matches_direct_forward(ctx):
+    """The timed loop's HIP-graph replay computes what the directly launched
+    forward computes, replay after replay, with direct launches in between."""
+    spec = W.QWEN3_30B_A3B_Q8_0
+    L = synth.make_layer(spec, seed=8)
+    layer = moe.MoeLayer(ctx, spec, L)
+    for T in (1, 64):
+        h = synth.activations(spec, T, seed=8)
+        lg = synth.uniform_logits(spec, T, seed=8)
+        want = layer.forward(h, lg)
+        d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lg), ctx.alloc(T * spec.hidden * 4)
+        for _ in range(3):
+            moe.time_forward([layer], d_h, T, d_lg, d_out, 0, 2, graph=True)
+            got = ctx.from_device(d_out, (T, spec.hidden), np.float32)
+            assert np.array_equal(bits(got), bits(want))
+            assert np.array_equal(bits(layer.forward(h, lg)), bits(want))
+        for p in (d_h, d_lg, d_out):
+            ctx.free(p)
+    layer.free()
