@@ -34,6 +34,14 @@
 namespace anedvd {
 
 constexpr int kWaves = 4;
+#ifndef ANEDVD_WG_TARGET
+#define ANEDVD_WG_TARGET 1024
+#endif
+#ifdef ANEDVD_MM_WPE
+#define MM_ATTR __attribute__((amdgpu_waves_per_eu(ANEDVD_MM_WPE)))
+#else
+#define MM_ATTR
+#endif
 constexpr int kMTile = 16;  // tokens per MFMA pass
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -59,13 +67,42 @@ __device__ inline half8 bytes_h8(uint32_t lo, uint32_t hi)
     return h;
 }
 
-template <class T>
-__device__ inline T ld_stream(const T *p)
+__device__ inline uint32_t pick4(u32x4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+// Raw buffer loads: a wave-uniform descriptor (base, size), a per-lane byte offset
+// that stays fixed while a wavefront streams, and a scalar per-step offset -- no
+// per-step 64-bit address arithmetic, and loads outside the buffer return 0.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
+constexpr int kNT = 2;                  // non-temporal: weights are streamed once
+
+__device__ inline rsrc_t make_rsrc(const void *p, size_t bytes)
 {
-    return __builtin_nontemporal_load(p);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, kRsrcWord3);
 }
 
-__device__ inline uint32_t pick4(u32x4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+// The planes of one matrix (expert) of a QMat.
+struct Planes {
+    rsrc_t q, s, h, d;
+    int steps, units;
+};
+
+__device__ inline Planes planes(const QMat &m, int mat)
+{
+    Planes p;
+    p.q = make_rsrc(m.q + (size_t)mat * m.q_stride, m.q_stride);
+    p.s = make_rsrc(m.s + (size_t)mat * m.s_stride, m.s_stride);
+    p.h = make_rsrc(m.h ? m.h + (size_t)mat * m.h_stride : m.q, m.h_stride);
+    p.d = make_rsrc(m.d ? m.d + (size_t)mat * m.d_stride : m.q, m.d_stride);
+    p.steps = m.steps;
+    p.units = m.units;
+    return p;
+}
+
+// Byte offset of (row block rb, step s) in a per-lane plane of `bytes` per lane,
+// and of (rb, unit u) in a per-row plane of `bytes` per row (tile layout).
+__device__ inline int lane_plane_off(const Planes &p, int rb, int s, int bytes) { return (rb * p.steps + s) * 256 * bytes; }
+__device__ inline int row_plane_off(const Planes &p, int rb, int u, int bytes) { return (rb * p.units + u) * 64 * bytes; }
 
 // ------------------------------------------------------------------ decoders
 //
@@ -75,6 +112,7 @@ __device__ inline uint32_t pick4(u32x4 v, int i) { return i == 0 ? v.x : i == 1 
 // MFMA result r then contributes d * r - mn * (activation block sum).
 
 struct MQ8_0 {
+    static constexpr bool kDeep = true;  // weights two steps ahead
     static constexpr int kSpu = 1;
     static constexpr bool kMin = false;
     struct Raw {
@@ -82,15 +120,13 @@ struct MQ8_0 {
         uint32_t s[4];
     };
     struct State {};
-    __device__ static inline void load(Raw &r, const QMat &m, int mat, int rb, int s, int lane)
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
-        const Fmt f = tile_fmt(ANEDVD_Q8_0);
-        const uint8_t *q = m.q + (size_t)mat * m.q_stride, *sp = m.s + (size_t)mat * m.s_stride;
+        const int qo = lane_plane_off(p, rb, s, 16), so = row_plane_off(p, rb, s, 4);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.q[t] = ld_stream((const u32x4 *)(q + tile_q_off(f, m.steps, rb, s, t, lane)));
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane + 1024 * t, qo, kNT);
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-            r.s[t] = ld_stream((const uint32_t *)(sp + tile_s_off(f, m.units, rb, s, t, lane & 15)));
+        for (int t = 0; t < 4; t++) r.s[t] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * t, so, kNT);
     }
     __device__ static inline void begin(const Raw &, State &, int) {}
     __device__ static inline void operand(const Raw &r, const State &, int, int, int t, int j, half8 &b, float &d,
@@ -103,6 +139,7 @@ struct MQ8_0 {
 };
 
 struct MQ4_0 {
+    static constexpr bool kDeep = true;  // weights two steps ahead
     static constexpr int kSpu = 1;
     static constexpr bool kMin = false;
     struct Raw {
@@ -110,15 +147,13 @@ struct MQ4_0 {
         uint32_t s[4];
     };
     struct State {};
-    __device__ static inline void load(Raw &r, const QMat &m, int mat, int rb, int s, int lane)
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
-        const Fmt f = tile_fmt(ANEDVD_Q4_0);
-        const uint8_t *q = m.q + (size_t)mat * m.q_stride, *sp = m.s + (size_t)mat * m.s_stride;
+        const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, 4);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.q[t] = ld_stream((const u32x2 *)(q + tile_q_off(f, m.steps, rb, s, t, lane)));
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-            r.s[t] = ld_stream((const uint32_t *)(sp + tile_s_off(f, m.units, rb, s, t, lane & 15)));
+        for (int t = 0; t < 4; t++) r.s[t] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * t, so, kNT);
     }
     __device__ static inline void begin(const Raw &, State &, int) {}
     __device__ static inline void operand(const Raw &r, const State &, int, int, int t, int j, half8 &b, float &d,
@@ -154,6 +189,7 @@ __device__ inline void scale_min_k4(int j, uint32_t s1, uint32_t s2, uint32_t s3
 // Q4_K: step s covers sub-blocks 2 (s % 4) + j; y = d1 n - m1 with d1 = d * sc,
 // m1 = dmin * m.
 struct MQ4_K {
+    static constexpr bool kDeep = false;  // weights one step ahead
     static constexpr int kSpu = 4;
     static constexpr bool kMin = true;
     struct Raw {
@@ -163,16 +199,16 @@ struct MQ4_K {
     struct State {
         u32x4 sc[4];
     };
-    __device__ static inline void load(Raw &r, const QMat &m, int mat, int rb, int s, int lane)
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
-        const Fmt f = tile_fmt(ANEDVD_Q4_K);
-        const uint8_t *q = m.q + (size_t)mat * m.q_stride, *sp = m.s + (size_t)mat * m.s_stride;
+        const int qo = lane_plane_off(p, rb, s, 8);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.q[t] = ld_stream((const u32x2 *)(q + tile_q_off(f, m.steps, rb, s, t, lane)));
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
         if ((s & 3) == 0) {
+            const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int t = 0; t < 4; t++)
-                r.sc[t] = ld_stream((const u32x4 *)(sp + tile_s_off(f, m.units, rb, s >> 2, t, lane & 15)));
+                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * t, so, kNT);
         }
     }
     __device__ static inline void begin(const Raw &r, State &st, int s)
@@ -199,6 +235,7 @@ struct MQ4_K {
 // its int8 scale is folded into the f16 weights and the super-block's d applied
 // to the result.
 struct MQ6_K {
+    static constexpr bool kDeep = false;  // weights one step ahead
     static constexpr int kSpu = 4;
     static constexpr bool kMin = false;
     struct Raw {
@@ -211,21 +248,20 @@ struct MQ6_K {
         u32x4 sc[4];
         float d[4];
     };
-    __device__ static inline void load(Raw &r, const QMat &m, int mat, int rb, int s, int lane)
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
-        const Fmt f = tile_fmt(ANEDVD_Q6_K);
-        const uint8_t *q = m.q + (size_t)mat * m.q_stride, *hp = m.h + (size_t)mat * m.h_stride;
+        const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            r.q[t] = ld_stream((const u32x2 *)(q + tile_q_off(f, m.steps, rb, s, t, lane)));
-            r.h[t] = ld_stream((const uint32_t *)(hp + tile_h_off(m.steps, rb, s, t, lane)));
+            r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
+            r.h[t] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane + 256 * t, ho, kNT);
         }
         if ((s & 3) == 0) {
-            const uint8_t *sp = m.s + (size_t)mat * m.s_stride, *dp = m.d + (size_t)mat * m.d_stride;
+            const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, 2);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                r.sc[t] = ld_stream((const u32x4 *)(sp + tile_s_off(f, m.units, rb, s >> 2, t, lane & 15)));
-                r.d[t] = *(const uint16_t *)(dp + tile_d_off(m.units, rb, s >> 2, t, lane & 15));
+                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * t, so, kNT);
+                r.d[t] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * t, dof, kNT);
             }
         }
     }
@@ -255,66 +291,129 @@ struct MQ6_K {
 
 // ------------------------------------------------------------------ core
 
+// The activations of one step: lane group g's 16 values of its token row, and the
+// descales of the lane's four result tokens.
+struct AStep {
+    half8 a0, a1;
+    float dv[4];
+};
+
+// Where a lane's activations come from: its token row's byte offset (plus its lane
+// group's 32 bytes) in the f16 values, and its four result tokens' byte offsets in
+// one group's descales (ld4 bytes per group).
+struct AOp {
+    rsrc_t q, ds;
+    int qoff;
+    int doff[4];
+    int ld4;
+};
+
+__device__ inline half8 as_h8(u32x4 v)
+{
+    half8 h;
+    __builtin_memcpy(&h, &v, 16);
+    return h;
+}
+
+__device__ inline void load_a(AStep &x, const AOp &a, int s)
+{
+    x.a0 = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff, s * 2 * kStep, 0));
+    x.a1 = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff + 16, s * 2 * kStep, 0));
+#pragma unroll
+    for (int i = 0; i < 4; i++) x.dv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(a.ds, a.doff[i], s * a.ld4, 0));
+}
+
+// acc[t][i] += the step's contribution (see mm_steps).
+template <class D>
+__device__ inline void mm_step(const typename D::Raw &w, typename D::State &st, const AStep &x, int s, int lane,
+                               f32x4 *acc)
+{
+    const half8 ones = (half8)(half_t)1.0f;
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    D::begin(w, st, s);
+    f32x4 sum0 = zero, sum1 = zero;
+    if (D::kMin) {
+        sum0 = mfma(x.a0, ones, zero);
+        sum1 = mfma(x.a1, ones, zero);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            half8 b;
+            float d, mn;
+            D::operand(w, st, s, lane, t, j, b, d, mn);
+            const f32x4 r = mfma(j ? x.a1 : x.a0, b, zero);
+            const f32x4 sm = j ? sum1 : sum0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float v = D::kMin ? d * r[i] - mn * sm[i] : d * r[i];
+                acc[t][i] += x.dv[i] * v;
+            }
+        }
+    }
+}
+
 // Streams steps [s0, s1) of the wavefront's four tiles (row block rb of matrix
 // `mat`) against 16 tokens: lane l feeds A rows from `arow` (its token l % 16, the
 // row's column 0) and accumulates acc[t][i] = sum_k W[64 rb + 16 t + l % 16][k] *
 // x[token 4 (l / 16) + i][k], the tokens' descales taken from ds[step * ld +
-// dsrow[i]].  The next step's weights, activations and descales are in flight
-// while the current step's MFMAs run.
+// dsrow[i]].  Weights are loaded two steps ahead of the MFMAs that use them (three
+// register buffers in rotation) and activations one step ahead, issued before the
+// weights so that waiting for them never waits for the later weight loads.
 template <class D>
-__device__ inline void mm_steps(const QMat &W, int mat, int rb, int s0, int s1, int lane, const half_t *arow,
-                                const float *ds, int ld, const int *dsrow, f32x4 *acc)
+__device__ inline void mm_steps(const Planes &W, int rb, int s0, int s1, int lane, const AOp &A, f32x4 *acc)
 {
     if (s0 >= s1) return;
-    const int g = lane >> 4;
-    typename D::Raw cur, nxt;
-    typename D::State st;
-    D::load(cur, W, mat, rb, s0, lane);
-    const half8 *ap = (const half8 *)(arow + (size_t)kStep * s0 + 16 * g);
-    half8 a0 = ap[0], a1 = ap[1];
-    float dv[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) dv[i] = ds[(size_t)s0 * ld + dsrow[i]];
-    const half8 ones = (half8)(half_t)1.0f;
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s = s0; s < s1; s++) {
-        half8 na0 = a0, na1 = a1;
-        float ndv[4] = {dv[0], dv[1], dv[2], dv[3]};
-        if (s + 1 < s1) {
-            D::load(nxt, W, mat, rb, s + 1, lane);
-            const half8 *np = (const half8 *)(arow + (size_t)kStep * (s + 1) + 16 * g);
-            na0 = np[0];
-            na1 = np[1];
-#pragma unroll
-            for (int i = 0; i < 4; i++) ndv[i] = ds[(size_t)(s + 1) * ld + dsrow[i]];
-        }
-        D::begin(cur, st, s);
-        f32x4 sum0 = zero, sum1 = zero;
-        if (D::kMin) {
-            sum0 = mfma(a0, ones, zero);
-            sum1 = mfma(a1, ones, zero);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                half8 b;
-                float d, mn;
-                D::operand(cur, st, s, lane, t, j, b, d, mn);
-                const f32x4 r = mfma(j ? a1 : a0, b, zero);
-                const f32x4 sm = j ? sum1 : sum0;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float v = D::kMin ? d * r[i] - mn * sm[i] : d * r[i];
-                    acc[t][i] += dv[i] * v;
-                }
+    if (!D::kDeep) {  // one step ahead: the super-block formats carry more state per buffer
+        typename D::Raw w0, w1;
+        typename D::State st;
+        AStep x0, x1;
+        load_a(x0, A, s0);
+        D::load(w0, W, rb, s0, lane);
+        for (int s = s0; s < s1; s += 2) {
+            if (s + 1 < s1) {
+                load_a(x1, A, s + 1);
+                D::load(w1, W, rb, s + 1, lane);
             }
+            mm_step<D>(w0, st, x0, s, lane, acc);
+            if (s + 1 >= s1) break;
+            if (s + 2 < s1) {
+                load_a(x0, A, s + 2);
+                D::load(w0, W, rb, s + 2, lane);
+            }
+            mm_step<D>(w1, st, x1, s + 1, lane, acc);
         }
-        cur = nxt;
-        a0 = na0;
-        a1 = na1;
-#pragma unroll
-        for (int i = 0; i < 4; i++) dv[i] = ndv[i];
+        return;
+    }
+    // Loads are unconditional -- past the last step they repeat it, an L2 hit -- so
+    // every trip through the loop issues the same loads in the same order and the
+    // compiler's wait counts stay exact (a skipped load would make them
+    // conservative at the loop head and serialise the prefetch).
+    const int sl = s1 - 1;
+    typename D::Raw w0, w1, w2;
+    typename D::State st;
+    AStep x0, x1, x2;
+    load_a(x0, A, s0);
+    D::load(w0, W, rb, s0, lane);
+    D::load(w1, W, rb, min(s0 + 1, sl), lane);
+    // sched_barrier keeps the scheduler from sinking the prefetches down to their
+    // uses (which it does to shorten live ranges, undoing the pipelining).
+    for (int s = s0; s < s1; s += 3) {
+        load_a(x1, A, min(s + 1, sl));
+        D::load(w2, W, rb, min(s + 2, sl), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        mm_step<D>(w0, st, x0, s, lane, acc);
+        if (s + 1 >= s1) break;
+        load_a(x2, A, min(s + 2, sl));
+        D::load(w0, W, rb, min(s + 3, sl), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        mm_step<D>(w1, st, x1, s + 1, lane, acc);
+        if (s + 2 >= s1) break;
+        load_a(x0, A, min(s + 3, sl));
+        D::load(w1, W, rb, min(s + 4, sl), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        mm_step<D>(w2, st, x2, s + 2, lane, acc);
     }
 }
 
@@ -343,7 +442,7 @@ struct MmArgs {
 // w & 1 of the workgroup's K units; the four are summed through LDS and wave 0
 // applies SiLU(g) * u to its 64 rows x 16 tokens.
 template <class D>
-__global__ __launch_bounds__(256) void k_mm_gateup(MmArgs a)
+__global__ __launch_bounds__(256) MM_ATTR void k_mm_gateup(MmArgs a)
 {
     __shared__ f32x4 xch[3][4][64];
     const int ua = blockIdx.y;
@@ -356,20 +455,22 @@ __global__ __launch_bounds__(256) void k_mm_gateup(MmArgs a)
     const int mat = wv >> 1, half = wv & 1;
     const int hu = (upw + 1) / 2;
     const int ub = u0 + half * hu, ue = min(u0 + upw, ub + hu);
-    const QMat &W = mat ? a.w1 : a.w0;
+    const Planes W = planes(mat ? a.w1 : a.w0, e);
     const int n = lane & 15, gq = lane >> 4;
+    AOp A;
+    A.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);  // x: ld = tokens
+    A.ds = make_rsrc(a.x.ds, (size_t)(a.H / kStep) * a.x.ld * 4);
+    A.ld4 = a.x.ld * 4;
 
     for (int c0 = 0; c0 < ne; c0 += kMTile) {
         const int nt = min(kMTile, ne - c0);
-        const int tok = a.d.rows[p0 + c0 + min(n, nt - 1)];
-        int dsrow[4];
+        A.qoff = a.d.rows[p0 + c0 + min(n, nt - 1)] * a.H * 2 + 32 * gq;
 #pragma unroll
-        for (int i = 0; i < 4; i++) dsrow[i] = a.d.rows[p0 + c0 + min(4 * gq + i, nt - 1)];
+        for (int i = 0; i < 4; i++) A.doff[i] = a.d.rows[p0 + c0 + min(4 * gq + i, nt - 1)] * 4;
         f32x4 acc[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        mm_steps<D>(W, e, rb, ub * D::kSpu, ue * D::kSpu, lane, a.x.q + (size_t)tok * a.H, a.x.ds, a.x.ld, dsrow,
-                    acc);
+        mm_steps<D>(W, rb, ub * D::kSpu, ue * D::kSpu, lane, A, acc);
         if (wv) {
 #pragma unroll
             for (int t = 0; t < 4; t++) xch[wv - 1][t][lane] = acc[t];
@@ -449,7 +550,7 @@ __global__ __launch_bounds__(256) void k_act_reduce(MmArgs a)
 // Grid (ceil(H/256) * KS, max_u), 256 threads; wave w owns row block 4 x + w of
 // the output and the workgroup's K units.
 template <class D>
-__global__ __launch_bounds__(256) void k_mm_down(MmArgs a)
+__global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
 {
     const int ua = blockIdx.y;
     if (ua >= a.d.meta[0]) return;
@@ -460,18 +561,21 @@ __global__ __launch_bounds__(256) void k_mm_down(MmArgs a)
     if (rb >= a.H / kRowBlock) return;  // no barriers in this kernel
     const int units = a.I / kStep / D::kSpu, upw = units / a.KS, u0 = ks * upw;
     const int n = lane & 15, gq = lane >> 4;
+    const Planes W = planes(a.w0, e);
+    AOp A;
+    A.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
+    A.ds = make_rsrc(a.x.ds, (size_t)(a.I / kStep) * a.x.ld * 4);
+    A.ld4 = a.x.ld * 4;
 
     for (int c0 = 0; c0 < ne; c0 += kMTile) {
         const int nt = min(kMTile, ne - c0);
-        const int pos = p0 + c0 + min(n, nt - 1);
-        int dsrow[4];
+        A.qoff = (p0 + c0 + min(n, nt - 1)) * a.I * 2 + 32 * gq;
 #pragma unroll
-        for (int i = 0; i < 4; i++) dsrow[i] = p0 + c0 + min(4 * gq + i, nt - 1);
+        for (int i = 0; i < 4; i++) A.doff[i] = (p0 + c0 + min(4 * gq + i, nt - 1)) * 4;
         f32x4 acc[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        mm_steps<D>(a.w0, e, rb, u0 * D::kSpu, (u0 + upw) * D::kSpu, lane, a.x.q + (size_t)pos * a.I, a.x.ds, a.x.ld,
-                    dsrow, acc);
+        mm_steps<D>(W, rb, u0 * D::kSpu, (u0 + upw) * D::kSpu, lane, A, acc);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = 4 * gq + i;
@@ -486,58 +590,73 @@ __global__ __launch_bounds__(256) void k_mm_down(MmArgs a)
 
 // ------------------------------------------------------------- combine
 
-// out[t][h] = sum over slots s (in slot order) of p[t][s] * y[pos(t,s)][h], the
-// KS down partials of a position added in fixed order; a deterministic gather,
-// no atomics (main.zig:495-509 / engine.zig:725-777).  Then + scale * shared.
-// Slots are taken 8 at a time with their loads issued together (indices clamped
-// rather than branched on, so nothing waits on the previous slot).
+constexpr int kCombLanes = 8;   // slot lanes per output column group
+constexpr int kCombCols = 32;   // float4 column groups per workgroup
+constexpr int kMaxKS = 16;      // K partials the combine reads per position
+
+// out[t][h] = sum over slots s of p[t][s] * y[pos(t,s)][h] (+ scale[t] * shared),
+// a deterministic gather, no atomics (main.zig:495-509 / engine.zig:725-777).
+// Thread (c, l) of a workgroup takes column group c and the slots s = l, l + 8,
+// ...: it issues the KS partial loads of a slot together (one memory round trip
+// per slot instead of one per partial), adds them in partial order and weights
+// them; the eight slot-lane sums are then added in lane order through LDS.  The
+// order of every addition is fixed, so results do not depend on scheduling.
+// Grid: (ceil(H/4 / 32), T).
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart, const int32_t *__restrict__ inv,
                                                  const float *__restrict__ probs, int T, int k, int H, int KS, int P,
                                                  const float *__restrict__ shared, const float *__restrict__ shared_scale,
                                                  int sKS, float *__restrict__ out)
 {
-    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int H4 = H / 4;
-    if (id >= (size_t)T * H4) return;
-    const int t = (int)(id / H4), h = (int)(id % H4) * 4;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < k; s0 += 8) {
-        int pos[8];
-        float p[8];
-        bool ok[8];
-        float4 y[8];
+    __shared__ float4 part[kCombLanes + 1][kCombCols];  // slot-lane sums, then the shared term
+    const int c = threadIdx.x % kCombCols, l = threadIdx.x / kCombCols;
+    const int h = (blockIdx.x * kCombCols + c) * 4;
+    const bool live = h < H;
+    for (int t = blockIdx.y; t < T; t += gridDim.y) {  // uniform over the workgroup
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = l; s < k && live; s += kCombLanes) {
+            const int pos = inv[(size_t)t * k + s];
+            if (pos < 0) continue;
+            const float p = probs[(size_t)t * k + s];
+            float4 z[kMaxKS];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int s = min(s0 + i, k - 1);
-            pos[i] = inv[(size_t)t * k + s];
-            p[i] = probs[(size_t)t * k + s];
-            ok[i] = s0 + i < k && pos[i] >= 0;
-            pos[i] = max(pos[i], 0);
-            y[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int q = 0; q < kMaxKS; q++)
+                if (q < KS) z[q] = *(const float4 *)(ypart + ((size_t)q * P + pos) * H + h);
+            float4 y = z[0];
+#pragma unroll
+            for (int q = 1; q < kMaxKS; q++)
+                if (q < KS) {
+                    y.x += z[q].x; y.y += z[q].y; y.z += z[q].z; y.w += z[q].w;
+                }
+            acc.x += p * y.x; acc.y += p * y.y; acc.z += p * y.z; acc.w += p * y.w;
         }
-        for (int q = 0; q < KS; q++) {
+        part[l][c] = acc;
+        if (l == 0 && shared && live) {  // the shared expert's partials [sKS][T][H], then its scale
+            const float sc = shared_scale ? shared_scale[t] : 1.0f;
+            float4 z[kMaxKS];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 z = *(const float4 *)(ypart + ((size_t)q * P + pos[i]) * H + h);
-                y[i].x += z.x; y[i].y += z.y; y[i].z += z.z; y[i].w += z.w;
+            for (int q = 0; q < kMaxKS; q++)
+                if (q < sKS) z[q] = *(const float4 *)(shared + ((size_t)q * T + t) * H + h);
+            float4 y = z[0];
+#pragma unroll
+            for (int q = 1; q < kMaxKS; q++)
+                if (q < sKS) {
+                    y.x += z[q].x; y.y += z[q].y; y.z += z[q].z; y.w += z[q].w;
+                }
+            part[kCombLanes][c] = make_float4(sc * y.x, sc * y.y, sc * y.z, sc * y.w);
+        }
+        __syncthreads();
+        if (l == 0 && live) {
+            float4 r = part[0][c];
+#pragma unroll
+            for (int i = 1; i < kCombLanes + 1; i++) {
+                if (i == kCombLanes && !shared) break;
+                const float4 v = part[i][c];
+                r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
             }
+            *(float4 *)(out + (size_t)t * H + h) = r;
         }
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (ok[i]) {
-                acc.x += p[i] * y[i].x; acc.y += p[i] * y[i].y; acc.z += p[i] * y[i].z; acc.w += p[i] * y[i].w;
-            }
+        __syncthreads();
     }
-    if (shared) {  // the shared expert's down partials [sKS][T][H], then its scale
-        const float sc = shared_scale ? shared_scale[t] : 1.0f;
-        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int q = 0; q < sKS; q++) {
-            const float4 z = *(const float4 *)(shared + ((size_t)q * T + t) * H + h);
-            y.x += z.x; y.y += z.y; y.z += z.z; y.w += z.w;
-        }
-        acc.x += sc * y.x; acc.y += sc * y.y; acc.z += sc * y.z; acc.w += sc * y.w;
-    }
-    *(float4 *)(out + (size_t)t * H + h) = acc;
 }
 
 // ------------------------------------------------------------- planning
@@ -546,19 +665,19 @@ static int steps_per_unit(int type) { return tile_fmt(type).spu; }
 
 bool mm_supported(int type) { return tile_fmt(type).qb != 0; }
 
-// Splits a K axis of `units` scale units over ks workgroups, ks dividing units:
-// the smallest ks that gives `wg_per_ks * ks` >= 1024 workgroups (4 per CU) while
-// every wavefront keeps >= `min_steps` steps of `waves_per_k` shares, else the
-// largest ks keeping them.
+// Splits a K axis of `units` scale units over ks workgroups, ks dividing units
+// and at most kMaxKS (the partials the combine reads): the smallest ks that gives
+// `wg_per_ks * ks` >= ANEDVD_WG_TARGET workgroups while every wavefront keeps >=
+// `min_steps` steps of `waves_per_k` shares, else the largest ks keeping them.
 static int choose_ks(int units, int spu, long wg_per_ks, int waves_per_k, int min_steps)
 {
     int best = 1;
-    for (int ks = 1; ks <= units; ks++) {
+    for (int ks = 1; ks <= std::min(units, kMaxKS); ks++) {
         if (units % ks) continue;
         const int steps = (units / ks) * spu / waves_per_k;
         if (ks > 1 && steps < min_steps) break;
         best = ks;
-        if (wg_per_ks * ks >= 1024) break;
+        if (wg_per_ks * ks >= ANEDVD_WG_TARGET) break;
     }
     return best;
 }
@@ -570,6 +689,9 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int max_u)
                         2, 2);
     p.ks_dn = choose_ks(I / kStep / steps_per_unit(down_type), steps_per_unit(down_type),
                         (long)max_u * ((H / kRowBlock + kWaves - 1) / kWaves), 1, 2);
+#ifdef ANEDVD_KS_DN
+    if (max_u > 64 && (I / kStep / steps_per_unit(down_type)) % ANEDVD_KS_DN == 0) p.ks_dn = ANEDVD_KS_DN;
+#endif
     return p;
 }
 
@@ -654,10 +776,14 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
 int launch_combine(const float *ypart, const int32_t *inv, const float *probs, int T, int k, int H, int KS, int P,
                    const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st)
 {
-    const size_t n = (size_t)T * (H / 4);
-    if (n == 0) return ANEDVD_OK;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, ypart, inv, probs, T, k, H, KS, P,
-                       shared, shared_scale, sKS, out);
+    if (T <= 0) return ANEDVD_OK;
+    if (KS > kMaxKS || sKS > kMaxKS) {
+        set_error("combine: %d K partials, at most %d", max(KS, sKS), kMaxKS);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    const dim3 grid((unsigned)((H / 4 + kCombCols - 1) / kCombCols), (unsigned)std::min(T, 65535));
+    hipLaunchKernelGGL(k_combine, grid, dim3(kCombLanes * kCombCols), 0, st, ypart, inv, probs, T, k, H, KS, P, shared,
+                       shared_scale, sKS, out);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }

@@ -17,6 +17,15 @@ namespace anedvd {
 
 __constant__ uint64_t c_exp2_tab[32] = ANEDVD_EXP2_TABLE;
 
+// The exp table is read per lane with data-dependent indices: each routing
+// workgroup copies it to LDS first, so a lookup costs an LDS read rather than a
+// trip to the L2.  Call from every thread, before the first route_row.
+__device__ inline void load_exp_table(uint64_t *tab)
+{
+    if (threadIdx.x < 32) tab[threadIdx.x] = c_exp2_tab[threadIdx.x];
+    __syncthreads();
+}
+
 // ------------------------------------------------------------------ router
 
 // Block: 256 threads = 32 experts x 8 lanes.  Grid: (ceil(E/32), ceil(T/TT)).
@@ -77,67 +86,51 @@ int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, fl
 
 // ------------------------------------------------------------------- route
 
-// One step of a wavefront max over u64 keys: v = max(v, v of the lane the DPP
-// control names); lanes without a source keep their own value.
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ inline uint64_t dpp_max_u64(uint64_t v)
-{
-    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, ROW_MASK, 0xF, false);
-    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, ROW_MASK, 0xF, false);
-    const uint64_t o = ((uint64_t)ohi << 32) | olo;
-    return o > v ? o : v;
-}
-
-// Max of v over the 64 lanes, returned wave-uniform: DPP swaps within quads, row
-// mirrors, then row broadcasts 15 and 31 carry the row maxima up to lane 63.
-__device__ inline uint64_t wave_max_u64(uint64_t v)
-{
-    v = dpp_max_u64<0xB1>(v);        // quad_perm [1,0,3,2]
-    v = dpp_max_u64<0x4E>(v);        // quad_perm [2,3,0,1]
-    v = dpp_max_u64<0x141>(v);       // row_half_mirror
-    v = dpp_max_u64<0x140>(v);       // row_mirror
-    v = dpp_max_u64<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
-    v = dpp_max_u64<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-__device__ inline float lane_value(float v, int lane)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
 constexpr int kMaxExperts = 256;
 constexpr int kMaxK = 32;
 
 // ----------------------------------------------------- 16-lane row routing
 //
 // A DPP row (16 lanes) routes one token, so a wavefront routes 4 at once.  Lane
-// li of the row holds experts [li*VPL, (li+1)*VPL).  Row-wide max and argmax use
+// li of the row holds experts [li*VPL, (li+1)*VPL).  Row-wide max and argmin use
 // DPP swaps within the row (every lane ends with the result); the softmax
 // denominator is the reference's sequential sum in ascending expert order, carried
 // lane to lane with row_shr:1, each lane adding its experts one at a time.
 
-__device__ inline uint64_t row_max_u64(uint64_t v)
+template <int CTRL>
+__device__ inline uint32_t dpp_u32(uint32_t v)
 {
-    v = dpp_max_u64<0xB1>(v);
-    v = dpp_max_u64<0x4E>(v);
-    v = dpp_max_u64<0x141>(v);
-    v = dpp_max_u64<0x140>(v);
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+__device__ inline uint32_t row_max_u32(uint32_t v)
+{
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    v = max(v, dpp_u32<0x140>(v));
     return v;
 }
 
-// cpu.moeRoute (cpu.zig:1236-1288) for one token per row.  Selection key =
-// (p bits << 32) | ~e: p >= 0, so its bits order like the value, and among equal p
-// the lowest expert has the largest key -- the reference's strict `p > best_p`
-// scan in ascending e.  NaN probabilities are never chosen; a slot with nothing
-// left to choose gets (0, expert 0), as in the reference.  All lanes of the wave
+__device__ inline uint32_t row_min_u32(uint32_t v)
+{
+    v = min(v, dpp_u32<0xB1>(v));
+    v = min(v, dpp_u32<0x4E>(v));
+    v = min(v, dpp_u32<0x141>(v));
+    v = min(v, dpp_u32<0x140>(v));
+    return v;
+}
+
+// cpu.moeRoute (cpu.zig:1236-1288) for one token per row.  Each unchosen expert
+// with a non-NaN probability p carries key = bits(p) + 1 (p is in [0, 1], so its
+// bits order like its value and +0 still beats an empty slot); chosen experts and
+// NaNs carry 0.  A slot takes the row's largest key, then the lowest expert
+// holding it -- the reference's strict `p > best_p` scan in ascending e.  A slot
+// with nothing left gets (0, expert 0), as in the reference.  All lanes of the wave
 // run this (rows with live == false compute on -inf and store nothing).
 template <int VPL>
 __device__ void route_row(const float *__restrict__ lg, bool live, int E, int k, int norm, float *__restrict__ probs,
-                          uint32_t *__restrict__ idx, uint32_t *idx_copy, int li)
+                          uint32_t *__restrict__ idx, uint32_t *idx_copy, int li, const uint64_t *tab)
 {
     const int e0 = li * VPL;
     float v[VPL];
@@ -149,7 +142,7 @@ __device__ void route_row(const float *__restrict__ lg, bool live, int E, int k,
     mx = row_max_f32(mx);
     float ex[VPL];
 #pragma unroll
-    for (int j = 0; j < VPL; j++) ex[j] = expf_exact(v[j] - mx, c_exp2_tab);
+    for (int j = 0; j < VPL; j++) ex[j] = expf_exact(v[j] - mx, tab);
     // sequential sum: before step L, lane L holds the sum of experts < L*VPL
     float run = 0.0f, t = 0.0f;
 #pragma unroll
@@ -163,28 +156,32 @@ __device__ void route_row(const float *__restrict__ lg, bool live, int E, int k,
     const float sum = __shfl(t, (threadIdx.x & 63 & ~15) + 15, 64);  // lane 15 of the row
     const float inv_sum = sum > 0.0f ? __fdiv_rn(1.0f, sum) : 0.0f;
 
-    uint64_t key[VPL];
+    uint32_t key[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; j++) {
         const float p = __fmul_rn(ex[j], inv_sum);
-        const bool ok = live && e0 + j < E && !(p != p);
-        key[j] = ok ? ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)(e0 + j)) : 0ull;
+        key[j] = (live && e0 + j < E && !(p != p)) ? __float_as_uint(p) + 1u : 0u;
     }
     float my_p0 = 0.0f, my_p1 = 0.0f, rsum = 0.0f;
     uint32_t my_i0 = 0, my_i1 = 0;
     for (int slot = 0; slot < k; slot++) {
-        uint64_t best = key[0];
+        uint32_t m = key[0];
 #pragma unroll
-        for (int j = 1; j < VPL; j++) best = key[j] > best ? key[j] : best;
-        best = row_max_u64(best);
+        for (int j = 1; j < VPL; j++) m = max(m, key[j]);
+        const uint32_t best = row_max_u32(m);
+        uint32_t cand = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = VPL - 1; j >= 0; j--)
+            if (key[j] == best) cand = (uint32_t)(e0 + j);
+        const uint32_t first = row_min_u32(cand);
         float bp = 0.0f;
         uint32_t be = 0;
-        if (best != 0ull) {
-            be = 0xFFFFFFFFu - (uint32_t)best;
-            bp = __uint_as_float((uint32_t)(best >> 32));
+        if (best != 0u) {
+            be = first;
+            bp = __uint_as_float(best - 1u);
 #pragma unroll
             for (int j = 0; j < VPL; j++)
-                if (key[j] == best) key[j] = 0ull;
+                if ((uint32_t)(e0 + j) == be) key[j] = 0u;
         }
         rsum = __fadd_rn(rsum, bp);  // the renormalisation sum, in slot order
         if (li == (slot & 15)) {
@@ -216,7 +213,8 @@ __device__ void route_row(const float *__restrict__ lg, bool live, int E, int k,
 
 // Routes token t (if t < T) on this thread's row.
 __device__ inline void route_token_row(const float *__restrict__ logits, int t, int T, int E, int k, int norm,
-                                       float *__restrict__ probs, uint32_t *__restrict__ idx, uint32_t *idx_copy)
+                                       float *__restrict__ probs, uint32_t *__restrict__ idx, uint32_t *idx_copy,
+                                       const uint64_t *tab)
 {
     const bool live = t < T;
     const int tt = live ? t : 0;
@@ -225,11 +223,11 @@ __device__ inline void route_token_row(const float *__restrict__ logits, int t, 
     uint32_t *ix = idx + (size_t)tt * k;
     uint32_t *ic = idx_copy ? idx_copy + (size_t)tt * k : nullptr;
     const int li = threadIdx.x & 15;
-    if (E <= 16) route_row<1>(lg, live, E, k, norm, pr, ix, ic, li);
-    else if (E <= 32) route_row<2>(lg, live, E, k, norm, pr, ix, ic, li);
-    else if (E <= 64) route_row<4>(lg, live, E, k, norm, pr, ix, ic, li);
-    else if (E <= 128) route_row<8>(lg, live, E, k, norm, pr, ix, ic, li);
-    else route_row<16>(lg, live, E, k, norm, pr, ix, ic, li);
+    if (E <= 16) route_row<1>(lg, live, E, k, norm, pr, ix, ic, li, tab);
+    else if (E <= 32) route_row<2>(lg, live, E, k, norm, pr, ix, ic, li, tab);
+    else if (E <= 64) route_row<4>(lg, live, E, k, norm, pr, ix, ic, li, tab);
+    else if (E <= 128) route_row<8>(lg, live, E, k, norm, pr, ix, ic, li, tab);
+    else route_row<16>(lg, live, E, k, norm, pr, ix, ic, li, tab);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -322,7 +320,8 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
             meta[2] = s.bad;
         }
     }
-    const int W = kDispWords / E;  // bitmap words per expert per chunk
+    // bitmap words per expert per chunk: enough for all P entries when they fit
+    const int W = max(1, min(kDispWords / E, (P + 31) / 32));
     const int C = 32 * W, NW = W * E;
     const int per = (NW + NTH - 1) / NTH;  // words scanned per thread
     for (int c0 = 0; c0 < P; c0 += C) {
@@ -406,13 +405,15 @@ constexpr int kFusedMaxEntries = 2048;  // T*k routed and dispatched by one work
 // blocks after them convert the activations, 4 groups of 64 per block.
 __global__ __launch_bounds__(256) void k_route(RouteArgs a)
 {
+    __shared__ uint64_t tab[32];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if ((int)blockIdx.x >= a.n_route_blocks) {
         act_prep_wave(a.x, a.T, a.H, a.xq, (size_t)(blockIdx.x - a.n_route_blocks) * 4 + wv, lane);
         return;
     }
+    load_exp_table(tab);
     route_token_row(a.logits, blockIdx.x * 16 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx,
-                    nullptr);
+                    nullptr, tab);
 }
 
 // Decode-sized calls: block 0 (64 rows) routes every token, keeps the expert ids
@@ -421,13 +422,15 @@ __global__ __launch_bounds__(kDispThreads) void k_route_dispatch(RouteArgs a, Di
 {
     __shared__ DispLds s;
     __shared__ uint32_t idx_s[kFusedMaxEntries];
+    __shared__ uint64_t tab[32];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (blockIdx.x > 0) {
         act_prep_wave(a.x, a.T, a.H, a.xq, (size_t)(blockIdx.x - 1) * (kDispThreads / 64) + wv, lane);
         return;
     }
+    load_exp_table(tab);
     for (int t0 = 0; t0 < a.T; t0 += kDispThreads / 16)
-        route_token_row(a.logits, t0 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx, idx_s);
+        route_token_row(a.logits, t0 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx, idx_s, tab);
     __syncthreads();
     dispatch_block<kDispThreads>(idx_s, a.T, a.k, a.E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, s);
 }
