@@ -84,7 +84,7 @@ __device__ inline rsrc_t make_rsrc(const void *p, size_t bytes)
 // The planes of one matrix (expert) of a QMat.
 struct Planes {
     rsrc_t q, s, h, d;
-    int steps, units;
+    int steps, units, nrb;  // nrb: row blocks of the matrix
 };
 
 __device__ inline Planes planes(const QMat &m, int mat)
@@ -96,6 +96,7 @@ __device__ inline Planes planes(const QMat &m, int mat)
     p.d = make_rsrc(m.d ? m.d + (size_t)mat * m.d_stride : m.q, m.d_stride);
     p.steps = m.steps;
     p.units = m.units;
+    p.nrb = m.rows / kRowBlock;
     return p;
 }
 
@@ -386,32 +387,35 @@ __device__ inline void mm_steps(const Planes &W, int rb, int s0, int s1, int lan
         }
         return;
     }
-    // Loads are unconditional -- past the last step they repeat it, an L2 hit -- so
-    // every trip through the loop issues the same loads in the same order and the
-    // compiler's wait counts stay exact (a skipped load would make them
-    // conservative at the loop head and serialise the prefetch).
-    const int sl = s1 - 1;
+    // Loads are unconditional, so every trip through the loop issues the same loads
+    // in the same order and the compiler's wait counts stay exact (a skipped load
+    // would make them conservative at the loop head and serialise the prefetch).
+    // Past the wavefront's last step, weight loads go to step `so`, whose offsets
+    // land exactly at the end of the matrix's planes: out of range, so they read 0
+    // without touching memory.  Activation loads repeat the last step (L2 hits).
+    const int sl = s1 - 1, so = (W.nrb - rb) * W.steps;
+    auto ws = [&](int x) { return x < s1 ? x : so; };
     typename D::Raw w0, w1, w2;
     typename D::State st;
     AStep x0, x1, x2;
     load_a(x0, A, s0);
     D::load(w0, W, rb, s0, lane);
-    D::load(w1, W, rb, min(s0 + 1, sl), lane);
+    D::load(w1, W, rb, ws(s0 + 1), lane);
     // sched_barrier keeps the scheduler from sinking the prefetches down to their
     // uses (which it does to shorten live ranges, undoing the pipelining).
     for (int s = s0; s < s1; s += 3) {
         load_a(x1, A, min(s + 1, sl));
-        D::load(w2, W, rb, min(s + 2, sl), lane);
+        D::load(w2, W, rb, ws(s + 2), lane);
         __builtin_amdgcn_sched_barrier(0);
         mm_step<D>(w0, st, x0, s, lane, acc);
         if (s + 1 >= s1) break;
         load_a(x2, A, min(s + 2, sl));
-        D::load(w0, W, rb, min(s + 3, sl), lane);
+        D::load(w0, W, rb, ws(s + 3), lane);
         __builtin_amdgcn_sched_barrier(0);
         mm_step<D>(w1, st, x1, s + 1, lane, acc);
         if (s + 2 >= s1) break;
         load_a(x0, A, min(s + 3, sl));
-        D::load(w1, W, rb, min(s + 4, sl), lane);
+        D::load(w1, W, rb, ws(s + 4), lane);
         __builtin_amdgcn_sched_barrier(0);
         mm_step<D>(w2, st, x2, s + 2, lane, acc);
     }

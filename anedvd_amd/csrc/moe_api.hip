@@ -114,6 +114,11 @@ int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, si
     m.s_stride = (size_t)rows * m.units * f.sb;
     m.h_stride = type == ANEDVD_Q6_K ? (size_t)rows * m.steps * 16 : 0;
     m.d_stride = type == ANEDVD_Q6_K ? (size_t)rows * m.units * 2 : 0;
+    // The kernels address one matrix's planes with 32-bit buffer offsets.
+    if (m.q_stride > ((size_t)1 << 30)) {
+        set_error("%s: one %d x %d matrix is %zu bytes; at most 1 GiB per expert matrix", what, rows, cols, m.q_stride);
+        return ANEDVD_E_INVALID_SHAPE;
+    }
     ANEDVD_HIP(hipMalloc(&m.q, m.q_stride * n));
     ANEDVD_HIP(hipMalloc(&m.s, m.s_stride * n));
     if (m.h_stride) ANEDVD_HIP(hipMalloc(&m.h, m.h_stride * n));

@@ -37,12 +37,12 @@ def log(msg: str):
 
 
 def gateup_bytes(spec, touched: int, T: int) -> float:
-    """Algorithmic HBM bytes of one fused dequant + gate/up launch: the touched
-    experts' gate and up weights once, the activations once, the f32 gate/up
-    results of every (token, slot) once."""
+    """Algorithmic HBM bytes of one fused dequant + gate/up launch (no K split at
+    this size): the touched experts' gate and up weights once, the f16 activations
+    once, the f16 SwiGLU output of every (token, slot) once."""
     from anedvd_amd import workloads as W
     w = touched * spec.inter * spec.hidden * (W.bytes_per_weight(spec.gate_type) + W.bytes_per_weight(spec.up_type))
-    return w + T * spec.hidden * 4 + T * spec.k * 2 * spec.inter * 4
+    return w + T * spec.hidden * 2 + T * spec.k * spec.inter * 2
 
 
 def read_traffic(name: str):
@@ -84,6 +84,9 @@ def main():
     ap.add_argument("--copies", type=int, default=8, help="device copies of the layer rotated per step")
     ap.add_argument("--sweep", default="1,8,32", help="extra decode batches reported beside the headline ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first run 3 device-to-device copies of MIB MiB (a plain copy kernel of known size, "
+                         "for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -93,6 +96,17 @@ def main():
 
     from anedvd_amd import moe, synth
     from anedvd_amd import workloads as W
+
+    if args.calibrate_copy:
+        import torch
+        src = torch.ones(args.calibrate_copy << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration: 3 device copies of {args.calibrate_copy} MiB")
+        del src, dst
 
     spec = W.QWEN3_30B_A3B_Q8_0
     B = args.batch
@@ -138,10 +152,10 @@ def main():
     gu_ms = head["stage_ms"]["gate_up"]
     gu_bytes = gateup_bytes(spec, head["touched_experts"], B)
     achieved = gu_bytes / (gu_ms / 1e3) / 1e9
-    roofline = {"bound": "hbm", "kernel": "k_gateup<DecQ8_0> (fused Q8_0 dequant + gate/up GEMV)",
+    roofline = {"bound": "hbm", "kernel": "k_mm_gateup<MQ8_0> (fused Q8_0 dequant + gate/up + SwiGLU on MFMA)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": read_traffic("pmc_k_gateup_q8_0_decode_b64.md"),
+                "traffic": read_traffic("pmc_k_mm_gateup_q8_0_decode_b64.md"),
                 "bytes_per_launch": gu_bytes, "avg_launch_ms": gu_ms}
 
     cpu = None
