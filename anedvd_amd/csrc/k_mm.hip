@@ -30,6 +30,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "mma.h"
 
 namespace anedvd {
 
@@ -42,68 +43,6 @@ constexpr int kWaves = 4;
 #else
 #define MM_ATTR
 #endif
-constexpr int kMTile = 16;  // tokens per MFMA pass
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
-
-__device__ inline f32x4 mfma(half8 a, half8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-
-// Bytes (b0, b1) and (b2, b3) of `b` under the f16 exponent byte 0x64: the pairs
-// (1024 + b0, 1024 + b1) and (1024 + b2, 1024 + b3), exact.
-__device__ inline uint32_t pair01(uint32_t b) { return __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u); }
-__device__ inline uint32_t pair23(uint32_t b) { return __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u); }
-
-// 1024 + each byte of lo then hi, as 8 halves in byte order.
-__device__ inline half8 bytes_h8(uint32_t lo, uint32_t hi)
-{
-    const u32x4 w = {pair01(lo), pair23(lo), pair01(hi), pair23(hi)};
-    half8 h;
-    __builtin_memcpy(&h, &w, 16);
-    return h;
-}
-
-__device__ inline uint32_t pick4(u32x4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
-
-// Raw buffer loads: a wave-uniform descriptor (base, size), a per-lane byte offset
-// that stays fixed while a wavefront streams, and a scalar per-step offset -- no
-// per-step 64-bit address arithmetic, and loads outside the buffer return 0.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
-constexpr int kNT = 2;                  // non-temporal: weights are streamed once
-
-__device__ inline rsrc_t make_rsrc(const void *p, size_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, kRsrcWord3);
-}
-
-// The planes of one matrix (expert) of a QMat.
-struct Planes {
-    rsrc_t q, s, h, d;
-    int steps, units, nrb;  // nrb: row blocks of the matrix
-};
-
-__device__ inline Planes planes(const QMat &m, int mat)
-{
-    Planes p;
-    p.q = make_rsrc(m.q + (size_t)mat * m.q_stride, m.q_stride);
-    p.s = make_rsrc(m.s + (size_t)mat * m.s_stride, m.s_stride);
-    p.h = make_rsrc(m.h ? m.h + (size_t)mat * m.h_stride : m.q, m.h_stride);
-    p.d = make_rsrc(m.d ? m.d + (size_t)mat * m.d_stride : m.q, m.d_stride);
-    p.steps = m.steps;
-    p.units = m.units;
-    p.nrb = m.rows / kRowBlock;
-    return p;
-}
-
-// Byte offset of (row block rb, step s) in a per-lane plane of `bytes` per lane,
-// and of (rb, unit u) in a per-row plane of `bytes` per row (tile layout).
-__device__ inline int lane_plane_off(const Planes &p, int rb, int s, int bytes) { return (rb * p.steps + s) * 256 * bytes; }
-__device__ inline int row_plane_off(const Planes &p, int rb, int u, int bytes) { return (rb * p.units + u) * 64 * bytes; }
 
 // ------------------------------------------------------------------ decoders
 //
@@ -166,26 +105,6 @@ struct MQ4_0 {
         mn = 0.0f;
     }
 };
-
-// getScaleMinK4 (gguf.zig:948-958) over the 12 scale bytes held in 3 dwords, j at
-// run time.
-__device__ inline int scale_byte(uint32_t s1, uint32_t s2, uint32_t s3, int i)
-{
-    const uint32_t w = i < 4 ? s1 : i < 8 ? s2 : s3;
-    return (int)((w >> (8 * (i & 3))) & 0xFFu);
-}
-
-__device__ inline void scale_min_k4(int j, uint32_t s1, uint32_t s2, uint32_t s3, int &d, int &m)
-{
-    if (j < 4) {
-        d = scale_byte(s1, s2, s3, j) & 63;
-        m = scale_byte(s1, s2, s3, j + 4) & 63;
-    } else {
-        const int b = scale_byte(s1, s2, s3, j + 4);
-        d = (b & 0xF) | ((scale_byte(s1, s2, s3, j - 4) >> 6) << 4);
-        m = (b >> 4) | ((scale_byte(s1, s2, s3, j) >> 6) << 4);
-    }
-}
 
 // Q4_K: step s covers sub-blocks 2 (s % 4) + j; y = d1 n - m1 with d1 = d * sc,
 // m1 = dmin * m.
@@ -291,51 +210,72 @@ struct MQ6_K {
 };
 
 // ------------------------------------------------------------------ core
+//
+// A wavefront computes 64 weight rows (four 16-row tiles) against MT tiles of 16
+// tokens: acc[mt][t][i] = sum_k W[64 rb + 16 t + l % 16][k] * x[token 4 (l / 16) + i
+// of tile mt][k], lane l.  Each step's weights are decoded once and used by all MT
+// token tiles, so a 64-token chunk (MT = 4) reads and decodes the weights a quarter
+// as often as four 16-token passes.
+//
+// Activation descales come in two forms:
+//   kRow  one power of two per token row (the layer input x): the MFMA results
+//         accumulate with the weight scale only, and the row's descale is
+//         applied once after the K loop;
+//   kStep one per (row, 64-column group) (the SwiGLU activations, written group
+//         by group): each step's descales of the lane's four result tokens --
+//         consecutive positions -- come in with one 16-byte load per token tile.
+enum DsMode { kRow, kStepDs };
 
-// The activations of one step: lane group g's 16 values of its token row, and the
-// descales of the lane's four result tokens.
+template <int MT, int MODE>
 struct AStep {
-    half8 a0, a1;
-    float dv[4];
+    half8 a0[MT], a1[MT];
+    f32x4 dv[MODE == kStepDs ? MT : 1];
 };
 
-// Where a lane's activations come from: its token row's byte offset (plus its lane
-// group's 32 bytes) in the f16 values, and its four result tokens' byte offsets in
-// one group's descales (ld4 bytes per group).
+// Where a lane's activations come from: its A row's byte offset (token l % 16 of
+// tile mt, plus lane group g's 32 bytes) in the f16 values and, for kStepDs, the
+// byte offset of its first result token's descale within a group (ld4 bytes per
+// group).
+template <int MT>
 struct AOp {
     rsrc_t q, ds;
-    int qoff;
-    int doff[4];
+    int qoff[MT];
+    int doff[MT];
     int ld4;
 };
 
-__device__ inline half8 as_h8(u32x4 v)
+template <int MT, int MODE>
+__device__ inline void load_a(AStep<MT, MODE> &x, const AOp<MT> &a, int s)
 {
-    half8 h;
-    __builtin_memcpy(&h, &v, 16);
-    return h;
-}
-
-__device__ inline void load_a(AStep &x, const AOp &a, int s)
-{
-    x.a0 = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff, s * 2 * kStep, 0));
-    x.a1 = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff + 16, s * 2 * kStep, 0));
 #pragma unroll
-    for (int i = 0; i < 4; i++) x.dv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(a.ds, a.doff[i], s * a.ld4, 0));
+    for (int mt = 0; mt < MT; mt++) {
+        x.a0[mt] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff[mt], s * 2 * kStep, 0));
+        x.a1[mt] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff[mt] + 16, s * 2 * kStep, 0));
+    }
+    if (MODE == kStepDs) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(a.ds, a.doff[mt], s * a.ld4, 0);
+            __builtin_memcpy(&x.dv[mt], &v, 16);
+        }
+    }
 }
 
-// acc[t][i] += the step's contribution (see mm_steps).
-template <class D>
-__device__ inline void mm_step(const typename D::Raw &w, typename D::State &st, const AStep &x, int s, int lane,
-                               f32x4 *acc)
+// acc[mt][t][i] += the step's contribution.
+template <class D, int MT, int MODE>
+__device__ inline void mm_step(const typename D::Raw &w, typename D::State &st, const AStep<MT, MODE> &x, int s,
+                               int lane, f32x4 (*acc)[4])
 {
     const half8 ones = (half8)(half_t)1.0f;
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     D::begin(w, st, s);
-    f32x4 sum0 = zero, sum1 = zero;
+    f32x4 sum[MT][2];
     if (D::kMin) {
-        sum0 = mfma(x.a0, ones, zero);
-        sum1 = mfma(x.a1, ones, zero);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            sum[mt][0] = mfma(x.a0[mt], ones, zero);
+            sum[mt][1] = mfma(x.a1[mt], ones, zero);
+        }
     }
 #pragma unroll
     for (int t = 0; t < 4; t++) {
@@ -344,91 +284,89 @@ __device__ inline void mm_step(const typename D::Raw &w, typename D::State &st, 
             half8 b;
             float d, mn;
             D::operand(w, st, s, lane, t, j, b, d, mn);
-            const f32x4 r = mfma(j ? x.a1 : x.a0, b, zero);
-            const f32x4 sm = j ? sum1 : sum0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float v = D::kMin ? d * r[i] - mn * sm[i] : d * r[i];
-                acc[t][i] += x.dv[i] * v;
+            for (int mt = 0; mt < MT; mt++) {
+                const f32x4 r = mfma(j ? x.a1[mt] : x.a0[mt], b, zero);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (MODE == kRow) {
+                        acc[mt][t][i] = __builtin_fmaf(d, r[i], acc[mt][t][i]);
+                        if (D::kMin) acc[mt][t][i] = __builtin_fmaf(-mn, sum[mt][j][i], acc[mt][t][i]);
+                    } else {
+                        const float v = D::kMin ? d * r[i] - mn * sum[mt][j][i] : d * r[i];
+                        acc[mt][t][i] = __builtin_fmaf(x.dv[mt][i], v, acc[mt][t][i]);
+                    }
+                }
             }
         }
     }
 }
 
-// Streams steps [s0, s1) of the wavefront's four tiles (row block rb of matrix
-// `mat`) against 16 tokens: lane l feeds A rows from `arow` (its token l % 16, the
-// row's column 0) and accumulates acc[t][i] = sum_k W[64 rb + 16 t + l % 16][k] *
-// x[token 4 (l / 16) + i][k], the tokens' descales taken from ds[step * ld +
-// dsrow[i]].  Weights are loaded two steps ahead of the MFMAs that use them (three
-// register buffers in rotation) and activations one step ahead, issued before the
-// weights so that waiting for them never waits for the later weight loads.
-template <class D>
-__device__ inline void mm_steps(const Planes &W, int rb, int s0, int s1, int lane, const AOp &A, f32x4 *acc)
+// Streams steps [s0, s1) of the wavefront's four tiles (row block rb of the
+// matrix whose planes are W).
+//
+// MT = 1 with a two-step-ahead decoder (Q8_0, Q4_0): weights are loaded two steps
+// ahead of the MFMAs that use them (three register buffers in rotation) and
+// activations one step ahead, issued before the weights so that waiting for them
+// never waits for the later weight loads.  Otherwise (more token tiles, or the
+// super-block formats, which carry more state per buffer) everything is loaded
+// one step ahead.
+//
+// Loads are unconditional, so every trip through the loop issues the same loads
+// in the same order and the compiler's wait counts stay exact (a skipped load would
+// make them conservative at the loop head and serialise the prefetch).  Past the
+// wavefront's last step, weight loads go to step `so`, whose offsets land exactly
+// at the end of the matrix's planes: out of range, so they read 0 without touching
+// memory.  Activation loads repeat the last step (L2 hits).  sched_barrier keeps
+// the scheduler from sinking the prefetches down to their uses.
+template <class D, int MT, int MODE>
+__device__ inline void mm_steps(const Planes &W, int rb, int s0, int s1, int lane, const AOp<MT> &A,
+                                f32x4 (*acc)[4])
 {
     if (s0 >= s1) return;
-    if (!D::kDeep) {  // one step ahead: the super-block formats carry more state per buffer
+    const int sl = s1 - 1, so = (W.nrb - rb) * W.steps;
+    auto ws = [&](int x) { return x < s1 ? x : so; };
+    typename D::State st;
+    if (!D::kDeep || MT > 1) {
         typename D::Raw w0, w1;
-        typename D::State st;
-        AStep x0, x1;
+        AStep<MT, MODE> x0, x1;
         load_a(x0, A, s0);
         D::load(w0, W, rb, s0, lane);
         for (int s = s0; s < s1; s += 2) {
-            if (s + 1 < s1) {
-                load_a(x1, A, s + 1);
-                D::load(w1, W, rb, s + 1, lane);
-            }
-            mm_step<D>(w0, st, x0, s, lane, acc);
+            load_a(x1, A, min(s + 1, sl));
+            D::load(w1, W, rb, ws(s + 1), lane);
+            __builtin_amdgcn_sched_barrier(0);
+            mm_step<D, MT, MODE>(w0, st, x0, s, lane, acc);
             if (s + 1 >= s1) break;
-            if (s + 2 < s1) {
-                load_a(x0, A, s + 2);
-                D::load(w0, W, rb, s + 2, lane);
-            }
-            mm_step<D>(w1, st, x1, s + 1, lane, acc);
+            load_a(x0, A, min(s + 2, sl));
+            D::load(w0, W, rb, ws(s + 2), lane);
+            __builtin_amdgcn_sched_barrier(0);
+            mm_step<D, MT, MODE>(w1, st, x1, s + 1, lane, acc);
         }
         return;
     }
-    // Loads are unconditional, so every trip through the loop issues the same loads
-    // in the same order and the compiler's wait counts stay exact (a skipped load
-    // would make them conservative at the loop head and serialise the prefetch).
-    // Past the wavefront's last step, weight loads go to step `so`, whose offsets
-    // land exactly at the end of the matrix's planes: out of range, so they read 0
-    // without touching memory.  Activation loads repeat the last step (L2 hits).
-    const int sl = s1 - 1, so = (W.nrb - rb) * W.steps;
-    auto ws = [&](int x) { return x < s1 ? x : so; };
     typename D::Raw w0, w1, w2;
-    typename D::State st;
-    AStep x0, x1, x2;
+    AStep<MT, MODE> x0, x1, x2;
     load_a(x0, A, s0);
     D::load(w0, W, rb, s0, lane);
     D::load(w1, W, rb, ws(s0 + 1), lane);
-    // sched_barrier keeps the scheduler from sinking the prefetches down to their
-    // uses (which it does to shorten live ranges, undoing the pipelining).
     for (int s = s0; s < s1; s += 3) {
         load_a(x1, A, min(s + 1, sl));
         D::load(w2, W, rb, ws(s + 2), lane);
         __builtin_amdgcn_sched_barrier(0);
-        mm_step<D>(w0, st, x0, s, lane, acc);
+        mm_step<D, MT, MODE>(w0, st, x0, s, lane, acc);
         if (s + 1 >= s1) break;
         load_a(x2, A, min(s + 2, sl));
         D::load(w0, W, rb, ws(s + 3), lane);
         __builtin_amdgcn_sched_barrier(0);
-        mm_step<D>(w1, st, x1, s + 1, lane, acc);
+        mm_step<D, MT, MODE>(w1, st, x1, s + 1, lane, acc);
         if (s + 2 >= s1) break;
         load_a(x0, A, min(s + 3, sl));
         D::load(w1, W, rb, ws(s + 4), lane);
         __builtin_amdgcn_sched_barrier(0);
-        mm_step<D>(w2, st, x2, s + 2, lane, acc);
+        mm_step<D, MT, MODE>(w2, st, x2, s + 2, lane, acc);
     }
 }
-
-__device__ inline float gelu_tanh(float x)
-{
-    const float c = 0.7978845608028654f;
-    return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
-}
-
-// moeExpertAccumF32's activation: g / (1 + exp(-g)) (cpu.zig:434-437), or gelu.
-__device__ inline float gate_act(float g, int use_gelu) { return use_gelu ? gelu_tanh(g) : g / (1.0f + __expf(-g)); }
 
 struct MmArgs {
     QMat w0, w1;     // gate and up (gate/up), or down (w0)
@@ -438,22 +376,35 @@ struct MmArgs {
     ActQ act;        // gate/up output [P][I]
     float *ypart;    // down output [KS][P][H]
     int H, I, KS, P, use_gelu;
+    int nchunk;      // chunk rows of the grid: blockIdx.x = chunk + nchunk * (row block, K share)
 };
+
+// The token chunk `ci` of the dispatch's list: expert e, first position p0 and nt
+// (1..16 MT) tokens; false past the end of the list.
+template <int MT>
+__device__ inline bool chunk_of(const Dispatch &d, int ci, int &e, int &p0, int &nt)
+{
+    if (ci >= d.meta[3]) return false;
+    const int c = d.chunks[ci];
+    e = c >> 16;
+    p0 = d.offsets[e] + (c & 0xFFFF) * 16 * MT;
+    nt = min(16 * MT, d.offsets[e + 1] - p0);
+    return true;
+}
 
 // ------------------------------------------------------------ gate / up
 
-// Grid (I/64 * KS, max_u), 256 threads.  Wave w: matrix w >> 1 (gate, up), half
-// w & 1 of the workgroup's K units; the four are summed through LDS and wave 0
-// applies SiLU(g) * u to its 64 rows x 16 tokens.
-template <class D>
+// Grid nchunk * I/64 * KS workgroups of 256 threads; one per (token chunk of 16 MT,
+// 64-row block, K share), chunks fastest.  Wave w: matrix w >> 1 (gate, up), half w & 1 of
+// the workgroup's K units; the four are summed through LDS and wave 0 applies
+// SiLU(g) * u to its 64 rows x 16 MT tokens.
+template <class D, int MT>
 __global__ __launch_bounds__(256) MM_ATTR void k_mm_gateup(MmArgs a)
 {
-    __shared__ f32x4 xch[3][4][64];
-    const int ua = blockIdx.y;
-    if (ua >= a.d.meta[0]) return;  // uniform over the workgroup
-    const int e = a.d.active[ua];
-    const int p0 = a.d.offsets[e], ne = a.d.offsets[e + 1] - p0;
-    const int rb = blockIdx.x / a.KS, ks = blockIdx.x % a.KS;
+    __shared__ f32x4 xch[3][MT][4][64];
+    int e, p0, nt;
+    if (!chunk_of<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;  // uniform over the workgroup
+    const int rbk = (int)(blockIdx.x / a.nchunk), rb = rbk / a.KS, ks = rbk % a.KS;
     const int units = a.H / kStep / D::kSpu, upw = units / a.KS, u0 = ks * upw;
     const int wv = wave_id(), lane = threadIdx.x & 63;
     const int mat = wv >> 1, half = wv & 1;
@@ -461,72 +412,84 @@ __global__ __launch_bounds__(256) MM_ATTR void k_mm_gateup(MmArgs a)
     const int ub = u0 + half * hu, ue = min(u0 + upw, ub + hu);
     const Planes W = planes(mat ? a.w1 : a.w0, e);
     const int n = lane & 15, gq = lane >> 4;
-    AOp A;
+    AOp<MT> A;
     A.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);  // x: ld = tokens
     A.ds = make_rsrc(a.x.ds, (size_t)(a.H / kStep) * a.x.ld * 4);
     A.ld4 = a.x.ld * 4;
-
-    for (int c0 = 0; c0 < ne; c0 += kMTile) {
-        const int nt = min(kMTile, ne - c0);
-        A.qoff = a.d.rows[p0 + c0 + min(n, nt - 1)] * a.H * 2 + 32 * gq;
+    float dvr[MT][4];  // x's per-row descales of the lane's result tokens
 #pragma unroll
-        for (int i = 0; i < 4; i++) A.doff[i] = a.d.rows[p0 + c0 + min(4 * gq + i, nt - 1)] * 4;
-        f32x4 acc[4];
+    for (int mt = 0; mt < MT; mt++) {
+        A.qoff[mt] = a.d.rows[p0 + min(16 * mt + n, nt - 1)] * a.H * 2 + 32 * gq;
+        A.doff[mt] = 0;
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        mm_steps<D>(W, rb, ub * D::kSpu, ue * D::kSpu, lane, A, acc);
-        if (wv) {
+        for (int i = 0; i < 4; i++) dvr[mt][i] = a.x.ds[a.d.rows[p0 + min(16 * mt + 4 * gq + i, nt - 1)]];
+    }
+    f32x4 acc[MT][4];
 #pragma unroll
-            for (int t = 0; t < 4; t++) xch[wv - 1][t][lane] = acc[t];
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[mt][t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    mm_steps<D, MT, kRow>(W, rb, ub * D::kSpu, ue * D::kSpu, lane, A, acc);
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[mt][t][i] *= dvr[mt][i];
+    if (wv) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) xch[wv - 1][mt][t][lane] = acc[mt][t];
+    }
+    __syncthreads();
+    if (wv) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        f32x4 gs[4], us[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            gs[t] = acc[mt][t] + xch[0][mt][t][lane];
+            us[t] = xch[1][mt][t][lane] + xch[2][mt][t][lane];
         }
-        __syncthreads();
-        if (wv == 0) {
-            f32x4 gs[4], us[4];
+        if (a.KS == 1) {
+            // SiLU(g) * u, quantised per token over these 64 rows (one 64-column
+            // group of the down input): the 16 lanes of a DPP row hold them.
+            f32x4 v[4];
+            float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                gs[t] = acc[t] + xch[0][t][lane];
-                us[t] = xch[1][t][lane] + xch[2][t][lane];
-            }
-            if (a.KS == 1) {
-                // SiLU(g) * u, quantised per token over these 64 rows (one 64-column
-                // group of the down input): the 16 lanes of a DPP row hold them.
-                f32x4 v[4];
-                float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        v[t][i] = gate_act(gs[t][i], a.use_gelu) * us[t][i];
-                        mx[i] = fmaxf(mx[i], fabsf(v[t][i]));
-                    }
+            for (int t = 0; t < 4; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int m = 4 * gq + i;
-                    const float sc = pow2_scale(row_max_f32(mx[i]));
-                    if (m < nt) {
-                        const size_t pos = (size_t)p0 + c0 + m;
-                        half_t *dst = a.act.q + pos * a.I + (size_t)kStep * rb;
-#pragma unroll
-                        for (int t = 0; t < 4; t++) dst[mma_pos(16 * t + n)] = (half_t)(v[t][i] * sc);
-                        if (n == 0) a.act.ds[(size_t)rb * a.act.ld + pos] = 1.0f / sc;
-                    }
+                    v[t][i] = gate_act(gs[t][i], a.use_gelu) * us[t][i];
+                    mx[i] = fmaxf(mx[i], fabsf(v[t][i]));
                 }
-            } else {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int m = 4 * gq + i;
-                    if (m < nt) {
-                        float *pp = a.part + (((size_t)ks * a.P + p0 + c0 + m) * 2) * a.I + (size_t)kStep * rb + n;
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * mt + 4 * gq + i;
+                const float sc = pow2_scale(row_max_f32(mx[i]));
+                if (m < nt) {
+                    const size_t pos = (size_t)p0 + m;
+                    half_t *dst = a.act.q + pos * a.I + (size_t)kStep * rb;
 #pragma unroll
-                        for (int t = 0; t < 4; t++) {
-                            pp[16 * t] = gs[t][i];
-                            pp[a.I + 16 * t] = us[t][i];
-                        }
+                    for (int t = 0; t < 4; t++) dst[mma_pos(16 * t + n)] = (half_t)(v[t][i] * sc);
+                    if (n == 0) a.act.ds[(size_t)rb * a.act.ld + pos] = 1.0f / sc;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * mt + 4 * gq + i;
+                if (m < nt) {
+                    float *pp = a.part + (((size_t)ks * a.P + p0 + m) * 2) * a.I + (size_t)kStep * rb + n;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        pp[16 * t] = gs[t][i];
+                        pp[a.I + 16 * t] = us[t][i];
                     }
                 }
             }
         }
-        __syncthreads();
     }
 }
 
@@ -551,45 +514,49 @@ __global__ __launch_bounds__(256) void k_act_reduce(MmArgs a)
 
 // ---------------------------------------------------------------- down
 
-// Grid (ceil(H/256) * KS, max_u), 256 threads; wave w owns row block 4 x + w of
-// the output and the workgroup's K units.
-template <class D>
+// Grid nchunk * ceil(H/256) * KS workgroups of 256 threads, chunks fastest; wave w
+// owns row block 4 x + w of the output (x the workgroup's row-block group), the
+// workgroup's K units and token chunk.  The chunk's positions
+// are consecutive, so tokens past the group's end read other groups' (or, past
+// the last position, out-of-range zero) activations and are not stored.
+template <class D, int MT>
 __global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
 {
-    const int ua = blockIdx.y;
-    if (ua >= a.d.meta[0]) return;
-    const int e = a.d.active[ua];
-    const int p0 = a.d.offsets[e], ne = a.d.offsets[e + 1] - p0;
+    int e, p0, nt;
+    if (!chunk_of<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;
     const int wv = wave_id(), lane = threadIdx.x & 63;
-    const int rb = kWaves * (blockIdx.x / a.KS) + wv, ks = blockIdx.x % a.KS;
+    const int rbk = (int)(blockIdx.x / a.nchunk);
+    const int rb = kWaves * (rbk / a.KS) + wv, ks = rbk % a.KS;
     if (rb >= a.H / kRowBlock) return;  // no barriers in this kernel
     const int units = a.I / kStep / D::kSpu, upw = units / a.KS, u0 = ks * upw;
     const int n = lane & 15, gq = lane >> 4;
     const Planes W = planes(a.w0, e);
-    AOp A;
+    AOp<MT> A;
     A.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
     A.ds = make_rsrc(a.x.ds, (size_t)(a.I / kStep) * a.x.ld * 4);
     A.ld4 = a.x.ld * 4;
-
-    for (int c0 = 0; c0 < ne; c0 += kMTile) {
-        const int nt = min(kMTile, ne - c0);
-        A.qoff = (p0 + c0 + min(n, nt - 1)) * a.I * 2 + 32 * gq;
 #pragma unroll
-        for (int i = 0; i < 4; i++) A.doff[i] = (p0 + c0 + min(4 * gq + i, nt - 1)) * 4;
-        f32x4 acc[4];
+    for (int mt = 0; mt < MT; mt++) {
+        A.qoff[mt] = (p0 + 16 * mt + n) * a.I * 2 + 32 * gq;
+        A.doff[mt] = (p0 + 16 * mt + 4 * gq) * 4;
+    }
+    f32x4 acc[MT][4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        mm_steps<D>(W, rb, u0 * D::kSpu, (u0 + upw) * D::kSpu, lane, A, acc);
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[mt][t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    mm_steps<D, MT, kStepDs>(W, rb, u0 * D::kSpu, (u0 + upw) * D::kSpu, lane, A, acc);
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int m = 4 * gq + i;
+            const int m = 16 * mt + 4 * gq + i;
             if (m < nt) {
-                float *yp = a.ypart + ((size_t)ks * a.P + p0 + c0 + m) * a.H + (size_t)kRowBlock * rb + n;
+                float *yp = a.ypart + ((size_t)ks * a.P + p0 + m) * a.H + (size_t)kRowBlock * rb + n;
 #pragma unroll
-                for (int t = 0; t < 4; t++) yp[16 * t] = acc[t][i];
+                for (int t = 0; t < 4; t++) yp[16 * t] = acc[mt][t][i];
             }
         }
-    }
 }
 
 // ------------------------------------------------------------- combine
@@ -663,6 +630,59 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart
     }
 }
 
+// Large calls: one thread per (token, 4 columns), slots in order, eight slots'
+// loads issued together (indices clamped rather than branched on).  Grid: T * H/4
+// threads.
+__global__ __launch_bounds__(256) void k_combine_rows(const float *__restrict__ ypart, const int32_t *__restrict__ inv,
+                                                      const float *__restrict__ probs, int T, int k, int H, int KS,
+                                                      int P, const float *__restrict__ shared,
+                                                      const float *__restrict__ shared_scale, int sKS,
+                                                      float *__restrict__ out)
+{
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int H4 = H / 4;
+    if (id >= (size_t)T * H4) return;
+    const int t = (int)(id / H4), h = (int)(id % H4) * 4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < k; s0 += 8) {
+        int pos[8];
+        float p[8];
+        bool ok[8];
+        float4 y[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int s = min(s0 + i, k - 1);
+            pos[i] = inv[(size_t)t * k + s];
+            p[i] = probs[(size_t)t * k + s];
+            ok[i] = s0 + i < k && pos[i] >= 0;
+            pos[i] = max(pos[i], 0);
+            y[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        for (int q = 0; q < KS; q++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 z = *(const float4 *)(ypart + ((size_t)q * P + pos[i]) * H + h);
+                y[i].x += z.x; y[i].y += z.y; y[i].z += z.z; y[i].w += z.w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (ok[i]) {
+                acc.x += p[i] * y[i].x; acc.y += p[i] * y[i].y; acc.z += p[i] * y[i].z; acc.w += p[i] * y[i].w;
+            }
+    }
+    if (shared) {
+        const float sc = shared_scale ? shared_scale[t] : 1.0f;
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < sKS; q++) {
+            const float4 z = *(const float4 *)(shared + ((size_t)q * T + t) * H + h);
+            y.x += z.x; y.y += z.y; y.z += z.z; y.w += z.w;
+        }
+        acc.x += sc * y.x; acc.y += sc * y.y; acc.z += sc * y.z; acc.w += sc * y.w;
+    }
+    *(float4 *)(out + (size_t)t * H + h) = acc;
+}
+
 // ------------------------------------------------------------- planning
 
 static int steps_per_unit(int type) { return tile_fmt(type).spu; }
@@ -686,9 +706,18 @@ static int choose_ks(int units, int spu, long wg_per_ks, int waves_per_k, int mi
     return best;
 }
 
-MmPlan plan_mm(int gate_type, int down_type, int H, int I, int max_u)
+MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u)
 {
     MmPlan p{};
+    // The grouped GEMM (64-token chunks) once the groups average 32 tokens; the
+    // chunks then give the grid its parallelism and K is not split.
+    p.mt = (P >= 32 * max_u && grouped_supported(H, I)) ? 4 : 1;
+    p.chunk = 16 * p.mt;
+    p.nchunk = P / p.chunk + max_u;
+    if (p.mt > 1) {
+        p.ks_gu = p.ks_dn = 1;
+        return p;
+    }
     p.ks_gu = choose_ks(H / kStep / steps_per_unit(gate_type), steps_per_unit(gate_type), (long)max_u * (I / kRowBlock),
                         2, 2);
     p.ks_dn = choose_ks(I / kStep / steps_per_unit(down_type), steps_per_unit(down_type),
@@ -701,26 +730,40 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int max_u)
 
 // ------------------------------------------------------------- launchers
 
-template <class D>
-static int launch_gateup_t(const MmArgs &a, int max_u, hipStream_t st)
+template <class D, int MT>
+static int launch_gateup_t(const MmArgs &a, hipStream_t st)
 {
-    hipLaunchKernelGGL(k_mm_gateup<D>, dim3(a.I / kRowBlock * a.KS, max_u), dim3(256), 0, st, a);
+    const size_t wgs = (size_t)a.nchunk * (a.I / kRowBlock) * a.KS;
+    hipLaunchKernelGGL((k_mm_gateup<D, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
+template <class D, int MT>
+static int launch_down_t(const MmArgs &a, hipStream_t st)
+{
+    const size_t wgs = (size_t)a.nchunk * ((a.H / kRowBlock + kWaves - 1) / kWaves) * a.KS;
+    hipLaunchKernelGGL((k_mm_down<D, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }
 
 template <class D>
-static int launch_down_t(const MmArgs &a, int max_u, hipStream_t st)
+static int launch_gateup_d(const MmArgs &a, int, hipStream_t st)
 {
-    const int rbb = (a.H / kRowBlock + kWaves - 1) / kWaves;
-    hipLaunchKernelGGL(k_mm_down<D>, dim3(rbb * a.KS, max_u), dim3(256), 0, st, a);
-    ANEDVD_HIP(hipGetLastError());
-    return ANEDVD_OK;
+    return launch_gateup_t<D, 1>(a, st);
+}
+
+template <class D>
+static int launch_down_d(const MmArgs &a, int, hipStream_t st)
+{
+    return launch_down_t<D, 1>(a, st);
 }
 
 int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
-                         int max_u, const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st)
+                         const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st)
 {
+    if (plan.mt > 1) return launch_grouped_gateup(gate, up, x, H, I, d, P, plan.mt, plan.nchunk, act, use_gelu, st);
     if (gate.type != up.type) {
         set_error("expert gate/up: gate type %d and up type %d differ", gate.type, up.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
@@ -737,12 +780,13 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
     a.KS = plan.ks_gu;
     a.P = P;
     a.use_gelu = use_gelu;
+    a.nchunk = plan.nchunk;
     int rc;
     switch (gate.type) {
-    case ANEDVD_Q8_0: rc = launch_gateup_t<MQ8_0>(a, max_u, st); break;
-    case ANEDVD_Q4_0: rc = launch_gateup_t<MQ4_0>(a, max_u, st); break;
-    case ANEDVD_Q4_K: rc = launch_gateup_t<MQ4_K>(a, max_u, st); break;
-    case ANEDVD_Q6_K: rc = launch_gateup_t<MQ6_K>(a, max_u, st); break;
+    case ANEDVD_Q8_0: rc = launch_gateup_d<MQ8_0>(a, plan.mt, st); break;
+    case ANEDVD_Q4_0: rc = launch_gateup_d<MQ4_0>(a, plan.mt, st); break;
+    case ANEDVD_Q4_K: rc = launch_gateup_d<MQ4_K>(a, plan.mt, st); break;
+    case ANEDVD_Q6_K: rc = launch_gateup_d<MQ6_K>(a, plan.mt, st); break;
     default:
         set_error("expert gate/up: ggml type %d has no kernel", gate.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
@@ -754,9 +798,10 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
     return ANEDVD_OK;
 }
 
-int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int max_u,
+int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P,
                        const MmPlan &plan, float *ypart, hipStream_t st)
 {
+    if (plan.mt > 1) return launch_grouped_down(down, act, H, I, d, P, plan.mt, plan.nchunk, ypart, st);
     MmArgs a{};
     a.w0 = down;
     a.x = act;
@@ -766,11 +811,12 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
     a.I = I;
     a.KS = plan.ks_dn;
     a.P = P;
+    a.nchunk = plan.nchunk;
     switch (down.type) {
-    case ANEDVD_Q8_0: return launch_down_t<MQ8_0>(a, max_u, st);
-    case ANEDVD_Q4_0: return launch_down_t<MQ4_0>(a, max_u, st);
-    case ANEDVD_Q4_K: return launch_down_t<MQ4_K>(a, max_u, st);
-    case ANEDVD_Q6_K: return launch_down_t<MQ6_K>(a, max_u, st);
+    case ANEDVD_Q8_0: return launch_down_d<MQ8_0>(a, plan.mt, st);
+    case ANEDVD_Q4_0: return launch_down_d<MQ4_0>(a, plan.mt, st);
+    case ANEDVD_Q4_K: return launch_down_d<MQ4_K>(a, plan.mt, st);
+    case ANEDVD_Q6_K: return launch_down_d<MQ6_K>(a, plan.mt, st);
     default:
         set_error("expert down: ggml type %d has no kernel", down.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
@@ -785,9 +831,15 @@ int launch_combine(const float *ypart, const int32_t *inv, const float *probs, i
         set_error("combine: %d K partials, at most %d", max(KS, sKS), kMaxKS);
         return ANEDVD_E_INVALID_ARG;
     }
-    const dim3 grid((unsigned)((H / 4 + kCombCols - 1) / kCombCols), (unsigned)std::min(T, 65535));
-    hipLaunchKernelGGL(k_combine, grid, dim3(kCombLanes * kCombCols), 0, st, ypart, inv, probs, T, k, H, KS, P, shared,
-                       shared_scale, sKS, out);
+    const size_t threads = (size_t)T * (H / 4);
+    if (threads >= 65536) {  // enough (token, column) threads to fill the GPU: slots in order per thread
+        hipLaunchKernelGGL(k_combine_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, ypart, inv, probs,
+                           T, k, H, KS, P, shared, shared_scale, sKS, out);
+    } else {  // decode: spread the slots over lanes so each thread waits on one slot's loads
+        const dim3 grid((unsigned)((H / 4 + kCombCols - 1) / kCombCols), (unsigned)std::min(T, 65535));
+        hipLaunchKernelGGL(k_combine, grid, dim3(kCombLanes * kCombCols), 0, st, ypart, inv, probs, T, k, H, KS, P,
+                           shared, shared_scale, sKS, out);
+    }
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }

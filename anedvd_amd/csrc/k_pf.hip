@@ -1,0 +1,555 @@
+// k_pf.hip -- the grouped GEMM for prefill-sized expert groups.
+//
+// Same math as the decode kernels (cpu.moeExpertAccumF32, cpu.zig:416-452, over
+// the gguf.zig block formats), organised for groups of tens to hundreds of tokens:
+//   - a workgroup takes a 64-token chunk of one expert's group and 64 weight rows
+//     of both gate and up (or 128 rows of down);
+//   - the chunk's activations are staged in LDS once per 64-column step and shared
+//     by the four wavefronts;
+//   - each wavefront dequantises its two 16-row tiles once per step to f16 (Q8_0,
+//     Q4_0: d * q rounded once; Q4_K, Q6_K: the quant exact, the sub-block scale
+//     and min as f16, one rounding in the FMA) and runs them against the chunk's
+//     16-token tiles, accumulating the whole K inside the MFMA;
+//   - activations carry one power of two per row (x as converted; the SwiGLU
+//     activations are rescaled to their row's largest descale while staged), so
+//     nothing is rescaled inside the K loop.
+#include "common.h"
+#include "kernels.h"
+#include "mma.h"
+
+namespace anedvd {
+
+constexpr int kAStride = 72;  // halves per staged token row: 64 + 8 against LDS bank conflicts
+
+__device__ inline half_t h_bits(uint32_t b)
+{
+    const uint16_t u = (uint16_t)b;
+    half_t h;
+    __builtin_memcpy(&h, &u, 2);
+    return h;
+}
+
+// ------------------------------------------------------------------ decoders
+//
+// A decoder loads one step of a wavefront's two row tiles (t0, t0 + 1): load();
+// takes what stays valid for a whole scale unit on the unit's first step: begin();
+// and yields the f16 B operand of (tile tt, block j) at step `ss` of the unit:
+// bop().  Lane l = 16 g + n holds row n of the tile and the 8 columns 32 j + 8 g + i.
+
+struct FQ8_0 {
+    static constexpr int kSpu = 1;
+    struct Raw {
+        u32x4 q[2];
+        uint32_t s[2];
+    };
+    struct State {};
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int t0, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 16), so = row_plane_off(p, rb, s, 4);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane + 1024 * (t0 + tt), qo, kNT);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * (t0 + tt), so, kNT);
+        }
+    }
+    __device__ static inline void begin(const Raw &, State &, int, int) {}
+    __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int)
+    {
+        const half8 q = bytes_h8(r.q[tt][2 * j], r.q[tt][2 * j + 1]) - (half_t)1152.0f;  // exact q
+        return q * h_bits(r.s[tt] >> (16 * j));  // d * q, rounded once
+    }
+};
+
+struct FQ4_0 {
+    static constexpr int kSpu = 1;
+    struct Raw {
+        u32x2 q[2];
+        uint32_t s[2];
+    };
+    struct State {};
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int t0, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, 4);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * (t0 + tt), qo, kNT);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * (t0 + tt), so, kNT);
+        }
+    }
+    __device__ static inline void begin(const Raw &, State &, int, int) {}
+    __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int)
+    {
+        const uint32_t v = r.q[tt][j];
+        const half8 q = bytes_h8(v & 0x0F0F0F0Fu, (v >> 4) & 0x0F0F0F0Fu) - (half_t)1032.0f;  // exact n - 8
+        return q * h_bits(r.s[tt] >> (16 * j));
+    }
+};
+
+// Q4_K: y = d1 * n - m1 (gguf.zig:960-996) with d1 = d * sc and m1 = dmin * m
+// formed in f32 once per super-block and kept as f16; the nibble n is exact and
+// the f16 FMA rounds once, so a weight is within 2^-10 of its scale.
+struct FQ4_K {
+    static constexpr int kSpu = 4;
+    struct Raw {
+        u32x2 q[2];
+        u32x4 sc[2];  // d, dmin, scales: loaded on a unit's first step
+    };
+    struct State {
+        half_t d1[2][8], m1[2][8];
+    };
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int t0, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 8);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * (t0 + tt), qo, kNT);
+        if ((s & 3) == 0) {
+            const int so = row_plane_off(p, rb, s >> 2, 16);
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * (t0 + tt), so, kNT);
+        }
+    }
+    __device__ static inline void begin(const Raw &r, State &st, int ss, int)
+    {
+        if (ss) return;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const float d = f16_bits_to_f32((uint16_t)(r.sc[tt].x & 0xFFFFu));
+            const float dmin = f16_bits_to_f32((uint16_t)(r.sc[tt].x >> 16));
+#pragma unroll
+            for (int sub = 0; sub < 8; sub++) {
+                int a, m;
+                scale_min_k4(sub, r.sc[tt].y, r.sc[tt].z, r.sc[tt].w, a, m);
+                st.d1[tt][sub] = (half_t)(d * (float)a);
+                st.m1[tt][sub] = (half_t)(dmin * (float)m);
+            }
+        }
+    }
+    __device__ static inline half8 bop(const Raw &r, const State &st, int ss, int tt, int j, int)
+    {
+        const uint32_t v = r.q[tt][j];
+        const half8 nib = bytes_h8(v & 0x0F0F0F0Fu, (v >> 4) & 0x0F0F0F0Fu) - (half_t)1024.0f;  // exact n
+        return nib * st.d1[tt][2 * ss + j] - st.m1[tt][2 * ss + j];
+    }
+};
+
+// Q6_K: y = d * sc * q (gguf.zig:1036-1059) with d * sc formed in f32 once per
+// super-block and kept as f16; q - 32 is exact and the product rounds once.  The
+// lane's 8 columns of block j lie in sub-block 4 ss + 2 j + g / 2.
+struct FQ6_K {
+    static constexpr int kSpu = 4;
+    struct Raw {
+        u32x2 q[2];
+        uint32_t h[2];
+        u32x4 sc[2];    // int8 scales (a unit's first step)
+        uint16_t d[2];  // f16 d (a unit's first step)
+    };
+    struct State {
+        half_t dsc[2][8];  // [tt][2 ss + j]: d * sc of the lane's sub-block 4 ss + 2 j + g / 2
+    };
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int t0, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 4);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * (t0 + tt), qo, kNT);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane + 256 * (t0 + tt), ho, kNT);
+        }
+        if ((s & 3) == 0) {
+            const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, 2);
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++) {
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * (t0 + tt), so, kNT);
+                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * (t0 + tt), dof, kNT);
+            }
+        }
+    }
+    __device__ static inline void begin(const Raw &r, State &st, int ss, int lane)
+    {
+        if (ss) return;
+        const int hg = lane >> 5;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const float d = f16_bits_to_f32(r.d[tt]);
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int sub = 2 * k + hg;  // = 4 ss + 2 j + hg with k = 2 ss + j
+                const int sc = (int)(int8_t)((pick4(r.sc[tt], sub >> 2) >> (8 * (sub & 3))) & 0xFFu);
+                st.dsc[tt][k] = (half_t)(d * (float)sc);
+            }
+        }
+    }
+    __device__ static inline half8 bop(const Raw &r, const State &st, int ss, int tt, int j, int)
+    {
+        const uint32_t v = r.q[tt][j], hb = r.h[tt];
+        const uint32_t lo = (v & 0x0F0F0F0Fu) | (((hb >> (4 * j)) & 0x03030303u) << 4);
+        const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) | (((hb >> (4 * j + 2)) & 0x03030303u) << 4);
+        const half8 q = bytes_h8(lo, hi) - (half_t)1056.0f;  // exact q - 32
+        return q * st.dsc[tt][2 * ss + j];
+    }
+};
+
+// ------------------------------------------------------------ staging
+
+// Thread tid of a workgroup stages, per step, quarter q = tid / 64 of the step's
+// 64 columns (32 bytes) of token rows r = tid % 64 + 64 h, h < R: consecutive lanes
+// write consecutive rows, so the LDS writes of a wavefront hit distinct banks.  The
+// global loads land in a ring of NB register slots, so a step's activations can be
+// loaded several steps before they are written to LDS.
+template <int R, int NB>
+struct StageX {  // gate/up: token rows gathered through the dispatch; x has per-row descales
+    rsrc_t q;
+    int off[R];
+    u32x4 v[NB][R][2];
+    template <int B>
+    __device__ inline void load(int s)
+    {
+#pragma unroll
+        for (int h = 0; h < R; h++) {
+            v[B][h][0] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep, 0);
+            v[B][h][1] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h] + 16, s * 2 * kStep, 0);
+        }
+    }
+    template <int B>
+    __device__ inline void store(half_t *dst) const  // dst: this thread's first row, its quarter
+    {
+#pragma unroll
+        for (int h = 0; h < R; h++) {
+            *(u32x4 *)(dst + h * 64 * kAStride) = v[B][h][0];
+            *(u32x4 *)(dst + h * 64 * kAStride + 8) = v[B][h][1];
+        }
+    }
+};
+
+template <int R, int NB>
+struct StageAct {  // down: consecutive positions, rescaled from their group's descale to the row's
+    rsrc_t q, ds;
+    int off[R], doff[R], ld4;
+    float inv_ref[R];
+    u32x4 v[NB][R][2];
+    float dg[NB][R];
+    template <int B>
+    __device__ inline void load(int s)
+    {
+#pragma unroll
+        for (int h = 0; h < R; h++) {
+            v[B][h][0] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep, 0);
+            v[B][h][1] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h] + 16, s * 2 * kStep, 0);
+            dg[B][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ds, doff[h], s * ld4, 0));
+        }
+    }
+    template <int B>
+    __device__ inline void store(half_t *dst) const
+    {
+#pragma unroll
+        for (int h = 0; h < R; h++) {
+            const half_t f = (half_t)(dg[B][h] * inv_ref[h]);  // a power of two <= 1
+            *(half8 *)(dst + h * 64 * kAStride) = as_h8(v[B][h][0]) * f;
+            *(half8 *)(dst + h * 64 * kAStride + 8) = as_h8(v[B][h][1]) * f;
+        }
+    }
+};
+
+// Register slot b chosen at run time; inside the unrolled step loop b is a
+// constant and the branch folds away.
+template <class S>
+__device__ inline void stage_load(S &st, int b, int s)
+{
+    if (b == 0) st.template load<0>(s);
+    else st.template load<1>(s);
+}
+
+template <class S>
+__device__ inline void stage_store(const S &st, int b, half_t *dst)
+{
+    if (b == 0) st.template store<0>(dst);
+    else st.template store<1>(dst);
+}
+
+// ------------------------------------------------------------ main loop
+
+// Steps [0, steps) of the wavefront's tiles t0, t0 + 1 of row block rb against the
+// MT 16-token tiles staged in `abuf` (two buffers of 16 MT x kAStride halves):
+// acc[tt][mt] = sum_k W[64 rb + 16 (t0 + tt) + l % 16][k] * A[16 mt + 4 (l / 16) + i][k].
+// Weights are loaded three steps ahead (a ring of four register buffers) and the
+// next step's activations one step ahead (two register slots); every thread of the
+// workgroup takes part in the staging, so all of them reach the barriers.  Steps go
+// in unrolled blocks of four, so the rings and the LDS buffers rotate at
+// compile-time indices.  Weight loads past the last step go out of range (zero, no
+// memory traffic).
+template <class F, int MT, class S>
+__device__ inline void pf_loop(const Planes &W, int rb, int t0, int steps, int lane, S &stage, half_t *abuf,
+                               int srow, f32x4 (*acc)[MT])
+{
+    constexpr int U = 4;
+    constexpr int BUF = 16 * MT * kAStride;
+    static_assert(U % F::kSpu == 0, "a scale unit must fit an unrolled block");
+    const int n = lane & 15, g = lane >> 4;
+    const int so = (W.nrb - rb) * W.steps;
+    auto ws = [&](int x) { return x < steps ? x : so; };
+    typename F::Raw w[U];
+    typename F::State st;
+    stage.template load<0>(0);
+#pragma unroll
+    for (int k = 0; k < U - 1; k++) F::load(w[k], W, rb, ws(k), t0, lane);
+    stage.template store<0>(abuf + srow);
+    __syncthreads();
+    for (int s0 = 0; s0 < steps; s0 += U) {
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            const int s = s0 + k;
+            if (s >= steps) break;  // uniform; only for a step count that is not a multiple of 4
+            const bool more = s + 1 < steps;
+            if (more) stage_load(stage, (k + 1) & 1, s + 1);
+            F::load(w[(k + U - 1) % U], W, rb, ws(s + U - 1), t0, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            const int ss = k % F::kSpu;
+            F::begin(w[k], st, ss, lane);
+            const half_t *a = abuf + (k & 1) * BUF + n * kAStride + 16 * g;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                half8 b[2];
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) b[tt] = F::bop(w[k], st, ss, tt, j, lane);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const half8 av = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
+#pragma unroll
+                    for (int tt = 0; tt < 2; tt++) acc[tt][mt] = mfma(av, b[tt], acc[tt][mt]);
+                }
+            }
+            if (more) stage_store(stage, (k + 1) & 1, abuf + ((k + 1) & 1) * BUF + srow);
+            __syncthreads();
+        }
+    }
+}
+
+struct PfArgs {
+    QMat w0, w1;  // gate, up (or down in w0)
+    ActQ x;       // gate/up input (tokens) or down input (positions)
+    Dispatch d;
+    ActQ act;     // gate/up output
+    float *ypart; // down output [P][H]
+    int H, I, P, nchunk, use_gelu;
+};
+
+// The chunk `ci` of the dispatch's (16 MT)-token work list.
+template <int MT>
+__device__ inline bool pf_chunk(const Dispatch &d, int ci, int &e, int &p0, int &nt)
+{
+    if (ci >= d.meta[3]) return false;
+    const int c = d.chunks[ci];
+    e = c >> 16;
+    p0 = d.offsets[e] + (c & 0xFFFF) * 16 * MT;
+    nt = min(16 * MT, d.offsets[e + 1] - p0);
+    return true;
+}
+
+// LDS of one workgroup: the two staged activation tiles during the K loop, then
+// (gate/up) the gate and up results of 64 tokens x 64 rows at a time.
+template <int MT>
+struct PfLds {
+    static constexpr int kA = 2 * 16 * MT * kAStride * 2;        // bytes
+    static constexpr int kEpi = 2 * 64 * (kRowBlock + 1) * 4;    // bytes
+    static constexpr int kBytes = kA > kEpi ? kA : kEpi;
+};
+
+// ------------------------------------------------------------ gate / up
+
+// Grid nchunk * I/64 workgroups of 256 threads, chunks fastest.  Wave w: matrix
+// w >> 1 (gate, up), tiles 2 (w & 1) and 2 (w & 1) + 1 of row block rb.  After the
+// K loop the gate and up results of 64 tokens at a time go through LDS; each
+// wavefront then applies SiLU(g) * u to 16 of them and writes them in the
+// activation format (one 64-column group per token).
+template <class F, int MT>
+__global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
+{
+    constexpr int R = MT / 4;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kBytes];
+    int e, p0, nt;
+    if (!pf_chunk<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;  // uniform over the workgroup
+    const int rb = (int)(blockIdx.x / a.nchunk);
+    const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int mat = wv >> 1, t0 = 2 * (wv & 1);
+    const Planes W = planes(mat ? a.w1 : a.w0, e);
+    half_t *abuf = (half_t *)smem;
+    const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
+    StageX<R, 2> stage;
+    stage.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
+#pragma unroll
+    for (int h = 0; h < R; h++) stage.off[h] = a.d.rows[p0 + min(r + 64 * h, nt - 1)] * a.H * 2 + 32 * q;
+    f32x4 acc[2][MT];
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    pf_loop<F, MT>(W, rb, t0, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q, acc);
+
+    // results * the tokens' descales -> LDS [mat][token][row], 64 tokens at a time
+    float *res = (float *)smem;
+#pragma unroll
+    for (int h = 0; h < R; h++) {
+#pragma unroll
+        for (int mq = 0; mq < 4; mq++) {
+            const int mt = 4 * h + mq;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * mq + 4 * g + i;
+                const float dv = a.x.ds[a.d.rows[p0 + min(64 * h + m, nt - 1)]];
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+                    res[(mat * 64 + m) * (kRowBlock + 1) + 16 * (t0 + tt) + n] = acc[tt][mt][i] * dv;
+            }
+        }
+        __syncthreads();
+        for (int m = 16 * wv; m < 16 * wv + 16; m++) {  // uniform per wavefront
+            const float gv = res[m * (kRowBlock + 1) + lane], uv = res[(64 + m) * (kRowBlock + 1) + lane];
+            const float v = gate_act(gv, a.use_gelu) * uv;
+            const float sc = pow2_scale(wave_max(fabsf(v)));
+            if (64 * h + m < nt) {
+                const size_t pos = (size_t)p0 + 64 * h + m;
+                a.act.q[pos * a.I + (size_t)kStep * rb + mma_pos(lane)] = (half_t)(v * sc);
+                if (lane == 0) a.act.ds[(size_t)rb * a.act.ld + pos] = 1.0f / sc;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------- down
+
+// Grid nchunk * H/128 workgroups of 256 threads, chunks fastest.  Wave w: row block
+// 2 x + (w >> 1), tiles 2 (w & 1) and 2 (w & 1) + 1.  Before the K loop the
+// workgroup finds each position's largest descale over the I/64 groups (the row
+// reference); staging scales every group to it, and the results are multiplied by
+// it once at the end.  Positions past the group's end are computed on the next
+// group's (or, past the last position, the last position's) activations and not
+// stored.
+template <class F, int MT>
+__global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
+{
+    constexpr int R = MT / 4;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
+    __shared__ float ref[16 * MT];
+    int e, p0, nt;
+    if (!pf_chunk<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;
+    const int rbg = (int)(blockIdx.x / a.nchunk);
+    const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int rb = 2 * rbg + (wv >> 1), t0 = 2 * (wv & 1);
+    const Planes W = planes(a.w0, e);
+    const int G = a.I / kStep, ld = a.x.ld;
+    for (int m = threadIdx.x; m < 16 * MT; m += 256) {  // the row references
+        const int pr = min(p0 + m, a.P - 1);
+        float mx = 0.0f;
+        for (int gg = 0; gg < G; gg++) mx = fmaxf(mx, a.x.ds[(size_t)gg * ld + pr]);
+        ref[m] = mx;
+    }
+    __syncthreads();
+    const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
+    StageAct<R, 2> stage;
+    stage.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
+    stage.ds = make_rsrc(a.x.ds, (size_t)G * ld * 4);
+    stage.ld4 = ld * 4;
+#pragma unroll
+    for (int h = 0; h < R; h++) {
+        const int pos = min(p0 + r + 64 * h, a.P - 1);
+        stage.off[h] = pos * a.I * 2 + 32 * q;
+        stage.doff[h] = pos * 4;
+        stage.inv_ref[h] = 1.0f / ref[r + 64 * h];
+    }
+    f32x4 acc[2][MT];
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    pf_loop<F, MT>(W, rb, t0, a.I / kStep, lane, stage, (half_t *)smem, r * kAStride + 16 * q, acc);
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * mt + 4 * g + i;
+            if (m < nt) {
+                float *yp = a.ypart + ((size_t)p0 + m) * a.H + (size_t)kRowBlock * rb + n;
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) yp[16 * (t0 + tt)] = acc[tt][mt][i] * ref[m];
+            }
+        }
+}
+
+// ------------------------------------------------------------- launchers
+
+bool grouped_supported(int H, int I) { return H % 128 == 0 && I % 64 == 0; }
+
+template <class F, int MT>
+static int launch_pf(const PfArgs &a, bool gateup, hipStream_t st)
+{
+    if (gateup) {
+        const size_t wgs = (size_t)a.nchunk * (a.I / kRowBlock);
+        hipLaunchKernelGGL((k_pf_gateup<F, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    } else {
+        const size_t wgs = (size_t)a.nchunk * (a.H / (2 * kRowBlock));
+        hipLaunchKernelGGL((k_pf_down<F, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    }
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
+// 64-token chunks (mt = 4).  128-token chunks (MT = 8) compile too, but at 2-3
+// waves per SIMD they measured slower on the Mixtral 2048-token prefill (2.84 ms
+// against 2.36 ms), so the planner does not select them.
+template <class F>
+static int launch_pf_mt(const PfArgs &a, int, bool gateup, hipStream_t st)
+{
+    return launch_pf<F, 4>(a, gateup, st);
+}
+
+static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStream_t st)
+{
+    switch (type) {
+    case ANEDVD_Q8_0: return launch_pf_mt<FQ8_0>(a, mt, gateup, st);
+    case ANEDVD_Q4_0: return launch_pf_mt<FQ4_0>(a, mt, gateup, st);
+    case ANEDVD_Q4_K: return launch_pf_mt<FQ4_K>(a, mt, gateup, st);
+    case ANEDVD_Q6_K: return launch_pf_mt<FQ6_K>(a, mt, gateup, st);
+    default:
+        set_error("grouped GEMM: ggml type %d has no kernel", type);
+        return ANEDVD_E_UNSUPPORTED_TYPE;
+    }
+}
+
+int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
+                          int mt, int nchunk, const ActQ &act, int use_gelu, hipStream_t st)
+{
+    if (gate.type != up.type) {
+        set_error("grouped gate/up: gate type %d and up type %d differ", gate.type, up.type);
+        return ANEDVD_E_UNSUPPORTED_TYPE;
+    }
+    PfArgs a{};
+    a.w0 = gate;
+    a.w1 = up;
+    a.x = x;
+    a.d = d;
+    a.act = act;
+    a.H = H;
+    a.I = I;
+    a.P = P;
+    a.nchunk = nchunk;
+    a.use_gelu = use_gelu;
+    return launch_pf_type(gate.type, a, mt, true, st);
+}
+
+int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
+                        int nchunk, float *ypart, hipStream_t st)
+{
+    PfArgs a{};
+    a.w0 = down;
+    a.x = act;
+    a.d = d;
+    a.ypart = ypart;
+    a.H = H;
+    a.I = I;
+    a.P = P;
+    a.nchunk = nchunk;
+    return launch_pf_type(down.type, a, mt, false, st);
+}
+
+}  // namespace anedvd

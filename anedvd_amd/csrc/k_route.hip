@@ -244,7 +244,9 @@ __device__ inline void route_token_row(const float *__restrict__ logits, int t, 
 // Outputs: offsets[E+1]; rows/slots[T*k] grouped by expert, tokens ascending;
 // inv[t*k+s] = position of (t, s) or -1 for an expert id >= E; active[0..n) =
 // experts with tokens, ascending; meta[0] = n, meta[1] = largest group,
-// meta[2] = entries with expert id >= E (never written out of bounds).
+// meta[2] = entries with expert id >= E (never written out of bounds); and, when
+// `chunks` is given, the grouped GEMM's work list: chunks[c] = (e << 16) | j for
+// the j-th `chunk`-token slice of expert e, experts ascending, meta[3] = their count.
 constexpr int kDispWords = 4096;
 
 struct DispLds {
@@ -257,20 +259,30 @@ struct DispLds {
     int32_t bad;
 };
 
-__device__ inline int wave_incl_scan(int v, int lane)
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline int dpp_or_zero(int v)
 {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(v, o, 64);
-        if (lane >= o) v += u;
-    }
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Inclusive prefix sum over the wavefront: row_shr 1, 2, 4, 8 within each row of
+// 16 lanes, then the row totals carried up with row_bcast 15 and 31.
+__device__ inline int wave_incl_scan(int v, int)
+{
+    v += dpp_or_zero<0x111>(v);
+    v += dpp_or_zero<0x112>(v);
+    v += dpp_or_zero<0x114>(v);
+    v += dpp_or_zero<0x118>(v);
+    v += dpp_or_zero<0x142, 0xA>(v);
+    v += dpp_or_zero<0x143, 0xC>(v);
     return v;
 }
 
 template <int NTH>
 __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
                                int32_t *__restrict__ rows, int32_t *__restrict__ slots, int32_t *__restrict__ inv,
-                               int32_t *__restrict__ active, int32_t *__restrict__ meta, DispLds &s)
+                               int32_t *__restrict__ active, int32_t *__restrict__ meta, int32_t *__restrict__ chunks,
+                               int chunk, DispLds &s)
 {
     const int P = T * k, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     for (int e = tid; e < E; e += NTH) {
@@ -297,8 +309,12 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
             nz += c[q] > 0;
             mx = max(mx, c[q]);
         }
+        int nch = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) nch += (c[q] + chunk - 1) / chunk;
         int run = wave_incl_scan(tot, lane) - tot;
         int runa = wave_incl_scan(nz, lane) - nz;
+        int runc = wave_incl_scan(nch, lane) - nch;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int e = lane * 4 + q;
@@ -307,6 +323,8 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
                 offsets[e] = run;
                 if (c[q]) active[runa++] = e;
                 run += c[q];
+                if (chunks)
+                    for (int j = 0; j * chunk < c[q]; j++) chunks[runc++] = (e << 16) | j;
             }
         }
 #pragma unroll
@@ -314,6 +332,7 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
         if (lane == 63) {
             offsets[E] = run;
             meta[0] = runa;
+            meta[3] = runc;
         }
         if (lane == 0) {
             meta[1] = mx;
@@ -374,15 +393,22 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
 
 // --------------------------------------------------- activation conversion
 
-// x f32 [rows][K] -> the MFMA activation format (common.h): one wavefront per
-// (row, 64-column group); ds[g * ld + row].
+// x f32 [rows][K] -> the MFMA activation format (common.h) with one power of two
+// per row: wavefront w takes row w, finds its largest magnitude, then converts
+// it; every group's descale ds[g * ld + row] holds the row's, so the grouped GEMM
+// can accumulate a whole row's K in the MFMA.
 __device__ void act_prep_wave(const float *__restrict__ x, int rows, int K, const ActQ &xq, size_t w, int lane)
 {
-    const int G = K / 64;
-    if (w >= (size_t)rows * G) return;
-    const size_t r = w / G;
-    const int g = (int)(w % G);
-    act_group(x[r * K + g * 64 + lane], lane, xq.q + r * K + g * 64, xq.ds + (size_t)g * xq.ld + r);
+    if (w >= (size_t)rows) return;
+    const float *xr = x + w * K;
+    float m = 0.0f;
+    for (int c = lane; c < K; c += 64) m = fmaxf(m, fabsf(xr[c]));
+    const float sc = pow2_scale(wave_max(m)), inv = 1.0f / sc;
+    half_t *q = xq.q + w * K;
+    for (int g = 0; g < K / 64; g++) {
+        q[64 * g + mma_pos(lane)] = (half_t)(xr[64 * g + lane] * sc);
+        if (lane == 0) xq.ds[(size_t)g * xq.ld + w] = inv;
+    }
 }
 
 // ------------------------------------------------------- route launches
@@ -432,14 +458,15 @@ __global__ __launch_bounds__(kDispThreads) void k_route_dispatch(RouteArgs a, Di
     for (int t0 = 0; t0 < a.T; t0 += kDispThreads / 16)
         route_token_row(a.logits, t0 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx, idx_s, tab);
     __syncthreads();
-    dispatch_block<kDispThreads>(idx_s, a.T, a.k, a.E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, s);
+    dispatch_block<kDispThreads>(idx_s, a.T, a.k, a.E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, d.chunks,
+                                 d.chunk, s);
 }
 
 __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
                                                            Dispatch d)
 {
     __shared__ DispLds s;
-    dispatch_block<kDispThreads>(idx, T, k, E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, s);
+    dispatch_block<kDispThreads>(idx, T, k, E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, d.chunks, d.chunk, s);
 }
 
 __global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ x, int rows, int K, ActQ xq)
@@ -470,8 +497,8 @@ int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_
         return ANEDVD_E_INVALID_SHAPE;
     }
     RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, (T + 15) / 16};
-    const size_t groups = d_x ? (size_t)T * (H / 64) : 0;
-    const unsigned blocks = (unsigned)(a.n_route_blocks + (groups + 3) / 4);
+    const size_t waves = d_x ? (size_t)T : 0;  // activation conversion: one wavefront per token
+    const unsigned blocks = (unsigned)(a.n_route_blocks + (waves + 3) / 4);
     hipLaunchKernelGGL(k_route, dim3(blocks), dim3(256), 0, st, a);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
@@ -500,8 +527,8 @@ int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int no
         return launch_dispatch(d_idx, T, k, E, d, st);
     }
     RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, 1};
-    const size_t groups = d_x ? (size_t)T * (H / 64) : 0;
-    const unsigned blocks = (unsigned)(1 + (groups + 15) / 16);
+    const size_t waves = d_x ? (size_t)T : 0;
+    const unsigned blocks = (unsigned)(1 + (waves + 15) / 16);
     hipLaunchKernelGGL(k_route_dispatch, dim3(blocks), dim3(kDispThreads), 0, st, a, d);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
@@ -514,8 +541,7 @@ int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream
         set_error("activation conversion: %d columns is not a multiple of 64", K);
         return ANEDVD_E_INVALID_SHAPE;
     }
-    const size_t groups = (size_t)rows * (K / 64);
-    hipLaunchKernelGGL(k_act_prep, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, st, d_x, rows, K, xq);
+    hipLaunchKernelGGL(k_act_prep, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, d_x, rows, K, xq);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }

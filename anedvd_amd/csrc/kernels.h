@@ -16,9 +16,12 @@ struct ActQ {
 // Token-to-expert dispatch of T*k (token, slot) entries (engine.zig:1204-1216):
 // offsets[E+1]; rows/slots[T*k] grouped by expert, tokens ascending; inv[T*k] =
 // position of (t, s); active[] = experts with tokens, ascending; meta[0] = number
-// of active experts, meta[1] = largest group, meta[2] = ids >= E.
+// of active experts, meta[1] = largest group, meta[2] = ids >= E, meta[3] = number
+// of chunks; chunks[] (optional) = (e << 16) | j for each `chunk`-token slice j of
+// expert e's group, experts ascending -- the expert kernels' work list.
 struct Dispatch {
-    int32_t *offsets, *rows, *slots, *inv, *active, *meta;
+    int32_t *offsets, *rows, *slots, *inv, *active, *meta, *chunks;
+    int chunk;
 };
 
 // k_dequant.hip
@@ -44,18 +47,28 @@ int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream
 struct MmPlan {
     int ks_gu;    // K split of gate/up (workgroups per 64-row block)
     int ks_dn;    // K split of down
+    int mt;       // 16-token tiles per workgroup: 1 (decode kernels) or 4 (grouped GEMM, k_pf.hip)
+    int chunk;    // tokens per work-list chunk (16 mt), the dispatch's `chunk`
+    int nchunk;   // bound on the work list's length: P / chunk + max_u
 };
 bool mm_supported(int type);
-// max_u: most experts a call can touch.
-MmPlan plan_mm(int gate_type, int down_type, int H, int I, int max_u);
+// P (token, slot) entries over at most max_u experts.
+MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u);
 // gate/up + SiLU(gate)*up for every dispatched (token, expert) position, written
 // to `act` [P][I] in the activation format.  With plan.ks_gu > 1 the K partials
 // go to `part` [ks][P][2][I] and a second launch finishes them.
 int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
-                         int max_u, const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st);
+                         const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st);
 // down for every position: ypart [ks_dn][P][H] (the combine adds the K partials).
-int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int max_u,
+int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P,
                        const MmPlan &plan, float *ypart, hipStream_t st);
+// k_pf.hip -- the grouped GEMM for prefill-sized groups (chunks of 16 mt tokens)
+bool grouped_supported(int H, int I);
+int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
+                          int mt, int nchunk, const ActQ &act, int use_gelu, hipStream_t st);
+int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
+                        int nchunk, float *ypart, hipStream_t st);
+
 int launch_combine(const float *ypart, const int32_t *inv, const float *probs, int T, int k, int H, int KS, int P,
                    const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st);
 

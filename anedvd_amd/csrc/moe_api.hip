@@ -170,7 +170,7 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     Fwd x{};
     x.P = P;
     x.max_u = std::min(E, P);
-    x.plan = plan_mm(L->gate.type, L->down.type, H, I, x.max_u);
+    x.plan = plan_mm(L->gate.type, L->down.type, H, I, P, x.max_u);
     Carve c{base};
     x.logits = c.take<float>((size_t)T * E);
     x.probs = c.take<float>(P);
@@ -181,17 +181,21 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     x.d.inv = c.take<int32_t>(P);
     x.d.active = c.take<int32_t>(E);
     x.d.meta = c.take<int32_t>(4);
+    x.d.chunks = c.take<int32_t>((size_t)x.plan.nchunk);
+    x.d.chunk = x.plan.chunk;
     x.xq = ActQ{c.take<half_t>((size_t)T * H), c.take<float>((size_t)T * (H / kStep)), T};
     x.act = ActQ{c.take<half_t>((size_t)P * I), c.take<float>((size_t)P * (I / kStep)), P};
     x.part = x.plan.ks_gu > 1 ? c.take<float>((size_t)x.plan.ks_gu * P * 2 * I) : nullptr;
     x.ypart = c.take<float>((size_t)x.plan.ks_dn * P * H);
     if (L->Is) {
         const int Is = (int)L->Is;
-        x.splan = plan_mm(L->sgate.type, L->sdown.type, H, Is, 1);
+        x.splan = plan_mm(L->sgate.type, L->sdown.type, H, Is, T, 1);
         x.sd.offsets = c.take<int32_t>(2);
         x.sd.rows = c.take<int32_t>(T);
         x.sd.active = c.take<int32_t>(1);
         x.sd.meta = c.take<int32_t>(4);
+        x.sd.chunks = c.take<int32_t>((size_t)x.splan.nchunk);
+        x.sd.chunk = x.splan.chunk;
         x.sact = ActQ{c.take<half_t>((size_t)T * Is), c.take<float>((size_t)T * (Is / kStep)), T};
         x.sh_part = x.splan.ks_gu > 1 ? c.take<float>((size_t)x.splan.ks_gu * T * 2 * Is) : nullptr;
         x.sh_ypart = c.take<float>((size_t)x.splan.ks_dn * T * H);
@@ -206,8 +210,8 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     return (size_t)(c.p - base);
 }
 
-// Fills the shared expert's one-expert dispatch (all T tokens, in order) and,
-// if it is gated, its per-token scale sigmoid(shared_gate_lin . h).
+// Fills the shared expert's one-expert dispatch (all T tokens, in order, and its
+// chunk list) and, if it is gated, its per-token scale sigmoid(shared_gate_lin . h).
 __global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__restrict__ lin, int T, int H, Dispatch d,
                               float *scale)
 {
@@ -219,8 +223,12 @@ __global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__res
         d.meta[0] = 1;
         d.meta[1] = T;
         d.meta[2] = 0;
+        d.meta[3] = (T + d.chunk - 1) / d.chunk;
     }
-    if (threadIdx.x == 0) d.rows[t] = t;
+    if (threadIdx.x == 0) {
+        d.rows[t] = t;
+        if (t % d.chunk == 0) d.chunks[t / d.chunk] = t / d.chunk;  // expert 0, chunk j
+    }
     if (!lin) return;
     // one wavefront per token; sigmoid as cpu.sigmoid (cpu.zig:1223-1230)
     float g = 0.0f;
@@ -252,18 +260,17 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
     }
     ANEDVD_TRY(launch_route_and_dispatch(logits, T, E, k, L->norm, f.probs, f.idx, d_h, H, f.xq, f.d, st));
     mark(1);
-    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.max_u, f.plan, f.part, f.act,
-                                    L->gelu, st));
+    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act, L->gelu, st));
     mark(2);
-    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.max_u, f.plan, f.ypart, st));
+    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart, st));
     mark(3);
     if (L->Is) {
         const int Is = (int)L->Is;
         hipLaunchKernelGGL(k_shared_prep, dim3(T), dim3(64), 0, st, d_h, L->sgate_lin, T, H, f.sd, f.sh_scale);
         ANEDVD_HIP(hipGetLastError());
-        ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, f.xq, H, Is, f.sd, T, 1, f.splan, f.sh_part,
-                                        f.sact, L->gelu, st));
-        ANEDVD_TRY(launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, 1, f.splan, f.sh_ypart, st));
+        ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, f.xq, H, Is, f.sd, T, f.splan, f.sh_part, f.sact,
+                                        L->gelu, st));
+        ANEDVD_TRY(launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_ypart, st));
     }
     mark(4);
     ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, T, k, H, f.plan.ks_dn, P, L->Is ? f.sh_ypart : nullptr,
@@ -552,7 +559,7 @@ int anedvd_moe_dispatch(anedvd_moe_ctx *ctx, const uint32_t *idx, size_t T, size
     int32_t *dact = c.take<int32_t>(E);
     int32_t *dmeta = c.take<int32_t>(4);
     ANEDVD_HIP(hipMemcpyAsync(di, idx, P * 4, hipMemcpyHostToDevice, ctx->stream));
-    const Dispatch dd{doff, drows, dslots, dinv, dact, dmeta};
+    const Dispatch dd{doff, drows, dslots, dinv, dact, dmeta, nullptr, 16};
     ANEDVD_TRY(launch_dispatch(di, (int)T, (int)k, (int)E, dd, ctx->stream));
     int32_t meta[4];
     ANEDVD_HIP(hipMemcpyAsync(offsets, doff, (E + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -590,7 +597,7 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
     fwd_layout(L, 1, 1, &f, (uint8_t *)ctx->ws.base, true);
     std::vector<int32_t> off(E + 1);
     for (int e = 0; e <= E; e++) off[e] = e > (int)expert ? 1 : 0;
-    const int32_t zero = 0, act = (int32_t)expert, meta[4] = {1, 1, 0, 0};
+    const int32_t zero = 0, act = (int32_t)expert, meta[4] = {1, 1, 0, 1}, chunk0 = (int32_t)(expert << 16);
     hipStream_t st = ctx->stream;
     ANEDVD_HIP(hipMemcpyAsync(f.h_in, h, (size_t)H * 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.offsets, off.data(), (size_t)(E + 1) * 4, hipMemcpyHostToDevice, st));
@@ -598,11 +605,11 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
     ANEDVD_HIP(hipMemcpyAsync(f.d.inv, &zero, 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.active, &act, 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.meta, meta, sizeof meta, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.d.chunks, &chunk0, 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.probs, &weight, 4, hipMemcpyHostToDevice, st));
     ANEDVD_TRY(launch_act_prep(f.h_in, 1, H, f.xq, st));
-    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, 1, 1, f.plan, f.part, f.act, L->gelu,
-                                    st));
-    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, 1, 1, f.plan, f.ypart, st));
+    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, 1, f.plan, f.part, f.act, L->gelu, st));
+    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, 1, f.plan, f.ypart, st));
     ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, 1, 1, H, f.plan.ks_dn, 1, nullptr, nullptr, 0, f.out, st));
     std::vector<float> y(H);
     ANEDVD_HIP(hipMemcpyAsync(y.data(), f.out, (size_t)H * 4, hipMemcpyDeviceToHost, st));
@@ -684,7 +691,7 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *L, const float *h, size_t T, cons
         stats->touched_experts = (uint32_t)meta[0];
         stats->max_group = (uint32_t)meta[1];
         stats->weight_bytes = (uint64_t)(meta[0] * L->expert_bytes + L->shared_bytes + (logits ? 0.0 : 2.0 * L->E * L->H));
-        stats->path = 0;
+        stats->path = f.plan.mt > 1 ? 1 : 0;
     }
     return ANEDVD_OK;
 }

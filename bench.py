@@ -29,6 +29,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 METRIC = "MoE-layer tok/s + % HBM roofline (decode), % MFMA peak (prefill), 30B-A3B shape"
 
 
@@ -75,6 +76,51 @@ def cpu_baseline(spec, L, h, logits, budget_s: float):
                       f"SwiGLU GEMVs), first {n} tokens of the batch, {dt:.1f} s, gcc -O2, 1 thread"}, ref, n
 
 
+PREFILL = {
+    # name: (spec attribute, tokens, routing)
+    "qwen3-q4km-512": ("QWEN3_30B_A3B_Q4_K_M", 512, "zipf"),
+    "mixtral-q4_0-2048": ("MIXTRAL_8X7B_Q4_0", 2048, "normal"),
+}
+
+
+def run_prefill(name: str, ctx, warmup: int, steps: int) -> dict:
+    """One prefill-sized layer call (route + dispatch + grouped expert products +
+    combine, router logits given), two rotated layer copies, HIP graph per step;
+    reports useful MFMA-path FLOP/s against the fp16 dense peak."""
+    from anedvd_amd import moe, synth
+    from anedvd_amd import workloads as W
+    attr, T, routing = PREFILL[name]
+    spec = getattr(W, attr)
+    t0 = time.perf_counter()
+    L = synth.make_layer(spec, seed=0)
+    layers = [moe.MoeLayer(ctx, spec, L) for _ in range(2)]
+    h = synth.activations(spec, T, seed=1)
+    lg = synth.zipf_logits(spec, T, seed=1) if routing == "zipf" else synth.activations(spec, T, seed=2)[:, :spec.n_experts]
+    lg = np.ascontiguousarray(lg, dtype=np.float32)
+    _, st = layers[0].forward(h, lg, stats=True)
+    d_h, d_lg = ctx.to_device(h), ctx.to_device(lg)
+    d_out = ctx.alloc(T * spec.hidden * 4)
+    ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps, graph=True)
+    _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, steps, stages=True)
+    for p in (d_h, d_lg, d_out):
+        ctx.free(p)
+    for l in layers:
+        l.free()
+    t = ms / 1e3 / steps
+    flops = spec.call_flops(T, with_router=False)
+    lbytes = spec.call_bytes(st["touched_experts"], T, with_router=False)
+    r = {"workload": spec.name, "tokens": T, "routing": routing, "touched_experts": st["touched_experts"],
+         "max_group": st["max_group"], "ms_per_step": round(ms / steps, 4), "tokens_per_s": round(T / t, 1),
+         "TFLOPs": round(flops / t / 1e12, 2), "mfma_frac": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+         "layer_GBps": round(lbytes / t / 1e9, 1), "hbm_frac": round(lbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+         "stage_ms": dict(zip(["route_dispatch", "gate_up", "down", "shared", "combine", "total"],
+                              [round(x, 4) for x in stages]))}
+    log(f"[bench] prefill {name}: {r['ms_per_step'] * 1e3:.0f} us/step, {r['TFLOPs']} TFLOP/s "
+        f"({100 * r['mfma_frac']:.1f}% of fp16 MFMA peak), {r['layer_GBps']} GB/s, touched {r['touched_experts']}, "
+        f"max group {r['max_group']}, stages {r['stage_ms']} (setup {time.perf_counter() - t0:.1f} s)")
+    return r
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -84,6 +130,9 @@ def main():
     ap.add_argument("--copies", type=int, default=8, help="device copies of the layer rotated per step")
     ap.add_argument("--sweep", default="1,8,32", help="extra decode batches reported beside the headline ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
+    ap.add_argument("--prefill", default="qwen3-q4km-512,mixtral-q4_0-2048",
+                    help="prefill workloads reported beside the headline ('' = none)")
+    ap.add_argument("--prefill-only", action="store_true", help="run only the prefill workloads (profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (a plain copy kernel of known size, "
                          "for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -107,6 +156,13 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] calibration: 3 device copies of {args.calibrate_copy} MiB")
         del src, dst
+
+    if args.prefill_only:
+        ctx = moe.MoeContext(0)
+        out = [run_prefill(name, ctx, args.warmup, args.steps) for name in args.prefill.split(",") if name.strip()]
+        print(json.dumps({"prefill": out}), flush=True)
+        ctx.close()
+        return
 
     spec = W.QWEN3_30B_A3B_Q8_0
     B = args.batch
@@ -158,6 +214,10 @@ def main():
                 "traffic": read_traffic("pmc_k_mm_gateup_q8_0_decode_b64.md"),
                 "bytes_per_launch": gu_bytes, "avg_launch_ms": gu_ms}
 
+    prefill = []
+    for name in [x for x in args.prefill.split(",") if x.strip()]:
+        prefill.append(run_prefill(name, ctx, args.warmup, max(10, args.steps // 10)))
+
     cpu = None
     parity = None
     if args.cpu_seconds > 0:
@@ -180,6 +240,7 @@ def main():
         "touched_experts": head["touched_experts"], "stage_ms": head["stage_ms"],
         "roofline": roofline, "cpu_baseline": cpu, "parity_vs_oracle": parity,
         "sweep": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()} for r in sweep],
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
     for l in layers:

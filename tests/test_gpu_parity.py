@@ -246,17 +246,30 @@ FORMATS = [(W.Q4_0, W.Q4_0, W.Q4_0), (W.Q4_K, W.Q4_K, W.Q6_K), (W.Q8_0, W.Q8_0, 
 
 
 @pytest.mark.parametrize("types", FORMATS, ids=lambda t: "/".join(W.TYPE_NAMES[x] for x in t))
-@pytest.mark.parametrize("T", [1, 5, 64])
+@pytest.mark.parametrize("T", [1, 5, 64, 160])
 def test_forward_block_formats(ctx, types, T):
     """Fused dequant + SwiGLU for every supported GGUF block format, at group sizes
-    from 1 token (K split over workgroups) to more than one pass over the weights."""
+    from 1 token (K split over workgroups) through several 16-token chunks per
+    expert (T=64) to the grouped GEMM's 64-token chunks with partial last chunks
+    (T=160: 640 entries over 16 experts)."""
     spec = dataclasses.replace(W.QWEN3_30B_A3B_Q4_K_M, name="formats", hidden=1024, inter=512, n_experts=16, k=4,
                                gate_type=types[0], up_type=types[1], down_type=types[2], scale_sigma=0.01)
     _, _, err, _ = _forward_case(ctx, spec, T, seed=T)
     assert err <= REL_L2_TOL
 
 
-@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("types", FORMATS, ids=lambda t: "/".join(W.TYPE_NAMES[x] for x in t))
+def test_forward_grouped_large_groups(ctx, types):
+    """Groups of ~300 tokens (600 tokens, top-2 of 4 experts) take the grouped GEMM:
+    several 64-token chunks per expert and a partial last one."""
+    spec = dataclasses.replace(W.QWEN3_30B_A3B_Q4_K_M, name="formats", hidden=1024, inter=512, n_experts=4, k=2,
+                               gate_type=types[0], up_type=types[1], down_type=types[2], scale_sigma=0.01)
+    _, _, err, st = _forward_case(ctx, spec, 600, seed=11)
+    assert err <= REL_L2_TOL
+    assert st["path"] == 1
+
+
+@pytest.mark.parametrize("T", [1, 16, 160])
 def test_forward_mixtral_shape_q4_0(ctx, T):
     """Mixtral-8x7B proportions (hidden 4096, top-2 of 8) with the expert width cut to
     2048 so the oracle stays fast."""
