@@ -2,11 +2,11 @@
 //
 // Same math as the decode kernels (cpu.moeExpertAccumF32, cpu.zig:416-452, over
 // the gguf.zig block formats), organised for groups of tens to hundreds of tokens:
-//   - a workgroup takes a 64-token chunk of one expert's group and 64 weight rows
-//     of both gate and up (or 128 rows of down);
+//   - a workgroup takes a 64-token chunk of one expert's group and 128 weight rows
+//     of both gate and up (or 256 rows of down);
 //   - the chunk's activations are staged in LDS once per 64-column step and shared
 //     by the four wavefronts;
-//   - each wavefront dequantises its two 16-row tiles once per step to f16 (Q8_0,
+//   - each wavefront dequantises its four 16-row tiles once per step to f16 (Q8_0,
 //     Q4_0: d * q rounded once; Q4_K, Q6_K: the quant exact, the sub-block scale
 //     and min as f16, one rounding in the FMA) and runs them against the chunk's
 //     16-token tiles, accumulating the whole K inside the MFMA;
@@ -20,6 +20,7 @@
 namespace anedvd {
 
 constexpr int kAStride = 72;  // halves per staged token row: 64 + 8 against LDS bank conflicts
+constexpr int kPfTiles = 4;   // 16-row tiles per wavefront: each staged A read feeds four MFMAs
 
 __device__ inline half_t h_bits(uint32_t b)
 {
@@ -31,7 +32,7 @@ __device__ inline half_t h_bits(uint32_t b)
 
 // ------------------------------------------------------------------ decoders
 //
-// A decoder loads one step of a wavefront's two row tiles (t0, t0 + 1): load();
+// A decoder loads one step of a wavefront's four row tiles (a 64-row block): load();
 // takes what stays valid for a whole scale unit on the unit's first step: begin();
 // and yields the f16 B operand of (tile tt, block j) at step `ss` of the unit:
 // bop().  Lane l = 16 g + n holds row n of the tile and the 8 columns 32 j + 8 g + i.
@@ -39,17 +40,17 @@ __device__ inline half_t h_bits(uint32_t b)
 struct FQ8_0 {
     static constexpr int kSpu = 1;
     struct Raw {
-        u32x4 q[2];
-        uint32_t s[2];
+        u32x4 q[kPfTiles];
+        uint32_t s[kPfTiles];
     };
     struct State {};
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int t0, int lane)
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
         const int qo = lane_plane_off(p, rb, s, 16), so = row_plane_off(p, rb, s, 4);
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane + 1024 * (t0 + tt), qo, kNT);
-            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * (t0 + tt), so, kNT);
+        for (int tt = 0; tt < kPfTiles; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane + 1024 * tt, qo, kNT);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * tt, so, kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -63,17 +64,17 @@ struct FQ8_0 {
 struct FQ4_0 {
     static constexpr int kSpu = 1;
     struct Raw {
-        u32x2 q[2];
-        uint32_t s[2];
+        u32x2 q[kPfTiles];
+        uint32_t s[kPfTiles];
     };
     struct State {};
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int t0, int lane)
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
         const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, 4);
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * (t0 + tt), qo, kNT);
-            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * (t0 + tt), so, kNT);
+        for (int tt = 0; tt < kPfTiles; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * tt, so, kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -91,29 +92,29 @@ struct FQ4_0 {
 struct FQ4_K {
     static constexpr int kSpu = 4;
     struct Raw {
-        u32x2 q[2];
-        u32x4 sc[2];  // d, dmin, scales: loaded on a unit's first step
+        u32x2 q[kPfTiles];
+        u32x4 sc[kPfTiles];  // d, dmin, scales: loaded on a unit's first step
     };
     struct State {
-        half_t d1[2][8], m1[2][8];
+        half_t d1[kPfTiles][8], m1[kPfTiles][8];
     };
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int t0, int lane)
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
         const int qo = lane_plane_off(p, rb, s, 8);
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++) r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * (t0 + tt), qo, kNT);
+        for (int tt = 0; tt < kPfTiles; tt++) r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++)
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * (t0 + tt), so, kNT);
+            for (int tt = 0; tt < kPfTiles; tt++)
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
         }
     }
     __device__ static inline void begin(const Raw &r, State &st, int ss, int)
     {
         if (ss) return;
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
+        for (int tt = 0; tt < kPfTiles; tt++) {
             const float d = f16_bits_to_f32((uint16_t)(r.sc[tt].x & 0xFFFFu));
             const float dmin = f16_bits_to_f32((uint16_t)(r.sc[tt].x >> 16));
 #pragma unroll
@@ -139,28 +140,28 @@ struct FQ4_K {
 struct FQ6_K {
     static constexpr int kSpu = 4;
     struct Raw {
-        u32x2 q[2];
-        uint32_t h[2];
-        u32x4 sc[2];    // int8 scales (a unit's first step)
-        uint16_t d[2];  // f16 d (a unit's first step)
+        u32x2 q[kPfTiles];
+        uint32_t h[kPfTiles];
+        u32x4 sc[kPfTiles];    // int8 scales (a unit's first step)
+        uint16_t d[kPfTiles];  // f16 d (a unit's first step)
     };
     struct State {
-        half_t dsc[2][8];  // [tt][2 ss + j]: d * sc of the lane's sub-block 4 ss + 2 j + g / 2
+        half_t dsc[kPfTiles][8];  // [tt][2 ss + j]: d * sc of the lane's sub-block 4 ss + 2 j + g / 2
     };
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int t0, int lane)
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 4);
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * (t0 + tt), qo, kNT);
-            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane + 256 * (t0 + tt), ho, kNT);
+        for (int tt = 0; tt < kPfTiles; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane + 256 * tt, ho, kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, 2);
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++) {
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * (t0 + tt), so, kNT);
-                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * (t0 + tt), dof, kNT);
+            for (int tt = 0; tt < kPfTiles; tt++) {
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
+                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * tt, dof, kNT);
             }
         }
     }
@@ -169,7 +170,7 @@ struct FQ6_K {
         if (ss) return;
         const int hg = lane >> 5;
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
+        for (int tt = 0; tt < kPfTiles; tt++) {
             const float d = f16_bits_to_f32(r.d[tt]);
 #pragma unroll
             for (int k = 0; k < 8; k++) {
@@ -268,17 +269,17 @@ __device__ inline void stage_store(const S &st, int b, half_t *dst)
 
 // ------------------------------------------------------------ main loop
 
-// Steps [0, steps) of the wavefront's tiles t0, t0 + 1 of row block rb against the
-// MT 16-token tiles staged in `abuf` (two buffers of 16 MT x kAStride halves):
-// acc[tt][mt] = sum_k W[64 rb + 16 (t0 + tt) + l % 16][k] * A[16 mt + 4 (l / 16) + i][k].
-// Weights are loaded three steps ahead (a ring of four register buffers) and the
-// next step's activations one step ahead (two register slots); every thread of the
-// workgroup takes part in the staging, so all of them reach the barriers.  Steps go
-// in unrolled blocks of four, so the rings and the LDS buffers rotate at
+// Steps [0, steps) of the wavefront's four tiles of row block rb against the MT
+// 16-token tiles staged in `abuf` (two buffers of 16 MT x kAStride halves):
+// acc[tt][mt] = sum_k W[64 rb + 16 tt + l % 16][k] * A[16 mt + 4 (l / 16) + i][k].
+// Weights and the next step's activations are loaded one step ahead (two register
+// slots each); every thread of the workgroup takes part in the staging, so all of
+// them reach the barriers.  Steps go in unrolled blocks of four (one scale unit of
+// the super-block formats), so the slots and the LDS buffers alternate at
 // compile-time indices.  Weight loads past the last step go out of range (zero, no
 // memory traffic).
 template <class F, int MT, class S>
-__device__ inline void pf_loop(const Planes &W, int rb, int t0, int steps, int lane, S &stage, half_t *abuf,
+__device__ inline void pf_loop(const Planes &W, int rb, int steps, int lane, S &stage, half_t *abuf,
                                int srow, f32x4 (*acc)[MT])
 {
     constexpr int U = 4;
@@ -287,11 +288,10 @@ __device__ inline void pf_loop(const Planes &W, int rb, int t0, int steps, int l
     const int n = lane & 15, g = lane >> 4;
     const int so = (W.nrb - rb) * W.steps;
     auto ws = [&](int x) { return x < steps ? x : so; };
-    typename F::Raw w[U];
+    typename F::Raw w[2];
     typename F::State st;
     stage.template load<0>(0);
-#pragma unroll
-    for (int k = 0; k < U - 1; k++) F::load(w[k], W, rb, ws(k), t0, lane);
+    F::load(w[0], W, rb, 0, lane);
     stage.template store<0>(abuf + srow);
     __syncthreads();
     for (int s0 = 0; s0 < steps; s0 += U) {
@@ -301,21 +301,21 @@ __device__ inline void pf_loop(const Planes &W, int rb, int t0, int steps, int l
             if (s >= steps) break;  // uniform; only for a step count that is not a multiple of 4
             const bool more = s + 1 < steps;
             if (more) stage_load(stage, (k + 1) & 1, s + 1);
-            F::load(w[(k + U - 1) % U], W, rb, ws(s + U - 1), t0, lane);
+            F::load(w[(k + 1) & 1], W, rb, ws(s + 1), lane);
             __builtin_amdgcn_sched_barrier(0);
             const int ss = k % F::kSpu;
-            F::begin(w[k], st, ss, lane);
+            F::begin(w[k & 1], st, ss, lane);
             const half_t *a = abuf + (k & 1) * BUF + n * kAStride + 16 * g;
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                half8 b[2];
+                half8 b[kPfTiles];
 #pragma unroll
-                for (int tt = 0; tt < 2; tt++) b[tt] = F::bop(w[k], st, ss, tt, j, lane);
+                for (int tt = 0; tt < kPfTiles; tt++) b[tt] = F::bop(w[k & 1], st, ss, tt, j, lane);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     const half8 av = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
 #pragma unroll
-                    for (int tt = 0; tt < 2; tt++) acc[tt][mt] = mfma(av, b[tt], acc[tt][mt]);
+                    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av, b[tt], acc[tt][mt]);
                 }
             }
             if (more) stage_store(stage, (k + 1) & 1, abuf + ((k + 1) & 1) * BUF + srow);
@@ -356,10 +356,11 @@ struct PfLds {
 
 // ------------------------------------------------------------ gate / up
 
-// Grid nchunk * I/64 workgroups of 256 threads, chunks fastest.  Wave w: matrix
-// w >> 1 (gate, up), tiles 2 (w & 1) and 2 (w & 1) + 1 of row block rb.  After the
-// K loop the gate and up results of 64 tokens at a time go through LDS; each
-// wavefront then applies SiLU(g) * u to 16 of them and writes them in the
+// Grid nchunk * I/128 workgroups of 256 threads, chunks fastest.  Wave w: matrix
+// w & 1 (gate, up) of row block 2 x + (w >> 1), x the workgroup's row-block pair.
+// After the K loop the gate and up results of one row block at a time go through
+// LDS (64 tokens x 64 rows each, as many passes as 64-token groups); each
+// wavefront then applies SiLU(g) * u to 16 of the tokens and writes them in the
 // activation format (one 64-column group per token).
 template <class F, int MT>
 __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
@@ -368,9 +369,9 @@ __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
     __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kBytes];
     int e, p0, nt;
     if (!pf_chunk<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;  // uniform over the workgroup
-    const int rb = (int)(blockIdx.x / a.nchunk);
+    const int rbg = (int)(blockIdx.x / a.nchunk);
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const int mat = wv >> 1, t0 = 2 * (wv & 1);
+    const int mat = wv & 1, half = wv >> 1, rb = 2 * rbg + half;
     const Planes W = planes(mat ? a.w1 : a.w0, e);
     half_t *abuf = (half_t *)smem;
     const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
@@ -378,53 +379,61 @@ __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
     stage.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
 #pragma unroll
     for (int h = 0; h < R; h++) stage.off[h] = a.d.rows[p0 + min(r + 64 * h, nt - 1)] * a.H * 2 + 32 * q;
-    f32x4 acc[2][MT];
+    f32x4 acc[kPfTiles][MT];
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++)
+    for (int tt = 0; tt < kPfTiles; tt++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    pf_loop<F, MT>(W, rb, t0, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q, acc);
+    pf_loop<F, MT>(W, rb, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q, acc);
 
-    // results * the tokens' descales -> LDS [mat][token][row], 64 tokens at a time
+    // results * the tokens' descales -> LDS [mat][token][row]: one row block and 64
+    // tokens per pass
     float *res = (float *)smem;
+    float dv[MT][4];
 #pragma unroll
-    for (int h = 0; h < R; h++) {
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int mq = 0; mq < 4; mq++) {
-            const int mt = 4 * h + mq;
+        for (int i = 0; i < 4; i++) dv[mt][i] = a.x.ds[a.d.rows[p0 + min(16 * mt + 4 * g + i, nt - 1)]];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 16 * mq + 4 * g + i;
-                const float dv = a.x.ds[a.d.rows[p0 + min(64 * h + m, nt - 1)]];
+    for (int hb = 0; hb < 2; hb++) {
 #pragma unroll
-                for (int tt = 0; tt < 2; tt++)
-                    res[(mat * 64 + m) * (kRowBlock + 1) + 16 * (t0 + tt) + n] = acc[tt][mt][i] * dv;
+        for (int h = 0; h < R; h++) {
+            if (half == hb) {
+#pragma unroll
+                for (int mq = 0; mq < 4; mq++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int m = 16 * mq + 4 * g + i;
+#pragma unroll
+                        for (int tt = 0; tt < kPfTiles; tt++)
+                            res[(mat * 64 + m) * (kRowBlock + 1) + 16 * tt + n] = acc[tt][4 * h + mq][i] * dv[4 * h + mq][i];
+                    }
             }
-        }
-        __syncthreads();
-        for (int m = 16 * wv; m < 16 * wv + 16; m++) {  // uniform per wavefront
-            const float gv = res[m * (kRowBlock + 1) + lane], uv = res[(64 + m) * (kRowBlock + 1) + lane];
-            const float v = gate_act(gv, a.use_gelu) * uv;
-            const float sc = pow2_scale(wave_max(fabsf(v)));
-            if (64 * h + m < nt) {
-                const size_t pos = (size_t)p0 + 64 * h + m;
-                a.act.q[pos * a.I + (size_t)kStep * rb + mma_pos(lane)] = (half_t)(v * sc);
-                if (lane == 0) a.act.ds[(size_t)rb * a.act.ld + pos] = 1.0f / sc;
+            __syncthreads();
+            const int rbo = 2 * rbg + hb;
+            for (int m = 16 * wv; m < 16 * wv + 16; m++) {  // uniform per wavefront
+                const float gv = res[m * (kRowBlock + 1) + lane], uv = res[(64 + m) * (kRowBlock + 1) + lane];
+                const float v = gate_act(gv, a.use_gelu) * uv;
+                const float sc = pow2_scale(wave_max(fabsf(v)));
+                if (64 * h + m < nt) {
+                    const size_t pos = (size_t)p0 + 64 * h + m;
+                    a.act.q[pos * a.I + (size_t)kStep * rbo + mma_pos(lane)] = (half_t)(v * sc);
+                    if (lane == 0) a.act.ds[(size_t)rbo * a.act.ld + pos] = 1.0f / sc;
+                }
             }
+            __syncthreads();
         }
-        __syncthreads();
     }
 }
 
 // ---------------------------------------------------------------- down
 
-// Grid nchunk * H/128 workgroups of 256 threads, chunks fastest.  Wave w: row block
-// 2 x + (w >> 1), tiles 2 (w & 1) and 2 (w & 1) + 1.  Before the K loop the
-// workgroup finds each position's largest descale over the I/64 groups (the row
-// reference); staging scales every group to it, and the results are multiplied by
-// it once at the end.  Positions past the group's end are computed on the next
-// group's (or, past the last position, the last position's) activations and not
-// stored.
+// Grid nchunk * H/256 workgroups of 256 threads, chunks fastest.  Wave w: row block
+// 4 x + w.  Before the K loop the workgroup finds each position's largest descale
+// over the I/64 groups (the row reference); staging scales every group to it, and
+// the results are multiplied by it once at the end.  Positions past the group's
+// end are computed on the next group's (or, past the last position, the last
+// position's) activations and not stored.
 template <class F, int MT>
 __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
 {
@@ -435,7 +444,7 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
     if (!pf_chunk<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;
     const int rbg = (int)(blockIdx.x / a.nchunk);
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const int rb = 2 * rbg + (wv >> 1), t0 = 2 * (wv & 1);
+    const int rb = 4 * rbg + wv;
     const Planes W = planes(a.w0, e);
     const int G = a.I / kStep, ld = a.x.ld;
     for (int m = threadIdx.x; m < 16 * MT; m += 256) {  // the row references
@@ -457,12 +466,12 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
         stage.doff[h] = pos * 4;
         stage.inv_ref[h] = 1.0f / ref[r + 64 * h];
     }
-    f32x4 acc[2][MT];
+    f32x4 acc[kPfTiles][MT];
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++)
+    for (int tt = 0; tt < kPfTiles; tt++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    pf_loop<F, MT>(W, rb, t0, a.I / kStep, lane, stage, (half_t *)smem, r * kAStride + 16 * q, acc);
+    pf_loop<F, MT>(W, rb, a.I / kStep, lane, stage, (half_t *)smem, r * kAStride + 16 * q, acc);
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
@@ -471,23 +480,23 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
             if (m < nt) {
                 float *yp = a.ypart + ((size_t)p0 + m) * a.H + (size_t)kRowBlock * rb + n;
 #pragma unroll
-                for (int tt = 0; tt < 2; tt++) yp[16 * (t0 + tt)] = acc[tt][mt][i] * ref[m];
+                for (int tt = 0; tt < kPfTiles; tt++) yp[16 * tt] = acc[tt][mt][i] * ref[m];
             }
         }
 }
 
 // ------------------------------------------------------------- launchers
 
-bool grouped_supported(int H, int I) { return H % 128 == 0 && I % 64 == 0; }
+bool grouped_supported(int H, int I) { return H % 256 == 0 && I % 128 == 0; }
 
 template <class F, int MT>
 static int launch_pf(const PfArgs &a, bool gateup, hipStream_t st)
 {
     if (gateup) {
-        const size_t wgs = (size_t)a.nchunk * (a.I / kRowBlock);
+        const size_t wgs = (size_t)a.nchunk * (a.I / (2 * kRowBlock));
         hipLaunchKernelGGL((k_pf_gateup<F, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     } else {
-        const size_t wgs = (size_t)a.nchunk * (a.H / (2 * kRowBlock));
+        const size_t wgs = (size_t)a.nchunk * (a.H / (4 * kRowBlock));
         hipLaunchKernelGGL((k_pf_down<F, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     }
     ANEDVD_HIP(hipGetLastError());
