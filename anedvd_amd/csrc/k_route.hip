@@ -401,13 +401,28 @@ __device__ void act_prep_wave(const float *__restrict__ x, int rows, int K, cons
 {
     if (w >= (size_t)rows) return;
     const float *xr = x + w * K;
+    const int G = K / 64;
+    constexpr int B = 16;  // groups whose loads are issued together
     float m = 0.0f;
-    for (int c = lane; c < K; c += 64) m = fmaxf(m, fabsf(xr[c]));
+    for (int g0 = 0; g0 < G; g0 += B) {
+        float v[B];
+#pragma unroll
+        for (int b = 0; b < B; b++) v[b] = g0 + b < G ? xr[64 * (g0 + b) + lane] : 0.0f;
+#pragma unroll
+        for (int b = 0; b < B; b++) m = fmaxf(m, fabsf(v[b]));
+    }
     const float sc = pow2_scale(wave_max(m)), inv = 1.0f / sc;
     half_t *q = xq.q + w * K;
-    for (int g = 0; g < K / 64; g++) {
-        q[64 * g + mma_pos(lane)] = (half_t)(xr[64 * g + lane] * sc);
-        if (lane == 0) xq.ds[(size_t)g * xq.ld + w] = inv;
+    for (int g0 = 0; g0 < G; g0 += B) {
+        float v[B];
+#pragma unroll
+        for (int b = 0; b < B; b++) v[b] = g0 + b < G ? xr[64 * (g0 + b) + lane] : 0.0f;
+#pragma unroll
+        for (int b = 0; b < B; b++)
+            if (g0 + b < G) {
+                q[64 * (g0 + b) + mma_pos(lane)] = (half_t)(v[b] * sc);
+                if (lane == 0) xq.ds[(size_t)(g0 + b) * xq.ld + w] = inv;
+            }
     }
 }
 
@@ -438,6 +453,7 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a)
         return;
     }
     load_exp_table(tab);
+    if ((int)blockIdx.x * 16 + 4 * wv >= a.T) return;  // a wavefront with no token left (uniform)
     route_token_row(a.logits, blockIdx.x * 16 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx,
                     nullptr, tab);
 }
@@ -456,7 +472,8 @@ __global__ __launch_bounds__(kDispThreads) void k_route_dispatch(RouteArgs a, Di
     }
     load_exp_table(tab);
     for (int t0 = 0; t0 < a.T; t0 += kDispThreads / 16)
-        route_token_row(a.logits, t0 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx, idx_s, tab);
+        if (t0 + 4 * wv < a.T)  // wavefronts with no token left skip the routing (uniform)
+            route_token_row(a.logits, t0 + (int)(threadIdx.x >> 4), a.T, a.E, a.k, a.norm, a.probs, a.idx, idx_s, tab);
     __syncthreads();
     dispatch_block<kDispThreads>(idx_s, a.T, a.k, a.E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, d.chunks,
                                  d.chunk, s);

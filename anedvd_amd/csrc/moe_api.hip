@@ -851,6 +851,38 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
         for (int s = 0; s < 6; s++) kernel_ms[s] = (float)(acc[s] / iters);
         for (auto &e : ev) (void)hipEventDestroy(e);
     }
+    if (kernel_ms && (flags & ANEDVD_TIME_EXPERT_SOLO)) {
+        // The routed expert products alone: `iters` back-to-back launches of the
+        // gate/up (then the down) kernels over the rotated layers, reading the
+        // dispatch, activations and gate/up output the last call left in place (the
+        // calls above routed the same inputs).  Events bracket each loop only.
+        const int H = layers[0]->H, I = layers[0]->I, P = (int)T * layers[0]->k;
+        hipEvent_t a = nullptr, b = nullptr;
+        ANEDVD_HIP(hipEventCreate(&a));
+        ANEDVD_HIP(hipEventCreate(&b));
+        int src = ANEDVD_OK;
+        for (int s = 0; s < 2 && src == ANEDVD_OK; s++) {
+            auto launch = [&](int i) -> int {
+                const anedvd_moe_layer *L = layers[(size_t)i % n_layers];
+                return s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act,
+                                                     L->gelu, st)
+                              : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart, st);
+            };
+            for (int i = 0; i < warmup && src == ANEDVD_OK; i++) src = launch(i);
+            if (src == ANEDVD_OK && hipEventRecord(a, st) != hipSuccess) src = ANEDVD_E_HIP;
+            for (int i = 0; i < iters && src == ANEDVD_OK; i++) src = launch(i);
+            float x = 0.0f;
+            if (src == ANEDVD_OK && (hipEventRecord(b, st) != hipSuccess || hipEventSynchronize(b) != hipSuccess ||
+                                     hipEventElapsedTime(&x, a, b) != hipSuccess)) {
+                set_error("time_forward: expert timing failed");
+                src = ANEDVD_E_HIP;
+            }
+            kernel_ms[1 + s] = x / iters;
+        }
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        if (src != ANEDVD_OK) return src;
+    }
     return ANEDVD_OK;
 }
 

@@ -5,14 +5,16 @@ Workload: one Qwen3-30B-A3B-shaped MoE layer (hidden 2048, 128 experts of SwiGLU
 batch 64 with i.i.d. U(0,1) router logits (the router GEMV is not part of this
 workload).  A step is one layer forward over the batch (route, dispatch, fused
 dequant + gate/up, fused dequant + down, combine) with the inputs already
-resident in HBM, submitted as one HIP graph per call (the directly launched time
-is reported beside it).  Steps rotate over `--copies` device copies of the layer
-so the 256 MB Infinity Cache cannot serve the weights between steps.
+resident in HBM, its kernels launched directly on the library's stream (the
+time with one HIP graph per call is reported beside it).  Steps rotate over
+`--copies` device copies of the layer so the 256 MB Infinity Cache cannot serve
+the weights between steps.
 
 Prints ONE JSON line (rank 0, N=1) with the throughput, the roofline of the
-dominant kernel (the fused dequant + gate/up GEMV) measured with HIP events on
-the library's stream, and the CPU restatement of the reference path timed on
-the host cores on a bounded sample of the same batch.
+dominant kernel (the fused dequant + gate/up GEMV: its mean launch time over
+back-to-back launches, HIP events on the library's stream), and the CPU
+restatement of the reference path timed on the host cores on a bounded sample of
+the same batch.
 """
 from __future__ import annotations
 
@@ -85,7 +87,7 @@ PREFILL = {
 
 def run_prefill(name: str, ctx, warmup: int, steps: int) -> dict:
     """One prefill-sized layer call (route + dispatch + grouped expert products +
-    combine, router logits given), two rotated layer copies, HIP graph per step;
+    combine, router logits given), two rotated layer copies, kernels launched directly;
     reports useful MFMA-path FLOP/s against the fp16 dense peak."""
     from anedvd_amd import moe, synth
     from anedvd_amd import workloads as W
@@ -100,8 +102,9 @@ def run_prefill(name: str, ctx, warmup: int, steps: int) -> dict:
     _, st = layers[0].forward(h, lg, stats=True)
     d_h, d_lg = ctx.to_device(h), ctx.to_device(lg)
     d_out = ctx.alloc(T * spec.hidden * 4)
-    ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps, graph=True)
+    ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps)
     _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, steps, stages=True)
+    _, solo = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, steps, solo=True)
     for p in (d_h, d_lg, d_out):
         ctx.free(p)
     for l in layers:
@@ -114,10 +117,14 @@ def run_prefill(name: str, ctx, warmup: int, steps: int) -> dict:
          "TFLOPs": round(flops / t / 1e12, 2), "mfma_frac": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
          "layer_GBps": round(lbytes / t / 1e9, 1), "hbm_frac": round(lbytes / t / 1e9 / HBM_PEAK_GBS, 4),
          "stage_ms": dict(zip(["route_dispatch", "gate_up", "down", "shared", "combine", "total"],
-                              [round(x, 4) for x in stages]))}
+                              [round(x, 4) for x in stages])),
+         "solo_launch_ms": {"gate_up": round(solo[1], 4), "down": round(solo[2], 4)}}
+    gu_flops = 2 * 2 * T * spec.k * spec.hidden * spec.inter  # the routed gate and up products
+    r["gate_up_mfma_frac"] = round(gu_flops / (solo[1] / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
     log(f"[bench] prefill {name}: {r['ms_per_step'] * 1e3:.0f} us/step, {r['TFLOPs']} TFLOP/s "
         f"({100 * r['mfma_frac']:.1f}% of fp16 MFMA peak), {r['layer_GBps']} GB/s, touched {r['touched_experts']}, "
-        f"max group {r['max_group']}, stages {r['stage_ms']} (setup {time.perf_counter() - t0:.1f} s)")
+        f"max group {r['max_group']}, event stages {r['stage_ms']}, solo launches {r['solo_launch_ms']}, "
+        f"gate/up {100 * r['gate_up_mfma_frac']:.1f}% of MFMA peak (setup {time.perf_counter() - t0:.1f} s)")
     return r
 
 
@@ -180,23 +187,25 @@ def main():
         out_host, st = layers[0].forward(h, lg, stats=True)
         d_h, d_lg = ctx.to_device(h), ctx.to_device(lg)
         d_out = ctx.alloc(T * spec.hidden * 4)
-        ms_eager, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps)
-        ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps, graph=True)
+        ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps)
+        ms_graph, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps, graph=True)
         _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 2, steps, stages=True)
+        _, solo = moe.time_forward(layers, d_h, T, d_lg, d_out, 2, steps, solo=True)
         for p in (d_h, d_lg, d_out):
             ctx.free(p)
         touched = st["touched_experts"]
         layer_s = ms / 1e3 / steps
         lbytes = spec.call_bytes(touched, T, with_router=False)
-        r = {"batch": T, "touched_experts": touched, "ms_per_step": ms / steps, "eager_ms_per_step": ms_eager / steps,
+        r = {"batch": T, "touched_experts": touched, "ms_per_step": ms / steps, "graph_ms_per_step": ms_graph / steps,
              "tokens_per_s": T / layer_s, "layer_GBps": lbytes / layer_s / 1e9,
              "layer_hbm_frac": lbytes / layer_s / 1e9 / HBM_PEAK_GBS,
              "stage_ms": dict(zip(["route_dispatch", "gate_up", "down", "shared", "combine", "total"],
-                                  [round(x, 5) for x in stages]))}
-        log(f"[bench] B={T}: {ms / steps * 1e3:.1f} us/step (graph; {ms_eager / steps * 1e3:.1f} eager), "
+                                  [round(x, 5) for x in stages])),
+             "solo_launch_ms": {"gate_up": round(solo[1], 5), "down": round(solo[2], 5)}}
+        log(f"[bench] B={T}: {ms / steps * 1e3:.1f} us/step ({ms_graph / steps * 1e3:.1f} as graphs), "
             f"{r['tokens_per_s']:.0f} tok/s, "
             f"{r['layer_GBps']:.0f} GB/s ({100 * r['layer_hbm_frac']:.1f}% of HBM), touched {touched}, "
-            f"stages {r['stage_ms']}")
+            f"event stages {r['stage_ms']}, solo launches {r['solo_launch_ms']}")
         return r, h, lg, out_host
 
     sweep = []
@@ -205,7 +214,7 @@ def main():
 
     head, h, lg, out_gpu = run(B, args.steps, args.warmup)
     ms_step = head["ms_per_step"]
-    gu_ms = head["stage_ms"]["gate_up"]
+    gu_ms = head["solo_launch_ms"]["gate_up"]
     gu_bytes = gateup_bytes(spec, head["touched_experts"], B)
     achieved = gu_bytes / (gu_ms / 1e3) / 1e9
     roofline = {"bound": "hbm", "kernel": "k_mm_gateup<MQ8_0> (fused Q8_0 dequant + gate/up + SwiGLU on MFMA)",
@@ -235,9 +244,10 @@ def main():
                    "experts": spec.n_experts, "inter": spec.inter, "top_k": spec.k, "batch": B,
                    "weights": "q8_0", "layer_copies_rotated": args.copies,
                    "arithmetic": "f16 dot products of exact dequantised weights, f32 accumulation"},
-        "eager_ms_per_step": round(head["eager_ms_per_step"], 5),
+        "graph_ms_per_step": round(head["graph_ms_per_step"], 5),
         "layer_GBps": round(head["layer_GBps"], 1), "layer_hbm_frac": round(head["layer_hbm_frac"], 4),
         "touched_experts": head["touched_experts"], "stage_ms": head["stage_ms"],
+        "solo_launch_ms": head["solo_launch_ms"],
         "roofline": roofline, "cpu_baseline": cpu, "parity_vs_oracle": parity,
         "sweep": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()} for r in sweep],
         "prefill": prefill,

@@ -173,8 +173,12 @@ int anedvd_moe_synchronize(anedvd_moe_ctx *ctx);
  * a further pass of `iters` directly launched calls records events around every
  * stage and kernel_ms[0..5] receives the mean milliseconds per call of: route
  * (router + route + dispatch), expert gate/up, expert down, shared expert,
- * combine, and the whole call. */
+ * combine, and the whole call.  With ANEDVD_TIME_EXPERT_SOLO as well,
+ * kernel_ms[1] and kernel_ms[2] are instead the mean milliseconds of one routed
+ * gate/up (resp. down) launch, timed over `iters` back-to-back launches of that
+ * stage alone (same layer rotation, the last call's dispatch and activations). */
 #define ANEDVD_TIME_GRAPH 1
+#define ANEDVD_TIME_EXPERT_SOLO 2
 int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, const float *d_h,
                             size_t n_tokens, const float *d_logits, float *d_out, int warmup,
                             int iters, int flags, float *ms, float *kernel_ms);
