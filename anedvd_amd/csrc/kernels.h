@@ -37,8 +37,8 @@ int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_
                  const float *d_x, int H, const ActQ &xq, hipStream_t st);
 int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &d, hipStream_t st);
 // Route, dispatch and (d_x non-null) activation conversion of one forward call:
-// a single launch whose first workgroup routes and dispatches when T*k is small,
-// else a parallel route launch followed by the dispatch.
+// the route launch (one wavefront per token, the conversion beside it), then the
+// one-workgroup dispatch launch.
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                               const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st);
 int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st);

@@ -116,6 +116,30 @@ def test_moe_route_bit_exact(ctx, E, k, norm, T):
         assert np.array_equal(bits(p[t]), bits(op)), t
 
 
+@pytest.mark.parametrize("E", [60, 128, 256])
+def test_moe_route_special_values(ctx, E):
+    """NaN, +-inf, underflowing exps and all-tied rows route as cpu.moeRoute does
+    (cpu.zig:1244-1288: @max skips NaN, NaN probabilities are never chosen, an
+    empty slot gets (0, expert 0))."""
+    base = np.linspace(-3.0, 3.0, E).astype(np.float32)
+    rows = [base.copy()]
+    r = base.copy(); r[5] = np.nan; r[E - 3] = np.nan; rows.append(r)
+    r = np.full(E, -np.inf, np.float32); r[3] = 1.0; rows.append(r)      # one finite logit
+    rows.append(np.full(E, np.nan, np.float32))                           # every logit NaN
+    rows.append(np.full(E, -np.inf, np.float32))                          # every logit -inf
+    r = np.zeros(E, np.float32); r[9] = np.inf; rows.append(r)            # +inf: the sum is NaN
+    r = np.zeros(E, np.float32); r[::2] = -200.0; rows.append(r)          # half the exps underflow
+    rows.append(np.zeros(E, np.float32))                                  # all tied
+    r = base.copy(); r[-1] = 7.0; r[0] = 7.0; rows.append(r)              # tie between first and last
+    lg = np.stack(rows)
+    for k, norm in [(8, True), (8, False), (1, False), (32, True)]:
+        p, idx = ctx.moe_route(lg, k, norm)
+        for t in range(len(rows)):
+            op, oi = O.moe_route(lg[t], k, norm)
+            assert np.array_equal(idx[t], oi), (t, k, norm)
+            assert np.array_equal(bits(p[t]), bits(op)), (t, k, norm)
+
+
 @pytest.mark.parametrize("T,E,k", [(1, 8, 2), (16, 8, 2), (64, 128, 8), (512, 128, 8), (2048, 8, 2), (1024, 64, 6)])
 def test_dispatch_bit_exact(ctx, T, E, k):
     lg = synth.normal(11, T, T * E).astype(np.float32).reshape(T, E)
