@@ -709,9 +709,12 @@ static int choose_ks(int units, int spu, long wg_per_ks, int waves_per_k, int mi
 MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u)
 {
     MmPlan p{};
-    // The grouped GEMM (64-token chunks) once the groups average 32 tokens; the
-    // chunks then give the grid its parallelism and K is not split.
-    p.mt = (P >= 32 * max_u && grouped_supported(H, I)) ? 4 : 1;
+    // The grouped GEMM (64-token chunks) once the groups average 32 tokens and its
+    // gate/up grid has a workgroup per CU at least; the chunks then give the grid
+    // its parallelism and K is not split.  (A single shared expert at 32 tokens
+    // would be 22 workgroups: it measured 105 us against the decode kernels' split K.)
+    const long pf_wgs = (long)((P + 63) / 64) * (I / 128);
+    p.mt = (P >= 32 * max_u && grouped_supported(H, I) && pf_wgs >= 256) ? 4 : 1;
     p.chunk = 16 * p.mt;
     p.nchunk = P / p.chunk + max_u;
     if (p.mt > 1) {

@@ -78,42 +78,74 @@ def cpu_baseline(spec, L, h, logits, budget_s: float):
                       f"SwiGLU GEMVs), first {n} tokens of the batch, {dt:.1f} s, gcc -O2, 1 thread"}, ref, n
 
 
-PREFILL = {
-    # name: (spec attribute, tokens, routing)
-    "qwen3-q4km-512": ("QWEN3_30B_A3B_Q4_K_M", 512, "zipf"),
-    "mixtral-q4_0-2048": ("MIXTRAL_8X7B_Q4_0", 2048, "normal"),
+CONFIGS = {
+    # name: (spec attribute, tokens, routing, device copies rotated, layers timed as a stack)
+    "qwen3-q4km-512": ("QWEN3_30B_A3B_Q4_K_M", 512, "zipf", 2, 1),
+    "mixtral-q4_0-2048": ("MIXTRAL_8X7B_Q4_0", 2048, "normal", 3, 1),
+    "mixtral-q4_0-1": ("MIXTRAL_8X7B_Q4_0", 1, "normal", 3, 1),
+    "deepseek-v2-lite-32-x26": ("DEEPSEEK_V2_LITE_Q8_0", 32, "uniform", 26, 26),
+    "deepseek-v2-lite-1024-x26": ("DEEPSEEK_V2_LITE_Q8_0", 1024, "uniform", 26, 26),
 }
+_LAYERS = {}  # spec name -> resident layer copies, shared by the configs of one spec
 
 
-def run_prefill(name: str, ctx, warmup: int, steps: int) -> dict:
-    """One prefill-sized layer call (route + dispatch + grouped expert products +
-    combine, router logits given), two rotated layer copies, kernels launched directly;
-    reports useful MFMA-path FLOP/s against the fp16 dense peak."""
+def resident_layers(ctx, spec, copies: int) -> list:
+    """`copies` device copies of one synthetic layer of `spec` (seed 0): each copy
+    is a distinct HBM allocation, so rotating through them defeats the Infinity
+    Cache as a stack of distinct layers would."""
+    from anedvd_amd import moe, synth
+    have = _LAYERS.setdefault(spec.name, [])
+    if len(have) < copies:
+        L = synth.make_layer(spec, seed=0)
+        while len(have) < copies:
+            have.append(moe.MoeLayer(ctx, spec, L))
+    return have[:copies]
+
+
+def free_layers():
+    for ls in _LAYERS.values():
+        for l in ls:
+            l.free()
+    _LAYERS.clear()
+
+
+def run_config(name: str, ctx, warmup: int, steps: int) -> dict:
+    """One workload beside the headline: a layer call (route + dispatch + expert
+    products + shared expert + combine, router logits given), rotated over device
+    copies of the layer.  For a stack, call j runs layer j mod n of n distinct
+    resident layers and the stack time is n times the mean call.  Reports tokens/s,
+    the layer's algorithmic HBM bytes/s and useful MFMA-path FLOP/s against the peaks."""
     from anedvd_amd import moe, synth
     from anedvd_amd import workloads as W
-    attr, T, routing = PREFILL[name]
+    attr, T, routing, copies, stack = CONFIGS[name]
     spec = getattr(W, attr)
     t0 = time.perf_counter()
-    L = synth.make_layer(spec, seed=0)
-    layers = [moe.MoeLayer(ctx, spec, L) for _ in range(2)]
+    layers = resident_layers(ctx, spec, copies)
     h = synth.activations(spec, T, seed=1)
-    lg = synth.zipf_logits(spec, T, seed=1) if routing == "zipf" else synth.activations(spec, T, seed=2)[:, :spec.n_experts]
+    if routing == "zipf":
+        lg = synth.zipf_logits(spec, T, seed=1)
+    elif routing == "uniform":
+        lg = synth.uniform_logits(spec, T, seed=1)
+    else:
+        lg = synth.activations(spec, T, seed=2)[:, :spec.n_experts]
     lg = np.ascontiguousarray(lg, dtype=np.float32)
     _, st = layers[0].forward(h, lg, stats=True)
     d_h, d_lg = ctx.to_device(h), ctx.to_device(lg)
     d_out = ctx.alloc(T * spec.hidden * 4)
+    steps = max(steps, 2 * copies) // copies * copies
+    warmup = max(warmup, copies)
     ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps)
     _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, steps, stages=True)
     _, solo = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, steps, solo=True)
     for p in (d_h, d_lg, d_out):
         ctx.free(p)
-    for l in layers:
-        l.free()
     t = ms / 1e3 / steps
     flops = spec.call_flops(T, with_router=False)
     lbytes = spec.call_bytes(st["touched_experts"], T, with_router=False)
-    r = {"workload": spec.name, "tokens": T, "routing": routing, "touched_experts": st["touched_experts"],
-         "max_group": st["max_group"], "ms_per_step": round(ms / steps, 4), "tokens_per_s": round(T / t, 1),
+    r = {"name": name, "workload": spec.name, "tokens": T, "routing": routing, "layer_copies_rotated": copies,
+         "touched_experts": st["touched_experts"], "max_group": st["max_group"],
+         "path": "grouped GEMM" if st["path"] else "decode GEMV",
+         "ms_per_call": round(ms / steps, 4), "tokens_per_s": round(T / t, 1),
          "TFLOPs": round(flops / t / 1e12, 2), "mfma_frac": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
          "layer_GBps": round(lbytes / t / 1e9, 1), "hbm_frac": round(lbytes / t / 1e9 / HBM_PEAK_GBS, 4),
          "stage_ms": dict(zip(["route_dispatch", "gate_up", "down", "shared", "combine", "total"],
@@ -121,10 +153,16 @@ def run_prefill(name: str, ctx, warmup: int, steps: int) -> dict:
          "solo_launch_ms": {"gate_up": round(solo[1], 4), "down": round(solo[2], 4)}}
     gu_flops = 2 * 2 * T * spec.k * spec.hidden * spec.inter  # the routed gate and up products
     r["gate_up_mfma_frac"] = round(gu_flops / (solo[1] / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
-    log(f"[bench] prefill {name}: {r['ms_per_step'] * 1e3:.0f} us/step, {r['TFLOPs']} TFLOP/s "
-        f"({100 * r['mfma_frac']:.1f}% of fp16 MFMA peak), {r['layer_GBps']} GB/s, touched {r['touched_experts']}, "
-        f"max group {r['max_group']}, event stages {r['stage_ms']}, solo launches {r['solo_launch_ms']}, "
-        f"gate/up {100 * r['gate_up_mfma_frac']:.1f}% of MFMA peak (setup {time.perf_counter() - t0:.1f} s)")
+    if stack > 1:
+        r["stack_layers"] = stack
+        r["stack_ms"] = round(ms / steps * stack, 4)
+        r["stack_tokens_per_s"] = round(T / (t * stack), 1)
+    log(f"[bench] {name}: {r['ms_per_call'] * 1e3:.1f} us/call ({r['path']}), {r['tokens_per_s']:.0f} tok/s, "
+        f"{r['TFLOPs']} TFLOP/s ({100 * r['mfma_frac']:.1f}% of fp16 MFMA peak), {r['layer_GBps']} GB/s "
+        f"({100 * r['hbm_frac']:.1f}% of HBM), touched {r['touched_experts']}, max group {r['max_group']}"
+        + (f", {stack}-layer stack {r['stack_ms']:.3f} ms" if stack > 1 else "")
+        + f", event stages {r['stage_ms']}, solo launches {r['solo_launch_ms']} "
+        f"(setup {time.perf_counter() - t0:.1f} s)")
     return r
 
 
@@ -137,9 +175,9 @@ def main():
     ap.add_argument("--copies", type=int, default=8, help="device copies of the layer rotated per step")
     ap.add_argument("--sweep", default="1,8,32", help="extra decode batches reported beside the headline ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
-    ap.add_argument("--prefill", default="qwen3-q4km-512,mixtral-q4_0-2048",
-                    help="prefill workloads reported beside the headline ('' = none)")
-    ap.add_argument("--prefill-only", action="store_true", help="run only the prefill workloads (profiling)")
+    ap.add_argument("--configs", default=",".join(CONFIGS),
+                    help="further workloads reported beside the headline ('' = none): " + ", ".join(CONFIGS))
+    ap.add_argument("--configs-only", action="store_true", help="run only the --configs workloads (profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (a plain copy kernel of known size, "
                          "for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -164,10 +202,11 @@ def main():
         log(f"[bench] calibration: 3 device copies of {args.calibrate_copy} MiB")
         del src, dst
 
-    if args.prefill_only:
+    if args.configs_only:
         ctx = moe.MoeContext(0)
-        out = [run_prefill(name, ctx, args.warmup, args.steps) for name in args.prefill.split(",") if name.strip()]
-        print(json.dumps({"prefill": out}), flush=True)
+        out = [run_config(name, ctx, args.warmup, args.steps) for name in args.configs.split(",") if name.strip()]
+        print(json.dumps({"configs": out}), flush=True)
+        free_layers()
         ctx.close()
         return
 
@@ -223,9 +262,10 @@ def main():
                 "traffic": read_traffic("pmc_k_mm_gateup_q8_0_decode_b64.md"),
                 "bytes_per_launch": gu_bytes, "avg_launch_ms": gu_ms}
 
-    prefill = []
-    for name in [x for x in args.prefill.split(",") if x.strip()]:
-        prefill.append(run_prefill(name, ctx, args.warmup, max(10, args.steps // 10)))
+    configs = []
+    for name in [x for x in args.configs.split(",") if x.strip()]:
+        configs.append(run_config(name, ctx, args.warmup, max(10, args.steps // 4)))
+    free_layers()
 
     cpu = None
     parity = None
@@ -250,7 +290,7 @@ def main():
         "solo_launch_ms": head["solo_launch_ms"],
         "roofline": roofline, "cpu_baseline": cpu, "parity_vs_oracle": parity,
         "sweep": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()} for r in sweep],
-        "prefill": prefill,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
     for l in layers:

@@ -232,6 +232,16 @@ def test_forward_shared_expert_deepseek_shape(ctx):
     assert err <= REL_L2_TOL
 
 
+def test_forward_shared_expert_grouped(ctx):
+    """A 512-token call whose shared expert (width 4096) takes the grouped GEMM
+    while the small routed experts take the decode kernels."""
+    spec = dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="shared-grouped", hidden=512, inter=512, n_experts=8,
+                               k=2, shared_inter=4096)
+    _, _, err, st = _forward_case(ctx, spec, 512, seed=12)
+    assert err <= REL_L2_TOL
+    assert st["path"] == 0
+
+
 def test_forward_gated_shared_expert(ctx):
     spec = dataclasses.replace(W.TINY_Q8_0, shared_inter=1024, shared_gated=True)
     _, _, err, _ = _forward_case(ctx, spec, 16, seed=6)
@@ -285,8 +295,9 @@ def test_forward_block_formats(ctx, types, T):
 @pytest.mark.parametrize("types", FORMATS, ids=lambda t: "/".join(W.TYPE_NAMES[x] for x in t))
 def test_forward_grouped_large_groups(ctx, types):
     """Groups of ~300 tokens (600 tokens, top-2 of 4 experts) take the grouped GEMM:
-    several 64-token chunks per expert and a partial last one."""
-    spec = dataclasses.replace(W.QWEN3_30B_A3B_Q4_K_M, name="formats", hidden=1024, inter=512, n_experts=4, k=2,
+    several 64-token chunks per expert and a partial last one (expert width 2048, so
+    the grouped grid has the 256 workgroups the planner asks for)."""
+    spec = dataclasses.replace(W.QWEN3_30B_A3B_Q4_K_M, name="formats", hidden=512, inter=2048, n_experts=4, k=2,
                                gate_type=types[0], up_type=types[1], down_type=types[2], scale_sigma=0.01)
     _, _, err, st = _forward_case(ctx, spec, 600, seed=11)
     assert err <= REL_L2_TOL
