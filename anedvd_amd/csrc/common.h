@@ -172,6 +172,14 @@ __device__ inline float wave_max(float v)
     return v;
 }
 
+// cpu.sigmoid (cpu.zig:1223-1230): the clamped logistic of the shared expert's gate.
+__device__ inline float shared_sigmoid(float g)
+{
+    if (g >= 0.0f) return 1.0f / (1.0f + __expf(-fminf(g, 80.0f)));
+    const float ex = __expf(fmaxf(g, -80.0f));
+    return ex / (1.0f + ex);
+}
+
 __device__ inline float pow2_scale(float maxabs)
 {
     if (!(maxabs > 0.0f) || !(maxabs < __builtin_inff())) return 1.0f;

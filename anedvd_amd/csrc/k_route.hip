@@ -206,14 +206,14 @@ __device__ void route_wave(const float *__restrict__ lg, int E, int k, int norm,
     }
 }
 
-// Routes token t of `a` on this wavefront (t < T).
-__device__ inline void route_token(const float *__restrict__ logits, int t, int E, int k, int norm,
+// Routes token t on this wavefront (t < T); its k slots start at row t of kk.
+__device__ inline void route_token(const float *__restrict__ logits, int t, int E, int k, int kk, int norm,
                                    float *__restrict__ probs, uint32_t *__restrict__ idx, int lane,
                                    const uint64_t *tab, float *row)
 {
     const float *lg = logits + (size_t)t * E;
-    float *pr = probs + (size_t)t * k;
-    uint32_t *ix = idx + (size_t)t * k;
+    float *pr = probs + (size_t)t * kk;
+    uint32_t *ix = idx + (size_t)t * kk;
     if (E <= 64) route_wave<1>(lg, E, k, norm, pr, ix, lane, tab, row);
     else if (E <= 128) route_wave<2>(lg, E, k, norm, pr, ix, lane, tab, row);
     else route_wave<4>(lg, E, k, norm, pr, ix, lane, tab, row);
@@ -273,7 +273,8 @@ __device__ inline int wave_incl_scan(int v, int)
 // and meta from the per-expert counts in s.cnt (4 experts per lane, E <= 256);
 // s.off gets the offsets.
 __device__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets, int32_t *__restrict__ active,
-                                 int32_t *__restrict__ meta, int32_t *__restrict__ chunks, int chunk, DispLds &s)
+                                 int32_t *__restrict__ meta, int32_t *__restrict__ chunks, int chunk, int n_routed,
+                                 DispLds &s)
 {
     int c[4], tot = 0, nz = 0, mx = 0;
 #pragma unroll
@@ -282,7 +283,7 @@ __device__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets,
         c[q] = e < E ? s.cnt[e] : 0;
         tot += c[q];
         nz += c[q] > 0;
-        mx = max(mx, c[q]);
+        if (n_routed <= 0 || e < n_routed) mx = max(mx, c[q]);
     }
     int nch = 0;
 #pragma unroll
@@ -319,7 +320,7 @@ template <int NTH>
 __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
                                int32_t *__restrict__ rows, int32_t *__restrict__ slots, int32_t *__restrict__ inv,
                                int32_t *__restrict__ active, int32_t *__restrict__ meta, int32_t *__restrict__ chunks,
-                               int chunk, DispLds &s)
+                               int chunk, int n_routed, DispLds &s)
 {
     static_assert(NTH >= 128, "wavefront 0 computes the offsets while the others prefix the bitmap");
     const int P = T * k, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -346,7 +347,7 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
         if (bad) atomicAdd(&s.bad, bad);
         __syncthreads();
         if (wv == 0) {
-            dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, s);
+            dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, s);
         } else {
             for (int e = tid - 64; e < E; e += NTH - 64) {
                 int run = 0;
@@ -385,7 +386,7 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
     }
     if (bad) atomicAdd(&s.bad, bad);
     __syncthreads();
-    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, s);
+    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, s);
     // bitmap words per expert per chunk of entries
     const int W = max(1, kDispWords / E);
     const int C = 32 * W, NW = W * E;
@@ -487,6 +488,9 @@ struct RouteArgs {
     int H;
     ActQ xq;
     int n_route_blocks;
+    int kk;              // slots per token row of probs/idx: k routed + n_sh shared pieces
+    int n_sh;            // shared expert pieces (experts E .. E+n_sh-1), written by the conversion
+    const uint16_t *sh_lin;  // shared gate vector [H] f16, or null (scale 1)
 };
 
 constexpr int kRouteWaves = 4;      // tokens per routing workgroup, one per wavefront
@@ -504,19 +508,38 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a)
     __shared__ __attribute__((aligned(16))) float rows[kRouteWaves][kMaxExperts];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if ((int)blockIdx.x >= a.n_route_blocks) {
-        act_prep_wave(a.x, a.T, a.H, a.xq, (size_t)(blockIdx.x - a.n_route_blocks) * kRouteWaves + wv, lane);
+        const size_t w = (size_t)(blockIdx.x - a.n_route_blocks) * kRouteWaves + wv;
+        act_prep_wave(a.x, a.T, a.H, a.xq, w, lane);
+        if (a.n_sh && w < (size_t)a.T) {
+            // the token's shared slots: experts E .. E+n_sh-1 with its shared scale,
+            // sigmoid(shared_gate_lin . h) (main.zig:512-515) or 1 (engine.zig:1170)
+            float s = 1.0f;
+            if (a.sh_lin) {
+                const float *xr = a.x + w * a.H;
+                float g = 0.0f;
+                for (int i = lane; i < a.H; i += 64) g += f16_bits_to_f32(a.sh_lin[i]) * xr[i];
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o, 64);
+                s = shared_sigmoid(g);
+            }
+            if (lane < a.n_sh) {
+                a.probs[w * a.kk + a.k + lane] = s;
+                a.idx[w * a.kk + a.k + lane] = (uint32_t)(a.E + lane);
+            }
+        }
         return;
     }
     load_exp_table(tab);
     const int t = (int)blockIdx.x * kRouteWaves + wv;
-    if (t < a.T) route_token(a.logits, t, a.E, a.k, a.norm, a.probs, a.idx, lane, tab, rows[wv]);
+    if (t < a.T) route_token(a.logits, t, a.E, a.k, a.kk, a.norm, a.probs, a.idx, lane, tab, rows[wv]);
 }
 
 __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
                                                            Dispatch d)
 {
     __shared__ DispLds s;
-    dispatch_block<kDispThreads>(idx, T, k, E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, d.chunks, d.chunk, s);
+    dispatch_block<kDispThreads>(idx, T, k, E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, d.chunks, d.chunk,
+                                 d.n_routed, s);
 }
 
 __global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ x, int rows, int K, ActQ xq)
@@ -538,7 +561,7 @@ static int check_route_shape(int T, int E, int k)
 }
 
 int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
-                 const float *d_x, int H, const ActQ &xq, hipStream_t st)
+                 const float *d_x, int H, const ActQ &xq, hipStream_t st, const SharedSlots &sh)
 {
     if (T <= 0) return ANEDVD_OK;
     ANEDVD_TRY(check_route_shape(T, E, k));
@@ -546,7 +569,12 @@ int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_
         set_error("route: hidden %d is not a multiple of 64", H);
         return ANEDVD_E_INVALID_SHAPE;
     }
-    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, (T + kRouteWaves - 1) / kRouteWaves};
+    if (sh.n && (!d_x || sh.n > 64 || E + sh.n > kMaxExperts)) {
+        set_error("route: %d shared pieces need the activations and E + pieces <= %d", sh.n, kMaxExperts);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, (T + kRouteWaves - 1) / kRouteWaves,
+                k + sh.n, sh.n, sh.lin};
     const size_t waves = d_x ? (size_t)T : 0;  // activation conversion: one wavefront per token
     const unsigned blocks = (unsigned)(a.n_route_blocks + (waves + kRouteWaves - 1) / kRouteWaves);
     hipLaunchKernelGGL(k_route, dim3(blocks), dim3(256), 0, st, a);
@@ -564,10 +592,11 @@ int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &
 }
 
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
-                              const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st)
+                              const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
+                              const SharedSlots &sh)
 {
-    ANEDVD_TRY(launch_route(d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, st));
-    return launch_dispatch(d_idx, T, k, E, d, st);
+    ANEDVD_TRY(launch_route(d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, st, sh));
+    return launch_dispatch(d_idx, T, k + sh.n, E + sh.n, d, st);
 }
 
 int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st)

@@ -22,6 +22,7 @@ struct ActQ {
 struct Dispatch {
     int32_t *offsets, *rows, *slots, *inv, *active, *meta, *chunks;
     int chunk;
+    int n_routed;  // meta[1] counts experts below this one only (0 = all): merged shared pieces are not groups
 };
 
 // k_dequant.hip
@@ -33,14 +34,21 @@ int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st);
 int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits, hipStream_t st);
 // cpu.moeRoute for T rows of logits; with d_x non-null the same launch also
 // converts x [T][H] to the GEMV activation format `xq`.
+// Shared-expert pieces merged into the routed experts: n pieces, experts E..E+n-1,
+// every token's slots k..k+n-1, scale sigmoid(lin . h) or 1 when lin is null.
+struct SharedSlots {
+    int n = 0;
+    const uint16_t *lin = nullptr;
+};
 int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
-                 const float *d_x, int H, const ActQ &xq, hipStream_t st);
+                 const float *d_x, int H, const ActQ &xq, hipStream_t st, const SharedSlots &sh = {});
 int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &d, hipStream_t st);
 // Route, dispatch and (d_x non-null) activation conversion of one forward call:
 // the route launch (one wavefront per token, the conversion beside it), then the
 // one-workgroup dispatch launch.
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
-                              const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st);
+                              const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
+                              const SharedSlots &sh = {});
 int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st);
 
 // k_mm.hip -- expert products on MFMA

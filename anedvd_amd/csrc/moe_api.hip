@@ -40,6 +40,8 @@ struct Workspace {
 struct anedvd_moe_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    hipStream_t aux = nullptr;            // the shared expert runs here beside the routed experts
+    hipEvent_t fork = nullptr, join = nullptr;
     Workspace ws;
     Workspace io;  // staging for the host-pointer entry points
 };
@@ -51,7 +53,8 @@ struct anedvd_moe_layer {
     QMat gate{}, up{}, down{};
     uint16_t *router = nullptr;
     uint32_t Is = 0;
-    QMat sgate{}, sup{}, sdown{};
+    uint32_t n_sh = 0;  // shared expert merged as n_sh expert-width pieces after the E routed experts
+    QMat sgate{}, sup{}, sdown{};  // the shared expert when it is not merged
     uint16_t *sgate_lin = nullptr;
     uint64_t device_bytes = 0;
     double expert_bytes = 0, shared_bytes = 0;
@@ -85,8 +88,15 @@ int ensure(Workspace &w, size_t bytes, hipStream_t st)
     return ANEDVD_OK;
 }
 
+// A host block copied into the upload staging buffer after the previous ones:
+// `height` rows of `width` bytes, `pitch` bytes apart in host memory.
+struct Seg {
+    const void *src;
+    size_t width, height, pitch;
+};
+
 int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, size_t bytes, hipStream_t st,
-              uint64_t &dev_bytes, const char *what)
+              uint64_t &dev_bytes, const char *what, const std::vector<Seg> &extra = {}, int n_extra = 0)
 {
     const Fmt f = tile_fmt(type);
     if (!mm_supported(type)) {
@@ -103,6 +113,9 @@ int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, si
         set_error("%s: %zu bytes given, %d x %d x %d of type %d needs %zu", what, bytes, n, rows, cols, type, per * n);
         return ANEDVD_E_DIMENSION;
     }
+    // `extra` holds n_extra more matrices of the same shape (a shared expert cut
+    // into expert-width pieces), appended after the n given ones.
+    n += n_extra;
     m.type = type;
     m.rows = rows;
     m.cols = cols;
@@ -125,8 +138,20 @@ int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, si
     if (m.d_stride) ANEDVD_HIP(hipMalloc(&m.d, m.d_stride * n));
     dev_bytes += (m.q_stride + m.s_stride + m.h_stride + m.d_stride) * n;
     uint8_t *staging = nullptr;
-    ANEDVD_HIP(hipMalloc(&staging, bytes));
+    ANEDVD_HIP(hipMalloc(&staging, per * n));
     hipError_t e = hipMemcpyAsync(staging, host, bytes, hipMemcpyHostToDevice, st);
+    size_t off = bytes;
+    for (const Seg &g : extra) {
+        if (e != hipSuccess) break;
+        e = hipMemcpy2DAsync(staging + off, g.width, g.src, g.pitch, g.width, g.height, hipMemcpyHostToDevice, st);
+        off += g.width * g.height;
+    }
+    if (e == hipSuccess && off != per * n) {
+        (void)hipStreamSynchronize(st);
+        (void)hipFree(staging);
+        set_error("%s: %zu bytes staged, %zu expected", what, off, per * n);
+        return ANEDVD_E_DIMENSION;
+    }
     int rc = e == hipSuccess ? launch_repack(m, staging, st) : ANEDVD_E_HIP;
     if (e != hipSuccess) set_error("%s: upload failed: %s", what, hipGetErrorString(e));
     hipError_t e2 = hipStreamSynchronize(st);
@@ -164,15 +189,17 @@ struct Fwd {
     int max_u, P;
 };
 
+// k: slots per token (the routed top-k plus the merged shared pieces for a
+// forward call).  Dispatch arrays cover the E routed experts and the pieces.
 size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base, bool with_io)
 {
-    const int H = L->H, I = L->I, E = L->E, P = T * k;
+    const int H = L->H, I = L->I, E = L->E + L->n_sh, P = T * k;
     Fwd x{};
     x.P = P;
     x.max_u = std::min(E, P);
     x.plan = plan_mm(L->gate.type, L->down.type, H, I, P, x.max_u);
     Carve c{base};
-    x.logits = c.take<float>((size_t)T * E);
+    x.logits = c.take<float>((size_t)T * L->E);
     x.probs = c.take<float>(P);
     x.idx = c.take<uint32_t>(P);
     x.d.offsets = c.take<int32_t>(E + 1);
@@ -183,11 +210,12 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     x.d.meta = c.take<int32_t>(4);
     x.d.chunks = c.take<int32_t>((size_t)x.plan.nchunk);
     x.d.chunk = x.plan.chunk;
+    x.d.n_routed = L->E;
     x.xq = ActQ{c.take<half_t>((size_t)T * H), c.take<float>((size_t)T * (H / kStep)), T};
     x.act = ActQ{c.take<half_t>((size_t)P * I), c.take<float>((size_t)P * (I / kStep)), P};
     x.part = x.plan.ks_gu > 1 ? c.take<float>((size_t)x.plan.ks_gu * P * 2 * I) : nullptr;
     x.ypart = c.take<float>((size_t)x.plan.ks_dn * P * H);
-    if (L->Is) {
+    if (L->Is && !L->n_sh) {
         const int Is = (int)L->Is;
         x.splan = plan_mm(L->sgate.type, L->sdown.type, H, Is, T, 1);
         x.sd.offsets = c.take<int32_t>(2);
@@ -203,7 +231,7 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     }
     if (with_io) {
         x.h_in = c.take<float>((size_t)T * H);
-        x.l_in = c.take<float>((size_t)T * E);
+        x.l_in = c.take<float>((size_t)T * L->E);
         x.out = c.take<float>((size_t)T * H);
     }
     if (f) *f = x;
@@ -234,21 +262,13 @@ __global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__res
     float g = 0.0f;
     for (int i = threadIdx.x; i < H; i += 64) g += f16_bits_to_f32(lin[i]) * h[(size_t)t * H + i];
     for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o);
-    if (threadIdx.x == 0) {
-        float s;
-        if (g >= 0) s = 1.0f / (1.0f + __expf(-fminf(g, 80.0f)));
-        else {
-            const float ex = __expf(fmaxf(g, -80.0f));
-            s = ex / (1.0f + ex);
-        }
-        scale[t] = s;
-    }
+    if (threadIdx.x == 0) scale[t] = shared_sigmoid(g);
 }
 
 int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_logits, float *d_out, const Fwd &f,
                    hipStream_t st, hipEvent_t *ev)
 {
-    const int H = L->H, I = L->I, E = L->E, k = L->k, P = T * k;
+    const int H = L->H, I = L->I, E = L->E, k = L->k, kk = k + (int)L->n_sh, P = T * kk;
     auto mark = [&](int i) {
         if (ev) (void)hipEventRecord(ev[i], st);
     };
@@ -258,23 +278,44 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
         ANEDVD_TRY(launch_router(L->router, d_h, T, E, H, f.logits, st));
         logits = f.logits;
     }
-    ANEDVD_TRY(launch_route_and_dispatch(logits, T, E, k, L->norm, f.probs, f.idx, d_h, H, f.xq, f.d, st));
+    SharedSlots sh;
+    sh.n = (int)L->n_sh;
+    sh.lin = L->sgate_lin;
+    ANEDVD_TRY(launch_route_and_dispatch(logits, T, E, k, L->norm, f.probs, f.idx, d_h, H, f.xq, f.d, st, sh));
     mark(1);
+    // A shared expert that is not merged into the routed launches needs only x
+    // (converted by the route launch): it runs on the context's second stream beside
+    // the routed experts, joined before the combine.  With stage events everything
+    // stays on `st`, so the stages time one at a time.
+    const bool separate = L->Is && !L->n_sh;
+    const bool fork = separate && !ev;
+    hipStream_t ss = fork ? L->ctx->aux : st;
+    if (fork) {
+        ANEDVD_HIP(hipEventRecord(L->ctx->fork, st));
+        ANEDVD_HIP(hipStreamWaitEvent(ss, L->ctx->fork, 0));
+    }
+    auto shared = [&]() -> int {
+        const int Is = (int)L->Is;
+        hipLaunchKernelGGL(k_shared_prep, dim3(T), dim3(64), 0, ss, d_h, L->sgate_lin, T, H, f.sd, f.sh_scale);
+        ANEDVD_HIP(hipGetLastError());
+        ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, f.xq, H, Is, f.sd, T, f.splan, f.sh_part, f.sact,
+                                        L->gelu, ss));
+        return launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_ypart, ss);
+    };
+    if (fork) {
+        ANEDVD_TRY(shared());
+        ANEDVD_HIP(hipEventRecord(L->ctx->join, ss));
+    }
     ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act, L->gelu, st));
     mark(2);
     ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart, st));
     mark(3);
-    if (L->Is) {
-        const int Is = (int)L->Is;
-        hipLaunchKernelGGL(k_shared_prep, dim3(T), dim3(64), 0, st, d_h, L->sgate_lin, T, H, f.sd, f.sh_scale);
-        ANEDVD_HIP(hipGetLastError());
-        ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, f.xq, H, Is, f.sd, T, f.splan, f.sh_part, f.sact,
-                                        L->gelu, st));
-        ANEDVD_TRY(launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_ypart, st));
-    }
+    if (fork) ANEDVD_HIP(hipStreamWaitEvent(st, L->ctx->join, 0));
+    else if (separate) ANEDVD_TRY(shared());
     mark(4);
-    ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, T, k, H, f.plan.ks_dn, P, L->Is ? f.sh_ypart : nullptr,
-                              (L->Is && L->sgate_lin) ? f.sh_scale : nullptr, L->Is ? f.splan.ks_dn : 0, d_out, st));
+    ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, T, kk, H, f.plan.ks_dn, P, separate ? f.sh_ypart : nullptr,
+                              (separate && L->sgate_lin) ? f.sh_scale : nullptr, separate ? f.splan.ks_dn : 0, d_out,
+                              st));
     mark(5);
     return ANEDVD_OK;
 }
@@ -317,9 +358,15 @@ int anedvd_moe_open(int device, anedvd_moe_ctx **out)
     ANEDVD_HIP(hipSetDevice(device));
     anedvd_moe_ctx *c = new anedvd_moe_ctx();
     c->device = device;
-    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->join, hipEventDisableTiming) != hipSuccess) {
+        if (c->fork) (void)hipEventDestroy(c->fork);
+        if (c->aux) (void)hipStreamDestroy(c->aux);
+        if (c->stream) (void)hipStreamDestroy(c->stream);
         delete c;
-        set_error("anedvd_moe_open: stream creation failed");
+        set_error("anedvd_moe_open: stream or event creation failed");
         return ANEDVD_E_HIP;
     }
     *out = c;
@@ -331,8 +378,12 @@ void anedvd_moe_close(anedvd_moe_ctx *ctx)
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamSynchronize(ctx->aux);
     if (ctx->ws.base) (void)hipFree(ctx->ws.base);
     if (ctx->io.base) (void)hipFree(ctx->io.base);
+    (void)hipEventDestroy(ctx->fork);
+    (void)hipEventDestroy(ctx->join);
+    (void)hipStreamDestroy(ctx->aux);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -363,10 +414,35 @@ int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *d,
     L->k = d->k;
     L->norm = d->norm_topk_prob != 0;
     L->gelu = d->use_gelu != 0;
-    const int H = (int)d->hidden, I = (int)d->inter, E = (int)d->n_experts;
-    int rc = make_qmat(L->gate, d->gate_type, I, H, E, d->gate, d->gate_bytes, ctx->stream, L->device_bytes, "gate");
-    if (!rc) rc = make_qmat(L->up, d->up_type, I, H, E, d->up, d->up_bytes, ctx->stream, L->device_bytes, "up");
-    if (!rc) rc = make_qmat(L->down, d->down_type, H, I, E, d->down, d->down_bytes, ctx->stream, L->device_bytes, "down");
+    const int H = (int)d->hidden, I = (int)d->inter, E = (int)d->n_experts, Is = (int)d->shared_inter;
+    // A shared expert of the routed experts' type whose width is a multiple of
+    // theirs is cut into Is / I expert-width pieces appended to the routed experts:
+    // every token takes them as extra slots with its shared scale, in the same
+    // launches (SwiGLU is separable over the intermediate width, so the pieces sum
+    // to the whole).  Otherwise it keeps matrices of its own and a launch sequence
+    // on the context's second stream.
+    const int st_ = d->shared_type, bl = block_elems(st_), bb = block_bytes(st_);
+    const bool merge = Is > 0 && I > 0 && st_ == d->gate_type && st_ == d->up_type && st_ == d->down_type && bl &&
+                       Is % I == 0 && I % bl == 0 && H % bl == 0 &&
+                       d->shared_gate_bytes == (size_t)Is * H / bl * bb && d->shared_up_bytes == d->shared_gate_bytes &&
+                       d->shared_down_bytes == d->shared_gate_bytes;
+    const int nsh = merge ? Is / I : 0;
+    std::vector<Seg> sg, su, sdn;
+    if (merge) {
+        sg.push_back({d->shared_gate, d->shared_gate_bytes, 1, d->shared_gate_bytes});
+        su.push_back({d->shared_up, d->shared_up_bytes, 1, d->shared_up_bytes});
+        const size_t piece = (size_t)I / bl * bb, row = (size_t)Is / bl * bb;  // down [H][Is]: column slices
+        for (int j = 0; j < nsh; j++)
+            sdn.push_back({(const uint8_t *)d->shared_down + j * piece, piece, (size_t)H, row});
+    }
+    L->n_sh = (uint32_t)nsh;
+    int rc = make_qmat(L->gate, d->gate_type, I, H, E, d->gate, d->gate_bytes, ctx->stream, L->device_bytes, "gate",
+                       sg, nsh);
+    if (!rc)
+        rc = make_qmat(L->up, d->up_type, I, H, E, d->up, d->up_bytes, ctx->stream, L->device_bytes, "up", su, nsh);
+    if (!rc)
+        rc = make_qmat(L->down, d->down_type, H, I, E, d->down, d->down_bytes, ctx->stream, L->device_bytes, "down",
+                       sdn, nsh);
     if (!rc) {
         const size_t rb = (size_t)E * H * 2;
         if (hipMalloc(&L->router, rb) != hipSuccess || hipMemcpy(L->router, d->router, rb, hipMemcpyHostToDevice) != hipSuccess) {
@@ -376,14 +452,16 @@ int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *d,
         L->device_bytes += rb;
     }
     if (!rc && d->shared_inter) {
-        const int Is = (int)d->shared_inter;
         L->Is = d->shared_inter;
-        rc = make_qmat(L->sgate, d->shared_type, Is, H, 1, d->shared_gate, d->shared_gate_bytes, ctx->stream,
-                       L->device_bytes, "shared gate");
-        if (!rc) rc = make_qmat(L->sup, d->shared_type, Is, H, 1, d->shared_up, d->shared_up_bytes, ctx->stream,
-                                L->device_bytes, "shared up");
-        if (!rc) rc = make_qmat(L->sdown, d->shared_type, H, Is, 1, d->shared_down, d->shared_down_bytes, ctx->stream,
-                                L->device_bytes, "shared down");
+        if (!merge) {
+            rc = make_qmat(L->sgate, d->shared_type, Is, H, 1, d->shared_gate, d->shared_gate_bytes, ctx->stream,
+                           L->device_bytes, "shared gate");
+            if (!rc) rc = make_qmat(L->sup, d->shared_type, Is, H, 1, d->shared_up, d->shared_up_bytes, ctx->stream,
+                                    L->device_bytes, "shared up");
+            if (!rc)
+                rc = make_qmat(L->sdown, d->shared_type, H, Is, 1, d->shared_down, d->shared_down_bytes, ctx->stream,
+                               L->device_bytes, "shared down");
+        }
         if (!rc && d->shared_gate_lin) {
             if (hipMalloc(&L->sgate_lin, (size_t)H * 2) != hipSuccess ||
                 hipMemcpy(L->sgate_lin, d->shared_gate_lin, (size_t)H * 2, hipMemcpyHostToDevice) != hipSuccess) {
@@ -398,7 +476,7 @@ int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *d,
     }
     auto bpw = [](int t) { return (double)block_bytes(t) / block_elems(t); };
     L->expert_bytes = (double)I * H * (bpw(L->gate.type) + bpw(L->up.type) + bpw(L->down.type));
-    L->shared_bytes = L->Is ? 3.0 * H * L->Is * bpw(L->sgate.type) : 0.0;
+    L->shared_bytes = L->Is ? 3.0 * H * L->Is * bpw(d->shared_type) : 0.0;
     *out = L;
     return ANEDVD_OK;
 }
@@ -657,14 +735,15 @@ static int prepare(anedvd_moe_layer *L, size_t T, bool io, Fwd &f)
     anedvd_moe_ctx *ctx = L->ctx;
     ANEDVD_HIP(hipSetDevice(ctx->device));
     if (!mm_supported(L->gate.type) || !mm_supported(L->down.type) || L->gate.type != L->up.type ||
-        (L->Is && (!mm_supported(L->sgate.type) || !mm_supported(L->sdown.type)))) {
+        (L->Is && !L->n_sh && (!mm_supported(L->sgate.type) || !mm_supported(L->sdown.type)))) {
         set_error("forward: no expert kernel for ggml types gate=%d up=%d down=%d", L->gate.type, L->up.type,
                   L->down.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
-    const size_t bytes = fwd_layout(L, (int)T, (int)L->k, nullptr, (uint8_t *)0, io);
+    const int ks = (int)(L->k + L->n_sh);
+    const size_t bytes = fwd_layout(L, (int)T, ks, nullptr, (uint8_t *)0, io);
     ANEDVD_TRY(ensure(ctx->ws, bytes + 4096, ctx->stream));
-    fwd_layout(L, (int)T, (int)L->k, &f, (uint8_t *)ctx->ws.base, io);
+    fwd_layout(L, (int)T, ks, &f, (uint8_t *)ctx->ws.base, io);
     return ANEDVD_OK;
 }
 
@@ -688,9 +767,10 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *L, const float *h, size_t T, cons
     ANEDVD_HIP(hipStreamSynchronize(st));
     if (stats) {
         stats->n_tokens = (uint32_t)T;
-        stats->touched_experts = (uint32_t)meta[0];
+        const int touched = meta[0] - (T ? (int)L->n_sh : 0);  // the merged shared pieces are always active
+        stats->touched_experts = (uint32_t)touched;
         stats->max_group = (uint32_t)meta[1];
-        stats->weight_bytes = (uint64_t)(meta[0] * L->expert_bytes + L->shared_bytes + (logits ? 0.0 : 2.0 * L->E * L->H));
+        stats->weight_bytes = (uint64_t)(touched * L->expert_bytes + L->shared_bytes + (logits ? 0.0 : 2.0 * L->E * L->H));
         stats->path = f.plan.mt > 1 ? 1 : 0;
     }
     return ANEDVD_OK;
@@ -761,7 +841,8 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
     anedvd_moe_ctx *ctx = layers[0]->ctx;
     for (size_t i = 0; i < n_layers; i++)
         if (!layers[i] || layers[i]->ctx != ctx || layers[i]->H != layers[0]->H || layers[i]->E != layers[0]->E ||
-            layers[i]->I != layers[0]->I || layers[i]->k != layers[0]->k || layers[i]->Is != layers[0]->Is) {
+            layers[i]->I != layers[0]->I || layers[i]->k != layers[0]->k || layers[i]->Is != layers[0]->Is ||
+            layers[i]->n_sh != layers[0]->n_sh) {
             set_error("time_forward: layers must share a context and a shape");
             return ANEDVD_E_INVALID_ARG;
         }
@@ -856,7 +937,7 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
         // gate/up (then the down) kernels over the rotated layers, reading the
         // dispatch, activations and gate/up output the last call left in place (the
         // calls above routed the same inputs).  Events bracket each loop only.
-        const int H = layers[0]->H, I = layers[0]->I, P = (int)T * layers[0]->k;
+        const int H = layers[0]->H, I = layers[0]->I, P = (int)T * (int)(layers[0]->k + layers[0]->n_sh);
         hipEvent_t a = nullptr, b = nullptr;
         ANEDVD_HIP(hipEventCreate(&a));
         ANEDVD_HIP(hipEventCreate(&b));

@@ -232,14 +232,28 @@ def test_forward_shared_expert_deepseek_shape(ctx):
     assert err <= REL_L2_TOL
 
 
-def test_forward_shared_expert_grouped(ctx):
-    """A 512-token call whose shared expert (width 4096) takes the grouped GEMM
-    while the small routed experts take the decode kernels."""
-    spec = dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="shared-grouped", hidden=512, inter=512, n_experts=8,
-                               k=2, shared_inter=4096)
+def test_forward_shared_expert_separate_grouped(ctx):
+    """A shared expert of another type than the routed experts keeps matrices of
+    its own and runs on the second stream: here (width 4096, 512 tokens) on the
+    grouped GEMM while the small routed experts take the decode kernels."""
+    spec = dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="shared-separate", hidden=512, inter=512, n_experts=8,
+                               k=2, shared_inter=4096, shared_type=W.Q4_0, shared_gated=True)
     _, _, err, st = _forward_case(ctx, spec, 512, seed=12)
     assert err <= REL_L2_TOL
     assert st["path"] == 0
+
+
+@pytest.mark.parametrize("T", [1, 600])
+def test_forward_shared_expert_merged(ctx, T):
+    """A shared expert of the routed type and twice their width is cut into two
+    expert-width pieces that every token takes as extra slots; at 600 tokens the
+    routed experts and the pieces share the grouped GEMM launches."""
+    spec = dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="shared-merged", hidden=512, inter=1024, n_experts=8,
+                               k=2, shared_inter=2048, shared_gated=True)
+    _, _, err, st = _forward_case(ctx, spec, T, seed=13)
+    assert err <= REL_L2_TOL
+    assert st["path"] == (1 if T == 600 else 0)
+    assert st["touched_experts"] <= spec.n_experts
 
 
 def test_forward_gated_shared_expert(ctx):
@@ -343,10 +357,16 @@ def test_forward_repeat_calls_keep_counters_clean(ctx):
     layer.free()
 
 
-def test_graph_replay_matches_direct_forward(ctx):
+GRAPH_SPECS = [W.QWEN3_30B_A3B_Q8_0,
+               dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="shared-gated", hidden=512, inter=512, n_experts=8,
+                                   k=2, shared_inter=1024, shared_gated=True)]
+
+
+@pytest.mark.parametrize("spec", GRAPH_SPECS, ids=lambda s: s.name.split()[0])
+def test_graph_replay_matches_direct_forward(ctx, spec):
     """The timed loop's HIP-graph replay computes what the directly launched
-    forward computes, replay after replay, with direct launches in between."""
-    spec = W.QWEN3_30B_A3B_Q8_0
+    forward computes, replay after replay, with direct launches in between (with a
+    shared expert, the graph holds the fork to the second stream and the join)."""
     L = synth.make_layer(spec, seed=8)
     layer = moe.MoeLayer(ctx, spec, L)
     for T in (1, 64):
