@@ -158,3 +158,68 @@ class Gguf:
             raise GgufError("InvalidTensorShape")
         per = len(allb) // n_experts
         return allb[expert * per:(expert + 1) * per]
+
+
+# ------------------------------------------------------------------ writing
+
+# metadata value types (gguf.zig ValueType)
+U8, I8, U16, I16, U32, I32, F32V, BOOL, STR, ARR, U64, I64, F64V = range(13)
+
+
+def _pack_value(vt: int, v) -> bytes:
+    if vt in _SCALAR:
+        return struct.pack(_SCALAR[vt], v)
+    if vt == STR:
+        b = v.encode()
+        return struct.pack("<Q", len(b)) + b
+    raise GgufError("InvalidMetadata")
+
+
+def _typed(v):
+    """(value type, value) of a metadata entry: explicit (type, value) pairs pass
+    through; Python ints are u32 (u64 when larger), floats f32, strings and bools
+    as themselves, lists arrays of the first element's type."""
+    if isinstance(v, tuple) and len(v) == 2 and isinstance(v[0], int) and not isinstance(v[0], bool):
+        return v
+    if isinstance(v, bool):
+        return BOOL, v
+    if isinstance(v, int):
+        return (U32, v) if 0 <= v < 2 ** 32 else (U64 if v >= 0 else I64, v)
+    if isinstance(v, float):
+        return F32V, v
+    if isinstance(v, str):
+        return STR, v
+    if isinstance(v, list):
+        return ARR, v
+    raise GgufError("InvalidMetadata")
+
+
+def write(metadata: dict, tensors: list, alignment: int = 32, version: int = 3) -> bytes:
+    """A GGUF v2/v3 image (the layout Gguf.parse reads, gguf.zig:587-657): metadata
+    in dict order, then `tensors` = [(name, dims fastest-first, ggml type, payload
+    bytes)], each payload at an `alignment`-aligned offset of the data section."""
+    out = [struct.pack("<IIQQ", MAGIC, version, len(tensors), len(metadata))]
+    for key, v in metadata.items():
+        vt, val = _typed(v)
+        kb = key.encode()
+        out.append(struct.pack("<Q", len(kb)) + kb + struct.pack("<I", vt))
+        if vt == ARR:
+            et, _ = _typed(val[0]) if val else (U32, 0)
+            out.append(struct.pack("<IQ", et, len(val)) + b"".join(_pack_value(et, x) for x in val))
+        else:
+            out.append(_pack_value(vt, val))
+    offs, off = [], 0
+    for name, dims, tt, payload in tensors:
+        off = (off + alignment - 1) // alignment * alignment
+        offs.append(off)
+        off += len(payload)
+    for (name, dims, tt, payload), o in zip(tensors, offs):
+        nb = name.encode()
+        out.append(struct.pack("<Q", len(nb)) + nb + struct.pack("<I", len(dims)))
+        out.append(b"".join(struct.pack("<Q", d) for d in dims) + struct.pack("<IQ", tt, o))
+    head = b"".join(out)
+    data_off = (len(head) + alignment - 1) // alignment * alignment
+    body = bytearray(off)
+    for (_, _, _, payload), o in zip(tensors, offs):
+        body[o:o + len(payload)] = bytes(payload)
+    return head + b"\0" * (data_off - len(head)) + bytes(body)

@@ -27,7 +27,8 @@ LIB_PATH = os.environ.get("ANEDVD_MOE_LIB") or os.path.join(HERE, "libanedvd_moe
 
 STATUS = {0: "OK", -1: "UnsupportedType", -2: "InvalidTensorShape", -3: "TruncatedFile",
           -4: "DimensionMismatch", -5: "TensorDataOutOfRange", -6: "InvalidArgument", -7: "HipError",
-          -8: "NoDevice"}
+          -8: "NoDevice", -9: "NotGgufFile", -10: "UnsupportedVersion", -11: "InvalidMetadata",
+          -12: "MissingTensor"}
 
 
 class MoeError(RuntimeError):
@@ -52,6 +53,20 @@ class LayerDesc(C.Structure):
         ("shared_down", C.c_void_p), ("shared_down_bytes", C.c_size_t),
         ("shared_gate_lin", C.c_void_p),
     ]
+
+
+class GgufMoeCfg(C.Structure):
+    _fields_ = [
+        ("arch", C.c_char * 64), ("version", C.c_uint32), ("n_tensors", C.c_uint64), ("data_offset", C.c_uint64),
+        ("hidden", C.c_uint32), ("n_layers", C.c_uint32), ("n_experts", C.c_uint32), ("k", C.c_uint32),
+        ("inter", C.c_uint32), ("shared_inter", C.c_uint32),
+        ("gate_type", C.c_int32), ("up_type", C.c_int32), ("down_type", C.c_int32), ("router_type", C.c_int32),
+        ("shared_type", C.c_int32), ("has_shared_gate_lin", C.c_int32),
+    ]
+
+
+class GgufMoeOpts(C.Structure):
+    _fields_ = [("norm_topk_prob", C.c_int32), ("use_gelu", C.c_int32)]
 
 
 class Stats(C.Structure):
@@ -85,6 +100,8 @@ SIGNATURES = {
     "anedvd_moe_synchronize": (_i, [_vp]),
     "anedvd_moe_time_forward": (_i, [C.POINTER(_vp), _sz, _vp, _sz, _vp, _vp, _i, _i, _i, C.POINTER(_f),
                                      C.POINTER(_f)]),
+    "anedvd_gguf_moe_info": (_i, [_vp, _sz, C.c_uint32, C.POINTER(GgufMoeCfg)]),
+    "anedvd_moe_layer_create_gguf": (_i, [_vp, _vp, _sz, C.c_uint32, C.POINTER(GgufMoeOpts), C.POINTER(_vp)]),
 }
 
 _lib = None
@@ -206,6 +223,25 @@ class MoeContext:
         _check(lib().anedvd_moe_synchronize(self.h))
 
 
+def _gguf_image(src):
+    """A GGUF image as a contiguous uint8 array: a path is memory-mapped, bytes are
+    viewed in place."""
+    if isinstance(src, (str, os.PathLike)):
+        return np.memmap(src, dtype=np.uint8, mode="r")
+    return np.frombuffer(src, dtype=np.uint8)
+
+
+def gguf_moe_config(src, layer: int = 0) -> dict:
+    """The MoE configuration of a GGUF file (load_gguf.zig:109-128, 251-289) and the
+    tensor types of block `layer`, as anedvd_gguf_moe_info derives them (host only)."""
+    img = _gguf_image(src)
+    cfg = GgufMoeCfg()
+    _check(lib().anedvd_gguf_moe_info(_p(img), img.nbytes, layer, C.byref(cfg)))
+    out = {name: getattr(cfg, name) for name, _ in GgufMoeCfg._fields_}
+    out["arch"] = cfg.arch.decode()
+    return out
+
+
 class MoeLayer:
     """One resident MoE layer (anedvd_moe_layer_create).  `arrays` is the dict of
     GGUF payloads from synth.make_layer (or a GGUF loader)."""
@@ -238,6 +274,29 @@ class MoeLayer:
         _check(lib().anedvd_moe_layer_create(ctx.h, C.byref(d), C.byref(h)))
         self.h = h
         ctx._layers.add(self)
+
+    @classmethod
+    def from_gguf(cls, ctx: MoeContext, src, layer: int, norm_topk_prob: bool | None = None,
+                  use_gelu: bool | None = None) -> "MoeLayer":
+        """Block `layer` of a GGUF file (path, or the image's bytes) loaded the way
+        loadMoeLayerStreaming does (load_gguf.zig:767-826); None keeps the
+        reference GGUF loader's value of an option (false)."""
+        c = gguf_moe_config(src, layer)
+        img = _gguf_image(src)
+        opts = GgufMoeOpts(-1 if norm_topk_prob is None else int(norm_topk_prob),
+                           -1 if use_gelu is None else int(use_gelu))
+        h = C.c_void_p()
+        _check(lib().anedvd_moe_layer_create_gguf(ctx.h, _p(img), img.nbytes, layer, C.byref(opts), C.byref(h)))
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        self.spec = W.LayerSpec(f"{c['arch']} blk.{layer}", c["hidden"], c["inter"], c["n_experts"], c["k"],
+                                bool(norm_topk_prob), c["gate_type"], c["up_type"], c["down_type"],
+                                shared_inter=c["shared_inter"],
+                                shared_type=c["shared_type"] if c["shared_type"] >= 0 else W.Q8_0,
+                                shared_gated=bool(c["has_shared_gate_lin"]))
+        self.h = h
+        ctx._layers.add(self)
+        return self
 
     def free(self):
         if self.h:

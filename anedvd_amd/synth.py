@@ -187,3 +187,47 @@ def zipf_logits(spec: W.LayerSpec, n_tokens: int, seed: int = 0, alpha: float = 
     bias = alpha * np.log(p)
     z = normal(seed, _STREAM["logits"] + 2, n_tokens * E).reshape(n_tokens, E)
     return (z + bias[None, :]).astype(np.float32)
+
+
+def moe_gguf(spec: W.LayerSpec, n_layers: int, seed: int = 0, arch: str = "qwen3moe", router_type: int = W.F32,
+             router_transposed: bool = False, extra_metadata: dict | None = None, drop: tuple = ()) -> tuple:
+    """A GGUF image of `n_layers` MoE blocks of `spec` in llama.cpp's tensor naming
+    (the names load_gguf.zig:767-826 reads): blk.N.ffn_gate_inp.weight {H, E}
+    (`router_type` F32 or F16; {E, H} when `router_transposed`),
+    blk.N.ffn_{gate,up}_exps.weight {H, I, E}, blk.N.ffn_down_exps.weight {I, H, E},
+    and the shared expert's blk.N.ffn_{gate,up}_shexp {H, Is}, ffn_down_shexp {Is, H}
+    and ffn_gate_inp_shexp {H} (F32).  Block N holds make_layer(spec, seed, N).
+    `drop` lists metadata keys or tensor names left out.  Returns (image bytes,
+    [per-layer arrays])."""
+    from . import gguf as G
+    H, I, E, Is = spec.hidden, spec.inter, spec.n_experts, spec.shared_inter
+    meta = {"general.architecture": arch, "general.alignment": 32, f"{arch}.block_count": n_layers,
+            f"{arch}.embedding_length": H, f"{arch}.feed_forward_length": 4 * H, f"{arch}.expert_count": E,
+            f"{arch}.expert_used_count": spec.k, f"{arch}.expert_feed_forward_length": I}
+    if Is:
+        meta[f"{arch}.expert_shared_feed_forward_length"] = Is
+    meta.update(extra_metadata or {})
+    meta = {k: v for k, v in meta.items() if k not in drop}
+    tensors, layers = [], []
+    for n in range(n_layers):
+        L = make_layer(spec, seed=seed, layer=n)
+        layers.append(L)
+        r = L["router"].astype(np.float32)
+        if router_transposed:
+            r, rdims = np.ascontiguousarray(r.T), (E, H)
+        else:
+            rdims = (H, E)
+        rb = (r.astype(np.float16) if router_type == W.F16 else r).tobytes()
+        tensors += [(f"blk.{n}.ffn_gate_inp.weight", rdims, router_type, rb),
+                    (f"blk.{n}.ffn_gate_exps.weight", (H, I, E), spec.gate_type, L["gate"].tobytes()),
+                    (f"blk.{n}.ffn_up_exps.weight", (H, I, E), spec.up_type, L["up"].tobytes()),
+                    (f"blk.{n}.ffn_down_exps.weight", (I, H, E), spec.down_type, L["down"].tobytes())]
+        if Is:
+            lin = L.get("shared_gate_lin")
+            lin = np.zeros(H, np.float32) if lin is None else lin.astype(np.float32)
+            tensors += [(f"blk.{n}.ffn_gate_shexp.weight", (H, Is), spec.shared_type, L["shared_gate"].tobytes()),
+                        (f"blk.{n}.ffn_up_shexp.weight", (H, Is), spec.shared_type, L["shared_up"].tobytes()),
+                        (f"blk.{n}.ffn_down_shexp.weight", (Is, H), spec.shared_type, L["shared_down"].tobytes()),
+                        (f"blk.{n}.ffn_gate_inp_shexp.weight", (H,), W.F32, lin.tobytes())]
+    tensors = [t for t in tensors if t[0] not in drop]
+    return G.write(meta, tensors), layers

@@ -44,7 +44,12 @@ enum anedvd_status {
     ANEDVD_E_OUT_OF_RANGE = -5,      /* error.TensorDataOutOfRange */
     ANEDVD_E_INVALID_ARG = -6,
     ANEDVD_E_HIP = -7,               /* a HIP runtime call failed; see last_error */
-    ANEDVD_E_NO_DEVICE = -8
+    ANEDVD_E_NO_DEVICE = -8,
+    /* GGUF container and loader errors (gguf.zig:587-657, load_gguf.zig:109-128, 358-386) */
+    ANEDVD_E_NOT_GGUF = -9,          /* error.NotGgufFile */
+    ANEDVD_E_GGUF_VERSION = -10,     /* error.UnsupportedVersion */
+    ANEDVD_E_INVALID_METADATA = -11, /* error.InvalidMetadata / TooMany* / UnsupportedMetadataType / no experts */
+    ANEDVD_E_MISSING_TENSOR = -12    /* error.MissingTensor: a tensor or config key the layer needs */
 };
 
 typedef struct anedvd_moe_ctx anedvd_moe_ctx;
@@ -136,6 +141,44 @@ int anedvd_moe_dispatch(anedvd_moe_ctx *ctx, const uint32_t *idx, size_t n_token
  * out[H] += weight * down(silu(gate h) * up h). */
 int anedvd_moe_expert_accum(anedvd_moe_layer *layer, uint32_t expert, const float *h, float weight,
                             float *out);
+
+/* ------------------------------------------------------------ GGUF loading */
+
+/* The MoE configuration of a GGUF file and the types of one block's tensors, as
+ * load_gguf.zig:109-128 and 251-289 derive them (types are ggml type ids, -1 when
+ * the tensor is absent). */
+typedef struct {
+    char arch[64];               /* general.architecture */
+    uint32_t version;            /* GGUF version (2 or 3) */
+    uint64_t n_tensors, data_offset;
+    uint32_t hidden;             /* <arch>.embedding_length */
+    uint32_t n_layers;           /* <arch>.block_count */
+    uint32_t n_experts, k;       /* expert_count (blk.0.ffn_gate_exps wins), expert_used_count (2 if absent) */
+    uint32_t inter;              /* routed expert width, from blk.0.ffn_gate_exps.weight or the metadata */
+    uint32_t shared_inter;       /* 0 = no shared expert */
+    int32_t gate_type, up_type, down_type, router_type, shared_type;
+    int32_t has_shared_gate_lin;
+} anedvd_gguf_moe_cfg;
+
+/* Options of anedvd_moe_layer_create_gguf; NULL or -1 fields = the reference GGUF
+ * loader's values (norm_topk_prob false, use_gelu false). */
+typedef struct {
+    int32_t norm_topk_prob;
+    int32_t use_gelu;
+} anedvd_gguf_moe_opts;
+
+/* Parses a GGUF v2/v3 image held in host memory (Gguf.parse, gguf.zig:587-657),
+ * derives its MoE configuration and checks block `layer`'s tensors.  Host only:
+ * no device is touched. */
+int anedvd_gguf_moe_info(const void *gguf, size_t len, uint32_t layer, anedvd_gguf_moe_cfg *out);
+
+/* loadMoeLayerStreaming (load_gguf.zig:767-826) onto the GPU: block `layer` of the
+ * GGUF image (the caller maps the file; it may be unmapped on return).  The expert
+ * payloads are uploaded as stored; the router and the shared gate vector are read
+ * as f16 (any type, dequantised bit-exactly, rounded to nearest even); the shared
+ * expert's three tensors must share one type the expert kernels take. */
+int anedvd_moe_layer_create_gguf(anedvd_moe_ctx *ctx, const void *gguf, size_t len, uint32_t layer,
+                                 const anedvd_gguf_moe_opts *opts, anedvd_moe_layer **out);
 
 /* ---------------------------------------------------------------- the layer */
 

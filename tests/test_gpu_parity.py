@@ -382,3 +382,47 @@ def test_graph_replay_matches_direct_forward(ctx, spec):
         for p in (d_h, d_lg, d_out):
             ctx.free(p)
     layer.free()
+
+
+# ------------------------------------------------------------------ GGUF loading
+
+GGUF_SPECS = [
+    dataclasses.replace(W.TINY_Q8_0, name="gguf-q8_0", hidden=512, inter=512, n_experts=8, k=2),
+    dataclasses.replace(W.QWEN3_30B_A3B_Q4_K_M, name="gguf-q4_k-q6_k", hidden=512, inter=512, n_experts=8, k=2),
+    dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="gguf-shared-merged", hidden=512, inter=512, n_experts=8, k=2,
+                        shared_inter=1024, shared_gated=True),
+    dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="gguf-shared-separate", hidden=512, inter=512, n_experts=8,
+                        k=2, shared_inter=1024, shared_type=W.Q4_0, shared_gated=True),
+]
+
+
+@pytest.mark.parametrize("spec", GGUF_SPECS, ids=lambda s: s.name)
+@pytest.mark.parametrize("router", ["f32", "f16-transposed"])
+def test_layer_from_gguf_matches_layer_from_arrays(ctx, spec, router):
+    """loadMoeLayerStreaming (load_gguf.zig:767-826) through the C++ GGUF loader:
+    block 1 of a two-block file computes bit for bit what the same arrays handed
+    to layer_create compute, and matches the oracle."""
+    rt, tr = (W.F32, False) if router == "f32" else (W.F16, True)
+    img, Ls = synth.moe_gguf(spec, 2, seed=3, router_type=rt, router_transposed=tr)
+    a = moe.MoeLayer.from_gguf(ctx, img, 1, norm_topk_prob=spec.norm_topk_prob)
+    b = moe.MoeLayer(ctx, spec, Ls[1])
+    assert (a.spec.hidden, a.spec.inter, a.spec.n_experts, a.spec.k) == (spec.hidden, spec.inter, spec.n_experts,
+                                                                         spec.k)
+    for T in (1, 24):
+        h = synth.activations(spec, T, seed=3)
+        ya, sa = a.forward(h, stats=True)
+        yb, sb = b.forward(h, stats=True)
+        assert np.array_equal(bits(ya), bits(yb))
+        assert sa == sb
+        want = O.OracleLayer(spec, Ls[1]).forward(h)
+        assert moe.rel_l2(ya, want) <= REL_L2_TOL
+    a.free()
+    b.free()
+
+
+def test_layer_from_gguf_rejects_truncated_data(ctx):
+    spec = GGUF_SPECS[0]
+    img, _ = synth.moe_gguf(spec, 1, seed=3)
+    with pytest.raises(moe.MoeError) as e:
+        moe.MoeLayer.from_gguf(ctx, img[:-100], 0)
+    assert e.value.name == "TensorDataOutOfRange"
