@@ -165,13 +165,6 @@ __host__ __device__ inline float f16_bits_to_f32(uint16_t h)
 // two scaling is exact; it keeps every group's largest value in [2^14, 2^15), far
 // from f16 overflow and subnormals.
 
-__device__ inline float wave_max(float v)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
 // cpu.sigmoid (cpu.zig:1223-1230): the clamped logistic of the shared expert's gate.
 __device__ inline float shared_sigmoid(float g)
 {
@@ -201,6 +194,18 @@ __device__ inline float row_max_f32(float v)
     v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
     v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
     return v;
+}
+
+// Wavefront-wide max (fmaxf: NaN only if every lane's is): DPP inside each row of
+// 16 lanes, readlane across the four rows; every lane gets the result.
+__device__ inline float wave_max(float v)
+{
+    v = row_max_f32(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // One wavefront converts one 64-element group: lane e holds element e.

@@ -19,6 +19,21 @@
 
 namespace anedvd {
 
+// Weight and activation steps loaded ahead of the one being multiplied: the
+// super-block formats (small register footprint per step, memory-bound prefill
+// shapes) go deeper than Q8_0 / Q4_0, whose kernels keep three wavefronts per SIMD.
+#ifndef ANEDVD_PF_DEPTH_K
+#define ANEDVD_PF_DEPTH_K 2
+#endif
+#ifndef ANEDVD_PF_DEPTH_L
+#define ANEDVD_PF_DEPTH_L 1
+#endif
+#ifndef ANEDVD_PF_STAGE_K
+#define ANEDVD_PF_STAGE_K 2
+#endif
+#ifndef ANEDVD_PF_STAGE_L
+#define ANEDVD_PF_STAGE_L 1
+#endif
 constexpr int kAStride = 72;  // halves per staged token row: 64 + 8 against LDS bank conflicts
 constexpr int kPfTiles = 4;   // 16-row tiles per wavefront: each staged A read feeds four MFMAs
 
@@ -39,6 +54,8 @@ __device__ inline half_t h_bits(uint32_t b)
 
 struct FQ8_0 {
     static constexpr int kSpu = 1;
+    static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
+    static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     struct Raw {
         u32x4 q[kPfTiles];
         uint32_t s[kPfTiles];
@@ -63,6 +80,8 @@ struct FQ8_0 {
 
 struct FQ4_0 {
     static constexpr int kSpu = 1;
+    static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
+    static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     struct Raw {
         u32x2 q[kPfTiles];
         uint32_t s[kPfTiles];
@@ -91,6 +110,8 @@ struct FQ4_0 {
 // the f16 FMA rounds once, so a weight is within 2^-10 of its scale.
 struct FQ4_K {
     static constexpr int kSpu = 4;
+    static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
+    static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     struct Raw {
         u32x2 q[kPfTiles];
         u32x4 sc[kPfTiles];  // d, dmin, scales: loaded on a unit's first step
@@ -139,6 +160,8 @@ struct FQ4_K {
 // lane's 8 columns of block j lie in sub-block 4 ss + 2 j + g / 2.
 struct FQ6_K {
     static constexpr int kSpu = 4;
+    static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
+    static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     struct Raw {
         u32x2 q[kPfTiles];
         uint32_t h[kPfTiles];
@@ -199,6 +222,7 @@ struct FQ6_K {
 // loaded several steps before they are written to LDS.
 template <int R, int NB>
 struct StageX {  // gate/up: token rows gathered through the dispatch; x has per-row descales
+    static constexpr int kSlots = NB;
     rsrc_t q;
     int off[R];
     u32x4 v[NB][R][2];
@@ -224,6 +248,7 @@ struct StageX {  // gate/up: token rows gathered through the dispatch; x has per
 
 template <int R, int NB>
 struct StageAct {  // down: consecutive positions, rescaled from their group's descale to the row's
+    static constexpr int kSlots = NB;
     rsrc_t q, ds;
     int off[R], doff[R], ld4;
     float inv_ref[R];
@@ -257,14 +282,18 @@ template <class S>
 __device__ inline void stage_load(S &st, int b, int s)
 {
     if (b == 0) st.template load<0>(s);
-    else st.template load<1>(s);
+    else if (b == 1) st.template load<1 % S::kSlots>(s);
+    else if (b == 2) st.template load<2 % S::kSlots>(s);
+    else st.template load<3 % S::kSlots>(s);
 }
 
 template <class S>
 __device__ inline void stage_store(const S &st, int b, half_t *dst)
 {
     if (b == 0) st.template store<0>(dst);
-    else st.template store<1>(dst);
+    else if (b == 1) st.template store<1 % S::kSlots>(dst);
+    else if (b == 2) st.template store<2 % S::kSlots>(dst);
+    else st.template store<3 % S::kSlots>(dst);
 }
 
 // ------------------------------------------------------------ main loop
@@ -272,15 +301,15 @@ __device__ inline void stage_store(const S &st, int b, half_t *dst)
 // Steps [0, steps) of the wavefront's four tiles of row block rb against the MT
 // 16-token tiles staged in `abuf` (two buffers of 16 MT x kAStride halves):
 // acc[tt][mt] = sum_k W[64 rb + 16 tt + l % 16][k] * A[16 mt + 4 (l / 16) + i][k].
-// Weights and the next step's activations are loaded one step ahead (two register
-// slots each); every thread of the workgroup takes part in the staging, so all of
+// Weights are loaded F::kDepth steps ahead and activations F::kStageDepth steps
+// ahead (rings of register slots); every thread of the workgroup takes part in the staging, so all of
 // them reach the barriers.  Steps go in unrolled blocks of four (one scale unit of
 // the super-block formats), so the slots and the LDS buffers alternate at
 // compile-time indices.  Weight loads past the last step go out of range (zero, no
 // memory traffic).
 template <class F, int MT, class S>
 __device__ inline void pf_loop(const Planes &W, int rb, int steps, int lane, S &stage, half_t *abuf,
-                               int srow, f32x4 (*acc)[MT])
+                               int srow, int mt_live, f32x4 (*acc)[MT])
 {
     constexpr int U = 4;
     constexpr int BUF = 16 * MT * kAStride;
@@ -288,11 +317,20 @@ __device__ inline void pf_loop(const Planes &W, int rb, int steps, int lane, S &
     const int n = lane & 15, g = lane >> 4;
     const int so = (W.nrb - rb) * W.steps;
     auto ws = [&](int x) { return x < steps ? x : so; };
-    typename F::Raw w[2];
+    constexpr int D = F::kDepth, DA = F::kStageDepth;
+    constexpr int R = D == 1 ? 2 : 4;    // ring of weight slots; divides the unrolled block
+    constexpr int RA = DA == 1 ? 2 : 4;  // ring of staging slots
+    static_assert(D >= 1 && D <= 3 && DA >= 1 && DA <= 3, "at most three steps ahead");
+    static_assert(S::kSlots == RA, "staging ring");
+    typename F::Raw w[R];
     typename F::State st;
     stage.template load<0>(0);
-    F::load(w[0], W, rb, 0, lane);
+#pragma unroll
+    for (int d = 0; d < D; d++) F::load(w[d], W, rb, ws(d), lane);
     stage.template store<0>(abuf + srow);
+#pragma unroll
+    for (int d = 1; d < DA; d++)
+        if (d < steps) stage_load(stage, d, d);
     __syncthreads();
     for (int s0 = 0; s0 < steps; s0 += U) {
 #pragma unroll
@@ -300,25 +338,26 @@ __device__ inline void pf_loop(const Planes &W, int rb, int steps, int lane, S &
             const int s = s0 + k;
             if (s >= steps) break;  // uniform; only for a step count that is not a multiple of 4
             const bool more = s + 1 < steps;
-            if (more) stage_load(stage, (k + 1) & 1, s + 1);
-            F::load(w[(k + 1) & 1], W, rb, ws(s + 1), lane);
+            if (s + DA < steps) stage_load(stage, (k + DA) % RA, s + DA);
+            F::load(w[(k + D) % R], W, rb, ws(s + D), lane);
             __builtin_amdgcn_sched_barrier(0);
             const int ss = k % F::kSpu;
-            F::begin(w[k & 1], st, ss, lane);
+            F::begin(w[k % R], st, ss, lane);
             const half_t *a = abuf + (k & 1) * BUF + n * kAStride + 16 * g;
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 half8 b[kPfTiles];
 #pragma unroll
-                for (int tt = 0; tt < kPfTiles; tt++) b[tt] = F::bop(w[k & 1], st, ss, tt, j, lane);
+                for (int tt = 0; tt < kPfTiles; tt++) b[tt] = F::bop(w[k % R], st, ss, tt, j, lane);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
+                    if (mt >= mt_live) break;  // uniform: token tiles past the chunk's end stay zero
                     const half8 av = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
 #pragma unroll
                     for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av, b[tt], acc[tt][mt]);
                 }
             }
-            if (more) stage_store(stage, (k + 1) & 1, abuf + ((k + 1) & 1) * BUF + srow);
+            if (more) stage_store(stage, (k + 1) % RA, abuf + ((k + 1) & 1) * BUF + srow);
             __syncthreads();
         }
     }
@@ -375,7 +414,7 @@ __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
     const Planes W = planes(mat ? a.w1 : a.w0, e);
     half_t *abuf = (half_t *)smem;
     const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
-    StageX<R, 2> stage;
+    StageX<R, F::kStageDepth == 1 ? 2 : 4> stage;
     stage.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
 #pragma unroll
     for (int h = 0; h < R; h++) stage.off[h] = a.d.rows[p0 + min(r + 64 * h, nt - 1)] * a.H * 2 + 32 * q;
@@ -384,7 +423,8 @@ __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
     for (int tt = 0; tt < kPfTiles; tt++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    pf_loop<F, MT>(W, rb, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q, acc);
+    pf_loop<F, MT>(W, rb, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q,
+                   __builtin_amdgcn_readfirstlane((nt + 15) / 16), acc);
 
     // results * the tokens' descales -> LDS [mat][token][row]: one row block and 64
     // tokens per pass
@@ -455,7 +495,7 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
     }
     __syncthreads();
     const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
-    StageAct<R, 2> stage;
+    StageAct<R, F::kStageDepth == 1 ? 2 : 4> stage;
     stage.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
     stage.ds = make_rsrc(a.x.ds, (size_t)G * ld * 4);
     stage.ld4 = ld * 4;
@@ -471,7 +511,8 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
     for (int tt = 0; tt < kPfTiles; tt++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    pf_loop<F, MT>(W, rb, a.I / kStep, lane, stage, (half_t *)smem, r * kAStride + 16 * q, acc);
+    pf_loop<F, MT>(W, rb, a.I / kStep, lane, stage, (half_t *)smem, r * kAStride + 16 * q,
+                   __builtin_amdgcn_readfirstlane((nt + 15) / 16), acc);
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll

@@ -123,11 +123,6 @@ __device__ inline uint32_t wave_max_u32(uint32_t v)
     return max(max(lane_u32(v, 0), lane_u32(v, 16)), max(lane_u32(v, 32), lane_u32(v, 48)));
 }
 
-__device__ inline float wave_maxnum_f32(float v)
-{
-    v = row_max_f32(v);
-    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
-}
 
 // cpu.moeRoute (cpu.zig:1236-1288) for the token whose E logits start at `lg`.
 // Each unchosen expert with a non-NaN probability p carries key = bits(p) + 1 (p is
@@ -146,7 +141,7 @@ __device__ void route_wave(const float *__restrict__ lg, int E, int k, int norm,
     float mx = v[0];
 #pragma unroll
     for (int j = 1; j < VPL; j++) mx = fmaxf(mx, v[j]);
-    mx = wave_maxnum_f32(mx);  // @max over the row: NaN only if every logit is NaN
+    mx = wave_max(mx);  // @max over the row: NaN only if every logit is NaN
     float ex[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; j++) {
@@ -459,7 +454,7 @@ __device__ void act_prep_wave(const float *__restrict__ x, int rows, int K, cons
         float m = 0.0f;
 #pragma unroll
         for (int b = 0; b < B; b++) m = fmaxf(m, fabsf(v[b]));
-        const float sc = pow2_scale(wave_maxnum_f32(m)), inv = 1.0f / sc;
+        const float sc = pow2_scale(wave_max(m)), inv = 1.0f / sc;
 #pragma unroll
         for (int b = 0; b < B; b++)
             if (b < G) {
@@ -470,7 +465,7 @@ __device__ void act_prep_wave(const float *__restrict__ x, int rows, int K, cons
     }
     float m = 0.0f;
     for (int g = 0; g < G; g++) m = fmaxf(m, fabsf(xr[64 * g + lane]));
-    const float sc = pow2_scale(wave_maxnum_f32(m)), inv = 1.0f / sc;
+    const float sc = pow2_scale(wave_max(m)), inv = 1.0f / sc;
     for (int g = 0; g < G; g++) {
         q[64 * g + mma_pos(lane)] = (half_t)(xr[64 * g + lane] * sc);
         if (lane == 0) xq.ds[(size_t)g * xq.ld + w] = inv;
