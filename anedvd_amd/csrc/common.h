@@ -104,6 +104,7 @@ __host__ __device__ inline Fmt tile_fmt(int t)
     case ANEDVD_Q8_0: return Fmt{16, 4, 1, 32};
     case ANEDVD_Q4_0: return Fmt{8, 4, 1, 32};
     case ANEDVD_Q4_K: return Fmt{8, 16, 4, 256};
+    case ANEDVD_Q5_K: return Fmt{8, 16, 4, 256};
     case ANEDVD_Q6_K: return Fmt{8, 16, 4, 256};
     default: return Fmt{0, 0, 0, 0};
     }
@@ -117,7 +118,7 @@ struct QMat {
     int type;
     int rows, cols, n;            // n stacked matrices (experts)
     int steps, units;             // cols / 64, steps / steps-per-unit
-    uint8_t *q, *s, *h, *d;       // quant, scale and (Q6_K) h and d planes
+    uint8_t *q, *s, *h, *d;       // quant, scale, (Q5_K, Q6_K) high-bit and (Q6_K) d planes
     size_t q_stride, s_stride, h_stride, d_stride;  // bytes per matrix in each plane
 };
 
@@ -131,9 +132,12 @@ __host__ __device__ inline size_t tile_s_off(const Fmt &f, int units, int rb, in
     return ((((size_t)rb * units + u) * 4 + t) * 16 + n) * (size_t)f.sb;
 }
 
-__host__ __device__ inline size_t tile_h_off(int steps, int rb, int s, int t, int lane)
+// High-bit plane bytes per lane per (step, tile): Q6_K 2 bits per value, Q5_K 1.
+__host__ __device__ inline int tile_hb(int type) { return type == ANEDVD_Q6_K ? 4 : type == ANEDVD_Q5_K ? 2 : 0; }
+
+__host__ __device__ inline size_t tile_h_off(int steps, int rb, int s, int t, int lane, int hb)
 {
-    return ((((size_t)rb * steps + s) * 4 + t) * 64 + lane) * 4;
+    return ((((size_t)rb * steps + s) * 4 + t) * 64 + lane) * (size_t)hb;
 }
 
 __host__ __device__ inline size_t tile_d_off(int units, int rb, int u, int t, int n)

@@ -245,7 +245,7 @@ __global__ void k_dequant_gguf(int t, const uint8_t *__restrict__ src, size_t n_
 // bytes, so the repack and its inverse share one statement of each format.
 
 // Raw quant of element e of a GGUF block: Q8_0 the int8, Q4_0 / Q4_K the nibble,
-// Q6_K the 6-bit value (before the -32 offset).
+// Q5_K the 5-bit value, Q6_K the 6-bit value (before the -32 offset).
 __device__ inline int gguf_quant(int t, const uint8_t *blk, int e)
 {
     switch (t) {
@@ -255,6 +255,11 @@ __device__ inline int gguf_quant(int t, const uint8_t *blk, int e)
         const int g = e >> 6, l = e & 63;
         const uint8_t q = blk[16 + 32 * g + (l & 31)];
         return l < 32 ? q & 0xF : q >> 4;
+    }
+    case ANEDVD_Q5_K: {  // dequantQ5K (gguf.zig:998-1034): group e/64, nibble + qh bit 2 g + (l >= 32)
+        const int g = e >> 6, l = e & 63;
+        const uint8_t q = blk[48 + 32 * g + (l & 31)], qh = blk[16 + (l & 31)];
+        return (l < 32 ? q & 0xF : q >> 4) | (((qh >> (2 * g + (l >> 5))) & 1) << 4);
     }
     case ANEDVD_Q6_K: {  // dequantQ6K: half e/128, quarter (e%128)/32
         const int h = e >> 7, qd = (e & 127) >> 5, l = e & 31;
@@ -279,6 +284,13 @@ __device__ inline void set_gguf_quant(int t, uint8_t *blk, int e, int v)
         q = l < 32 ? (uint8_t)((q & 0xF0) | v) : (uint8_t)((q & 0x0F) | (v << 4));
         break;
     }
+    case ANEDVD_Q5_K: {
+        const int g = e >> 6, l = e & 63, sh = 2 * g + (l >> 5);
+        uint8_t &q = blk[48 + 32 * g + (l & 31)], &qh = blk[16 + (l & 31)];
+        q = l < 32 ? (uint8_t)((q & 0xF0) | (v & 0xF)) : (uint8_t)((q & 0x0F) | ((v & 0xF) << 4));
+        qh = (uint8_t)((qh & ~(1 << sh)) | (((v >> 4) & 1) << sh));
+        break;
+    }
     case ANEDVD_Q6_K: {
         const int h = e >> 7, qd = (e & 127) >> 5, l = e & 31;
         uint8_t &ql = blk[64 * h + l + (qd & 1) * 32], &qh = blk[128 + 32 * h + l];
@@ -299,9 +311,18 @@ __device__ inline void pack_lane(int t, const int *v, uint8_t *out)
         break;
     case ANEDVD_Q4_0:
     case ANEDVD_Q4_K:
+    case ANEDVD_Q5_K:
     case ANEDVD_Q6_K:
         for (int j = 0; j < 2; j++)
             for (int b = 0; b < 4; b++) out[4 * j + b] = (uint8_t)((v[8 * j + b] & 0xF) | ((v[8 * j + b + 4] & 0xF) << 4));
+        if (t == ANEDVD_Q5_K) {  // bit 4 (2 j + hh) + b: the fifth bit of value 8 j + 4 hh + b
+            int h = 0;
+            for (int j = 0; j < 2; j++)
+                for (int hh = 0; hh < 2; hh++)
+                    for (int b = 0; b < 4; b++) h |= ((v[8 * j + 4 * hh + b] >> 4) & 1) << (4 * (2 * j + hh) + b);
+            out[8] = (uint8_t)(h & 0xFF);
+            out[9] = (uint8_t)(h >> 8);
+        }
         if (t == ANEDVD_Q6_K)
             for (int b = 0; b < 4; b++) {
                 int h = 0;
@@ -322,6 +343,12 @@ __device__ inline int unpack_lane(int t, const uint8_t *in, int k)
     case ANEDVD_Q4_K: {
         const int j = k >> 3, i = k & 7;
         return (in[4 * j + (i & 3)] >> (4 * (i >> 2))) & 0xF;
+    }
+    case ANEDVD_Q5_K: {
+        const int j = k >> 3, i = k & 7;
+        const int lo = (in[4 * j + (i & 3)] >> (4 * (i >> 2))) & 0xF;
+        const int bit = 4 * (2 * j + (i >> 2)) + (i & 3);
+        return lo | (((in[8 + (bit >> 3)] >> (bit & 7)) & 1) << 4);
     }
     case ANEDVD_Q6_K: {
         const int j = k >> 3, i = k & 7;
@@ -355,13 +382,13 @@ __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
                 const int c = kStep * s + mma_col(g, k >> 3, k & 7);
                 v[k] = gguf_quant(m.type, row + (size_t)(c / epb) * bpb, c % epb);
             }
-            uint8_t lb[16];  // Q8_0: 16 quant bytes; Q6_K: 8 quant + 4 h bytes
+            uint8_t lb[16];  // Q8_0: 16 quant bytes; Q5_K / Q6_K: 8 quant + 2 / 4 high-bit bytes
             pack_lane(m.type, v, lb);
             uint8_t *dst = q + tile_q_off(f, m.steps, rb, s, t, 16 * g + n);
             for (int k = 0; k < f.qb; k++) dst[k] = lb[k];
-            if (m.type == ANEDVD_Q6_K) {
-                uint8_t *hd = m.h + (size_t)mat * m.h_stride + tile_h_off(m.steps, rb, s, t, 16 * g + n);
-                for (int k = 0; k < 4; k++) hd[k] = lb[8 + k];
+            if (const int hb = tile_hb(m.type)) {
+                uint8_t *hd = m.h + (size_t)mat * m.h_stride + tile_h_off(m.steps, rb, s, t, 16 * g + n, hb);
+                for (int k = 0; k < hb; k++) hd[k] = lb[8 + k];
             }
         }
     uint8_t *sc = m.s + (size_t)mat * m.s_stride + tile_s_off(f, m.units, rb, u, t, n);
@@ -376,6 +403,7 @@ __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
         sc[3] = b0[bpb + 1];
         break;
     case ANEDVD_Q4_K:  // d, dmin, 12 scale bytes
+    case ANEDVD_Q5_K:
         for (int k = 0; k < 16; k++) sc[k] = b0[k];
         break;
     case ANEDVD_Q6_K: {  // 16 int8 scales; d to the d plane
@@ -406,12 +434,12 @@ __global__ void k_dequant_tiles(QMat m, int mat, float *__restrict__ out)
     for (int e = 0; e < epb; e++) {
         const int c = b * epb + e, s = c / kStep, w = c % kStep;
         const int j = w >> 5, g = (w & 31) >> 3, i = w & 7;
-        uint8_t lb[16];  // Q8_0: 16 quant bytes; Q6_K: 8 quant + 4 h bytes
+        uint8_t lb[16];  // Q8_0: 16 quant bytes; Q5_K / Q6_K: 8 quant + 2 / 4 high-bit bytes
         const uint8_t *src = q + tile_q_off(f, m.steps, rb, s, t, 16 * g + n);
         for (int k = 0; k < f.qb; k++) lb[k] = src[k];
-        if (m.type == ANEDVD_Q6_K) {
-            const uint8_t *hs = m.h + (size_t)mat * m.h_stride + tile_h_off(m.steps, rb, s, t, 16 * g + n);
-            for (int k = 0; k < 4; k++) lb[8 + k] = hs[k];
+        if (const int hb = tile_hb(m.type)) {
+            const uint8_t *hs = m.h + (size_t)mat * m.h_stride + tile_h_off(m.steps, rb, s, t, 16 * g + n, hb);
+            for (int k = 0; k < hb; k++) lb[8 + k] = hs[k];
         }
         set_gguf_quant(m.type, blk, e, unpack_lane(m.type, lb, 8 * j + i));
     }
@@ -426,6 +454,7 @@ __global__ void k_dequant_tiles(QMat m, int mat, float *__restrict__ out)
         break;
     }
     case ANEDVD_Q4_K:
+    case ANEDVD_Q5_K:
         for (int k = 0; k < 16; k++) blk[k] = sc[k];
         break;
     case ANEDVD_Q6_K: {

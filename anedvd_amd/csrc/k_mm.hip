@@ -151,6 +151,54 @@ struct MQ4_K {
     }
 };
 
+// Q5_K: the Q4_K scheme on 5-bit values, the fifth bit from the high-bit plane.
+struct MQ5_K {
+    static constexpr bool kDeep = false;  // weights one step ahead
+    static constexpr int kSpu = 4;
+    static constexpr bool kMin = true;
+    struct Raw {
+        u32x2 q[4];
+        uint32_t h[4];
+        u32x4 sc[4];  // d, dmin, scales of the row's super-block (first step of a unit)
+    };
+    using State = MQ4_K::State;
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 2);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
+            r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * t, ho, kNT);
+        }
+        if ((s & 3) == 0) {
+            const int so = row_plane_off(p, rb, s >> 2, 16);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * t, so, kNT);
+        }
+    }
+    __device__ static inline void begin(const Raw &r, State &st, int s)
+    {
+        if ((s & 3) == 0) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) st.sc[t] = r.sc[t];
+        }
+    }
+    __device__ static inline void operand(const Raw &r, const State &st, int s, int, int t, int j, half8 &b, float &d,
+                                          float &mn)
+    {
+        const uint32_t v = r.q[t][j], hb = r.h[t];
+        const uint32_t lo = (v & 0x0F0F0F0Fu) | bit4_of_bytes(hb >> (8 * j));
+        const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes(hb >> (8 * j + 4));
+        b = bytes_h8(lo, hi) - (half_t)1024.0f;  // q in [0, 31]
+        const u32x4 sc = st.sc[t];
+        int a, m;
+        scale_min_k4(2 * (s & 3) + j, sc.y, sc.z, sc.w, a, m);
+        d = f16_bits_to_f32((uint16_t)(sc.x & 0xFFFFu)) * (float)a;
+        mn = f16_bits_to_f32((uint16_t)(sc.x >> 16)) * (float)m;
+    }
+};
+
 // Q6_K: the lane's 8 columns of block j lie in sub-block 4 (s % 4) + 2 j + g / 2;
 // its int8 scale is folded into the f16 weights and the super-block's d applied
 // to the result.
@@ -789,6 +837,7 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
     case ANEDVD_Q8_0: rc = launch_gateup_d<MQ8_0>(a, plan.mt, st); break;
     case ANEDVD_Q4_0: rc = launch_gateup_d<MQ4_0>(a, plan.mt, st); break;
     case ANEDVD_Q4_K: rc = launch_gateup_d<MQ4_K>(a, plan.mt, st); break;
+    case ANEDVD_Q5_K: rc = launch_gateup_d<MQ5_K>(a, plan.mt, st); break;
     case ANEDVD_Q6_K: rc = launch_gateup_d<MQ6_K>(a, plan.mt, st); break;
     default:
         set_error("expert gate/up: ggml type %d has no kernel", gate.type);
@@ -819,6 +868,7 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
     case ANEDVD_Q8_0: return launch_down_d<MQ8_0>(a, plan.mt, st);
     case ANEDVD_Q4_0: return launch_down_d<MQ4_0>(a, plan.mt, st);
     case ANEDVD_Q4_K: return launch_down_d<MQ4_K>(a, plan.mt, st);
+    case ANEDVD_Q5_K: return launch_down_d<MQ5_K>(a, plan.mt, st);
     case ANEDVD_Q6_K: return launch_down_d<MQ6_K>(a, plan.mt, st);
     default:
         set_error("expert down: ggml type %d has no kernel", down.type);

@@ -155,6 +155,50 @@ struct FQ4_K {
     }
 };
 
+// Q5_K: y = d1 q - m1 (gguf.zig:998-1034), the Q4_K scheme with the fifth bit of
+// each value from the high-bit plane (2 bytes per lane per step).
+struct FQ5_K {
+    static constexpr int kSpu = 4;
+    static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
+    static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
+    struct Raw {
+        u32x2 q[kPfTiles];
+        uint32_t h[kPfTiles];
+        u32x4 sc[kPfTiles];  // d, dmin, scales: loaded on a unit's first step
+    };
+    using State = FQ4_K::State;
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 2);
+#pragma unroll
+        for (int tt = 0; tt < kPfTiles; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * tt, ho, kNT);
+        }
+        if ((s & 3) == 0) {
+            const int so = row_plane_off(p, rb, s >> 2, 16);
+#pragma unroll
+            for (int tt = 0; tt < kPfTiles; tt++)
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
+        }
+    }
+    __device__ static inline void begin(const Raw &r, State &st, int ss, int lane)
+    {
+        FQ4_K::Raw k;
+#pragma unroll
+        for (int tt = 0; tt < kPfTiles; tt++) k.sc[tt] = r.sc[tt];
+        FQ4_K::begin(k, st, ss, lane);
+    }
+    __device__ static inline half8 bop(const Raw &r, const State &st, int ss, int tt, int j, int)
+    {
+        const uint32_t v = r.q[tt][j], hb = r.h[tt];
+        const uint32_t lo = (v & 0x0F0F0F0Fu) | bit4_of_bytes(hb >> (8 * j));
+        const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes(hb >> (8 * j + 4));
+        const half8 q = bytes_h8(lo, hi) - (half_t)1024.0f;  // exact q in [0, 31]
+        return q * st.d1[tt][2 * ss + j] - st.m1[tt][2 * ss + j];
+    }
+};
+
 // Q6_K: y = d * sc * q (gguf.zig:1036-1059) with d * sc formed in f32 once per
 // super-block and kept as f16; q - 32 is exact and the product rounds once.  The
 // lane's 8 columns of block j lie in sub-block 4 ss + 2 j + g / 2.
@@ -559,6 +603,7 @@ static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStr
     case ANEDVD_Q8_0: return launch_pf_mt<FQ8_0>(a, mt, gateup, st);
     case ANEDVD_Q4_0: return launch_pf_mt<FQ4_0>(a, mt, gateup, st);
     case ANEDVD_Q4_K: return launch_pf_mt<FQ4_K>(a, mt, gateup, st);
+    case ANEDVD_Q5_K: return launch_pf_mt<FQ5_K>(a, mt, gateup, st);
     case ANEDVD_Q6_K: return launch_pf_mt<FQ6_K>(a, mt, gateup, st);
     default:
         set_error("grouped GEMM: ggml type %d has no kernel", type);

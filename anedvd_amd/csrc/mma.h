@@ -30,6 +30,10 @@ __device__ inline half8 bytes_h8(uint32_t lo, uint32_t hi)
     return h;
 }
 
+// Bit b (b < 4) of x -> bit 4 of byte b: the fifth bits of four packed values
+// (one full-rate 24-bit multiply spreads them 7 bits apart per step).
+__device__ inline uint32_t bit4_of_bytes(uint32_t x) { return ((x & 0xFu) * 0x00204081u & 0x01010101u) << 4; }
+
 __device__ inline uint32_t pick4(u32x4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // Raw buffer loads: a wave-uniform descriptor (base, size), a per-lane byte offset

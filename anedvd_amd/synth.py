@@ -101,7 +101,17 @@ def q6_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int
     return blk
 
 
-_GEN = {W.Q8_0: q8_0, W.Q4_0: q4_0, W.Q4_K: q4_k, W.Q6_K: q6_k}
+def q5_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q5_K super-blocks: d, dmin = f16(|N(0,sigma)|); random 12-byte packed 6-bit
+    scales/mins, random high bits qh[32] and 4-bit quants qs[128]."""
+    blk = np.empty((n_blocks, 176), dtype=np.uint8)
+    blk[:, 0:2] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 2:4] = _f16_abs_normal(seed, stream + 1, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 4:] = rand_bytes(seed, stream + 2, n_blocks * 172, offset * 172).reshape(n_blocks, 172)
+    return blk
+
+
+_GEN = {W.Q8_0: q8_0, W.Q4_0: q4_0, W.Q4_K: q4_k, W.Q5_K: q5_k, W.Q6_K: q6_k}
 
 
 def quant_matrix(t: int, seed: int, stream: int, n_elems: int, sigma: float, elem_offset: int = 0) -> np.ndarray:
