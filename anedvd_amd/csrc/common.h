@@ -102,7 +102,11 @@ __host__ __device__ inline Fmt tile_fmt(int t)
 {
     switch (t) {
     case ANEDVD_Q8_0: return Fmt{16, 4, 1, 32};
+    case ANEDVD_Q8_1: return Fmt{16, 4, 1, 32};
     case ANEDVD_Q4_0: return Fmt{8, 4, 1, 32};
+    case ANEDVD_Q4_1: return Fmt{8, 8, 1, 32};
+    case ANEDVD_Q5_0: return Fmt{8, 4, 1, 32};
+    case ANEDVD_Q5_1: return Fmt{8, 8, 1, 32};
     case ANEDVD_Q4_K: return Fmt{8, 16, 4, 256};
     case ANEDVD_Q5_K: return Fmt{8, 16, 4, 256};
     case ANEDVD_Q6_K: return Fmt{8, 16, 4, 256};
@@ -132,8 +136,12 @@ __host__ __device__ inline size_t tile_s_off(const Fmt &f, int units, int rb, in
     return ((((size_t)rb * units + u) * 4 + t) * 16 + n) * (size_t)f.sb;
 }
 
-// High-bit plane bytes per lane per (step, tile): Q6_K 2 bits per value, Q5_K 1.
-__host__ __device__ inline int tile_hb(int type) { return type == ANEDVD_Q6_K ? 4 : type == ANEDVD_Q5_K ? 2 : 0; }
+// High-bit plane bytes per lane per (step, tile): Q6_K 2 bits per value, the
+// 5-bit formats 1.
+__host__ __device__ inline int tile_hb(int type)
+{
+    return type == ANEDVD_Q6_K ? 4 : (type == ANEDVD_Q5_K || type == ANEDVD_Q5_0 || type == ANEDVD_Q5_1) ? 2 : 0;
+}
 
 __host__ __device__ inline size_t tile_h_off(int steps, int rb, int s, int t, int lane, int hb)
 {

@@ -244,13 +244,23 @@ __global__ void k_dequant_gguf(int t, const uint8_t *__restrict__ src, size_t n_
 // and set_gguf_quant() read and write one element's raw quant in GGUF block
 // bytes, so the repack and its inverse share one statement of each format.
 
-// Raw quant of element e of a GGUF block: Q8_0 the int8, Q4_0 / Q4_K the nibble,
-// Q5_K the 5-bit value, Q6_K the 6-bit value (before the -32 offset).
+// Raw quant of element e of a GGUF block: Q8_0 / Q8_1 the int8, Q4_0 / Q4_1 / Q4_K
+// the nibble, Q5_0 / Q5_1 / Q5_K the 5-bit value (before Q5_0's -16 offset), Q6_K
+// the 6-bit value (before the -32 offset).
 __device__ inline int gguf_quant(int t, const uint8_t *blk, int e)
 {
     switch (t) {
     case ANEDVD_Q8_0: return (int)(int8_t)blk[2 + e];
+    case ANEDVD_Q8_1: return (int)(int8_t)blk[4 + e];  // dequantQ8_1: qs after d and s
     case ANEDVD_Q4_0: return e < 16 ? blk[2 + e] & 0xF : blk[2 + e - 16] >> 4;  // dequantQ4_0
+    case ANEDVD_Q4_1: return e < 16 ? blk[4 + e] & 0xF : blk[4 + e - 16] >> 4;  // dequantQ4_1
+    case ANEDVD_Q5_0:
+    case ANEDVD_Q5_1: {  // dequantQ5 (gguf.zig:795-822): nibble of qs[e % 16], bit e of qh
+        const int o = t == ANEDVD_Q5_1 ? 4 : 2;
+        const uint32_t qh = blk[o] | (blk[o + 1] << 8) | (blk[o + 2] << 16) | ((uint32_t)blk[o + 3] << 24);
+        const int nib = e < 16 ? blk[o + 4 + e] & 0xF : blk[o + 4 + e - 16] >> 4;
+        return nib | (int)(((qh >> e) & 1) << 4);
+    }
     case ANEDVD_Q4_K: {  // dequantQ4K: group e/64, low nibbles first, then high
         const int g = e >> 6, l = e & 63;
         const uint8_t q = blk[16 + 32 * g + (l & 31)];
@@ -274,10 +284,23 @@ __device__ inline void set_gguf_quant(int t, uint8_t *blk, int e, int v)
 {
     switch (t) {
     case ANEDVD_Q8_0: blk[2 + e] = (uint8_t)v; break;
+    case ANEDVD_Q8_1: blk[4 + e] = (uint8_t)v; break;
     case ANEDVD_Q4_0:
-        if (e < 16) blk[2 + e] = (uint8_t)((blk[2 + e] & 0xF0) | v);
-        else blk[2 + e - 16] = (uint8_t)((blk[2 + e - 16] & 0x0F) | (v << 4));
+    case ANEDVD_Q4_1: {
+        const int o = t == ANEDVD_Q4_1 ? 4 : 2;
+        if (e < 16) blk[o + e] = (uint8_t)((blk[o + e] & 0xF0) | v);
+        else blk[o + e - 16] = (uint8_t)((blk[o + e - 16] & 0x0F) | (v << 4));
         break;
+    }
+    case ANEDVD_Q5_0:
+    case ANEDVD_Q5_1: {
+        const int o = t == ANEDVD_Q5_1 ? 4 : 2;
+        uint8_t &q = e < 16 ? blk[o + 4 + e] : blk[o + 4 + e - 16];
+        q = e < 16 ? (uint8_t)((q & 0xF0) | (v & 0xF)) : (uint8_t)((q & 0x0F) | ((v & 0xF) << 4));
+        uint8_t &h = blk[o + (e >> 3)];
+        h = (uint8_t)((h & ~(1 << (e & 7))) | (((v >> 4) & 1) << (e & 7)));
+        break;
+    }
     case ANEDVD_Q4_K: {
         const int g = e >> 6, l = e & 63;
         uint8_t &q = blk[16 + 32 * g + (l & 31)];
@@ -307,15 +330,19 @@ __device__ inline void pack_lane(int t, const int *v, uint8_t *out)
 {
     switch (t) {
     case ANEDVD_Q8_0:
+    case ANEDVD_Q8_1:
         for (int k = 0; k < 16; k++) out[k] = (uint8_t)((v[k] + 128) & 0xFF);
         break;
     case ANEDVD_Q4_0:
+    case ANEDVD_Q4_1:
+    case ANEDVD_Q5_0:
+    case ANEDVD_Q5_1:
     case ANEDVD_Q4_K:
     case ANEDVD_Q5_K:
     case ANEDVD_Q6_K:
         for (int j = 0; j < 2; j++)
             for (int b = 0; b < 4; b++) out[4 * j + b] = (uint8_t)((v[8 * j + b] & 0xF) | ((v[8 * j + b + 4] & 0xF) << 4));
-        if (t == ANEDVD_Q5_K) {  // bit 4 (2 j + hh) + b: the fifth bit of value 8 j + 4 hh + b
+        if (tile_hb(t) == 2) {  // bit 4 (2 j + hh) + b: the fifth bit of value 8 j + 4 hh + b
             int h = 0;
             for (int j = 0; j < 2; j++)
                 for (int hh = 0; hh < 2; hh++)
@@ -338,12 +365,16 @@ __device__ inline void pack_lane(int t, const int *v, uint8_t *out)
 __device__ inline int unpack_lane(int t, const uint8_t *in, int k)
 {
     switch (t) {
-    case ANEDVD_Q8_0: return (int)in[k] - 128;
+    case ANEDVD_Q8_0:
+    case ANEDVD_Q8_1: return (int)in[k] - 128;
     case ANEDVD_Q4_0:
+    case ANEDVD_Q4_1:
     case ANEDVD_Q4_K: {
         const int j = k >> 3, i = k & 7;
         return (in[4 * j + (i & 3)] >> (4 * (i >> 2))) & 0xF;
     }
+    case ANEDVD_Q5_0:
+    case ANEDVD_Q5_1:
     case ANEDVD_Q5_K: {
         const int j = k >> 3, i = k & 7;
         const int lo = (in[4 * j + (i & 3)] >> (4 * (i >> 2))) & 0xF;
@@ -362,9 +393,11 @@ __device__ inline int unpack_lane(int t, const uint8_t *in, int k)
 
 // One thread per (matrix, row, scale unit): moves the unit's quants and scales
 // from the stacked GGUF payload `src` (matrices slowest) into the tile layout.
+template <int TYPE>
 __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
 {
-    const Fmt f = tile_fmt(m.type);
+    m.type = TYPE;  // one instantiation per format: every format switch below folds
+    const Fmt f = tile_fmt(TYPE);
     const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t per_mat = (size_t)m.rows * m.units;
     if (id >= per_mat * m.n) return;
@@ -396,11 +429,20 @@ __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
     const uint8_t *b0 = row + (size_t)(c0 / epb) * bpb;
     switch (m.type) {
     case ANEDVD_Q8_0:
-    case ANEDVD_Q4_0:  // the f16 d of the step's two blocks
+    case ANEDVD_Q8_1:
+    case ANEDVD_Q4_0:
+    case ANEDVD_Q5_0:  // the f16 d of the step's two blocks
         sc[0] = b0[0];
         sc[1] = b0[1];
         sc[2] = b0[bpb];
         sc[3] = b0[bpb + 1];
+        break;
+    case ANEDVD_Q4_1:
+    case ANEDVD_Q5_1:  // d, m of the step's two blocks
+        for (int k = 0; k < 4; k++) {
+            sc[k] = b0[k];
+            sc[4 + k] = b0[bpb + k];
+        }
         break;
     case ANEDVD_Q4_K:  // d, dmin, 12 scale bytes
     case ANEDVD_Q5_K:
@@ -419,9 +461,11 @@ __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
 
 // One thread per GGUF block of matrix `mat`: rebuilds the block's bytes from the
 // tile layout and dequantises them (out[rows][cols] f32, bit-exact).
+template <int TYPE>
 __global__ void k_dequant_tiles(QMat m, int mat, float *__restrict__ out)
 {
-    const Fmt f = tile_fmt(m.type);
+    m.type = TYPE;  // one instantiation per format: every format switch below folds
+    const Fmt f = tile_fmt(TYPE);
     const int bpb = block_bytes(m.type), epb = block_elems(m.type);
     const int bpr = m.cols / epb;
     const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -447,10 +491,18 @@ __global__ void k_dequant_tiles(QMat m, int mat, float *__restrict__ out)
     const uint8_t *sc = m.s + (size_t)mat * m.s_stride + tile_s_off(f, m.units, rb, u, t, n);
     switch (m.type) {
     case ANEDVD_Q8_0:
-    case ANEDVD_Q4_0: {
+    case ANEDVD_Q8_1:  // (Q8_1's s is not read by its dequantisation; it stays 0)
+    case ANEDVD_Q4_0:
+    case ANEDVD_Q5_0: {
         const int j = (b * epb / 32) & 1;  // which of the step's two blocks
         blk[0] = sc[2 * j];
         blk[1] = sc[2 * j + 1];
+        break;
+    }
+    case ANEDVD_Q4_1:
+    case ANEDVD_Q5_1: {
+        const int j = (b * epb / 32) & 1;
+        for (int k = 0; k < 4; k++) blk[k] = sc[4 * j + k];
         break;
     }
     case ANEDVD_Q4_K:
@@ -480,10 +532,23 @@ int launch_dequant_gguf(int t, const uint8_t *d_src, size_t n_blocks, float *d_o
     return ANEDVD_OK;
 }
 
+// The formats with a tile layout, for the per-format kernel instantiations.
+#define ANEDVD_TILE_TYPES(X) X(ANEDVD_Q8_0) X(ANEDVD_Q8_1) X(ANEDVD_Q4_0) X(ANEDVD_Q4_1) X(ANEDVD_Q5_0) \
+    X(ANEDVD_Q5_1) X(ANEDVD_Q4_K) X(ANEDVD_Q5_K) X(ANEDVD_Q6_K)
+
 int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st)
 {
     const size_t n = (size_t)m.n * m.rows * m.units;
-    hipLaunchKernelGGL(k_repack, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, d_src);
+    const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    switch (m.type) {
+#define ANEDVD_CASE(T) \
+    case T: hipLaunchKernelGGL(k_repack<T>, grid, block, 0, st, m, d_src); break;
+        ANEDVD_TILE_TYPES(ANEDVD_CASE)
+#undef ANEDVD_CASE
+    default:
+        set_error("repack: ggml type %d has no tile layout", m.type);
+        return ANEDVD_E_UNSUPPORTED_TYPE;
+    }
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }
@@ -491,7 +556,16 @@ int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st)
 int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st)
 {
     const size_t n = (size_t)m.rows * (m.cols / block_elems(m.type));
-    hipLaunchKernelGGL(k_dequant_tiles, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, mat, d_out);
+    const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    switch (m.type) {
+#define ANEDVD_CASE(T) \
+    case T: hipLaunchKernelGGL(k_dequant_tiles<T>, grid, block, 0, st, m, mat, d_out); break;
+        ANEDVD_TILE_TYPES(ANEDVD_CASE)
+#undef ANEDVD_CASE
+    default:
+        set_error("dequant_tiles: ggml type %d has no tile layout", m.type);
+        return ANEDVD_E_UNSUPPORTED_TYPE;
+    }
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }

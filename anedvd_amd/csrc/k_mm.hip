@@ -106,6 +106,64 @@ struct MQ4_0 {
     }
 };
 
+// Q4_1 / Q5_1 (y = d q + m, gguf.zig:778-822) and Q5_0 (y = d (q - 16)): 32-element
+// blocks, the step's two blocks' d (and m) in the scale plane, the 5-bit formats'
+// fifth bits in the high-bit plane.  The min coefficient is -m.
+template <bool kFive, bool kHasMin>
+struct MQLegacy {
+    static constexpr bool kDeep = true;  // weights two steps ahead
+    static constexpr int kSpu = 1;
+    static constexpr bool kMin = kHasMin;
+    struct Raw {
+        u32x2 q[4];
+        uint32_t h[kFive ? 4 : 1];
+        u32x2 s[4];  // (d0 | m0 << 16, d1 | m1 << 16) with a min, else (d0 | d1 << 16, -)
+    };
+    struct State {};
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, kHasMin ? 8 : 4);
+#pragma unroll
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
+        if constexpr (kFive) {
+            const int ho = lane_plane_off(p, rb, s, 2);
+#pragma unroll
+            for (int t = 0; t < 4; t++) r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * t, ho, kNT);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            if constexpr (kHasMin)
+                r.s[t] = __builtin_amdgcn_raw_buffer_load_b64(p.s, 8 * (lane & 15) + 128 * t, so, kNT);
+            else
+                r.s[t].x = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * t, so, kNT);
+        }
+    }
+    __device__ static inline void begin(const Raw &, State &, int) {}
+    __device__ static inline void operand(const Raw &r, const State &, int, int, int t, int j, half8 &b, float &d,
+                                          float &mn)
+    {
+        const uint32_t v = r.q[t][j];
+        uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+        if constexpr (kFive) {
+            lo |= bit4_of_bytes(r.h[t] >> (8 * j));
+            hi |= bit4_of_bytes(r.h[t] >> (8 * j + 4));
+        }
+        // Q5_0 values are q - 16; the others the raw quant
+        b = bytes_h8(lo, hi) - (half_t)(kFive && !kHasMin ? 1040.0f : 1024.0f);
+        if constexpr (kHasMin) {
+            const uint32_t dm = r.s[t][j];
+            d = f16_bits_to_f32((uint16_t)(dm & 0xFFFFu));
+            mn = -f16_bits_to_f32((uint16_t)(dm >> 16));
+        } else {
+            d = f16_bits_to_f32((uint16_t)(r.s[t].x >> (16 * j)));
+            mn = 0.0f;
+        }
+    }
+};
+using MQ4_1 = MQLegacy<false, true>;
+using MQ5_0 = MQLegacy<true, false>;
+using MQ5_1 = MQLegacy<true, true>;
+
 // Q4_K: step s covers sub-blocks 2 (s % 4) + j; y = d1 n - m1 with d1 = d * sc,
 // m1 = dmin * m.
 struct MQ4_K {
@@ -834,8 +892,12 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
     a.nchunk = plan.nchunk;
     int rc;
     switch (gate.type) {
-    case ANEDVD_Q8_0: rc = launch_gateup_d<MQ8_0>(a, plan.mt, st); break;
+    case ANEDVD_Q8_0:
+    case ANEDVD_Q8_1: rc = launch_gateup_d<MQ8_0>(a, plan.mt, st); break;  // one tile layout
     case ANEDVD_Q4_0: rc = launch_gateup_d<MQ4_0>(a, plan.mt, st); break;
+    case ANEDVD_Q4_1: rc = launch_gateup_d<MQ4_1>(a, plan.mt, st); break;
+    case ANEDVD_Q5_0: rc = launch_gateup_d<MQ5_0>(a, plan.mt, st); break;
+    case ANEDVD_Q5_1: rc = launch_gateup_d<MQ5_1>(a, plan.mt, st); break;
     case ANEDVD_Q4_K: rc = launch_gateup_d<MQ4_K>(a, plan.mt, st); break;
     case ANEDVD_Q5_K: rc = launch_gateup_d<MQ5_K>(a, plan.mt, st); break;
     case ANEDVD_Q6_K: rc = launch_gateup_d<MQ6_K>(a, plan.mt, st); break;
@@ -865,8 +927,12 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
     a.P = P;
     a.nchunk = plan.nchunk;
     switch (down.type) {
-    case ANEDVD_Q8_0: return launch_down_d<MQ8_0>(a, plan.mt, st);
+    case ANEDVD_Q8_0:
+    case ANEDVD_Q8_1: return launch_down_d<MQ8_0>(a, plan.mt, st);
     case ANEDVD_Q4_0: return launch_down_d<MQ4_0>(a, plan.mt, st);
+    case ANEDVD_Q4_1: return launch_down_d<MQ4_1>(a, plan.mt, st);
+    case ANEDVD_Q5_0: return launch_down_d<MQ5_0>(a, plan.mt, st);
+    case ANEDVD_Q5_1: return launch_down_d<MQ5_1>(a, plan.mt, st);
     case ANEDVD_Q4_K: return launch_down_d<MQ4_K>(a, plan.mt, st);
     case ANEDVD_Q5_K: return launch_down_d<MQ5_K>(a, plan.mt, st);
     case ANEDVD_Q6_K: return launch_down_d<MQ6_K>(a, plan.mt, st);

@@ -105,6 +105,60 @@ struct FQ4_0 {
     }
 };
 
+// Q4_1 / Q5_1: y = d q + m (gguf.zig:778-822), d q + m rounded once to f16; Q5_0:
+// y = d (q - 16), rounded once.  The 5-bit formats' fifth bits come from the
+// high-bit plane.
+template <bool kFive, bool kHasMin>
+struct FQLegacy {
+    static constexpr int kSpu = 1;
+    static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
+    static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
+    struct Raw {
+        u32x2 q[kPfTiles];
+        uint32_t h[kFive ? kPfTiles : 1];
+        u32x2 s[kPfTiles];  // (d0 | m0 << 16, d1 | m1 << 16) with a min, else (d0 | d1 << 16, -)
+    };
+    struct State {};
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, kHasMin ? 8 : 4);
+#pragma unroll
+        for (int tt = 0; tt < kPfTiles; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
+            if constexpr (kHasMin)
+                r.s[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.s, 8 * (lane & 15) + 128 * tt, so, kNT);
+            else
+                r.s[tt].x = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * tt, so, kNT);
+        }
+        if constexpr (kFive) {
+            const int ho = lane_plane_off(p, rb, s, 2);
+#pragma unroll
+            for (int tt = 0; tt < kPfTiles; tt++)
+                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * tt, ho, kNT);
+        }
+    }
+    __device__ static inline void begin(const Raw &, State &, int, int) {}
+    __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int)
+    {
+        const uint32_t v = r.q[tt][j];
+        uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+        if constexpr (kFive) {
+            lo |= bit4_of_bytes(r.h[tt] >> (8 * j));
+            hi |= bit4_of_bytes(r.h[tt] >> (8 * j + 4));
+        }
+        const half8 q = bytes_h8(lo, hi) - (half_t)(kFive && !kHasMin ? 1040.0f : 1024.0f);  // exact
+        if constexpr (kHasMin) {
+            const uint32_t dm = r.s[tt][j];
+            return q * h_bits(dm) + h_bits(dm >> 16);
+        } else {
+            return q * h_bits(r.s[tt].x >> (16 * j));
+        }
+    }
+};
+using FQ4_1 = FQLegacy<false, true>;
+using FQ5_0 = FQLegacy<true, false>;
+using FQ5_1 = FQLegacy<true, true>;
+
 // Q4_K: y = d1 * n - m1 (gguf.zig:960-996) with d1 = d * sc and m1 = dmin * m
 // formed in f32 once per super-block and kept as f16; the nibble n is exact and
 // the f16 FMA rounds once, so a weight is within 2^-10 of its scale.
@@ -600,8 +654,12 @@ static int launch_pf_mt(const PfArgs &a, int, bool gateup, hipStream_t st)
 static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStream_t st)
 {
     switch (type) {
-    case ANEDVD_Q8_0: return launch_pf_mt<FQ8_0>(a, mt, gateup, st);
+    case ANEDVD_Q8_0:
+    case ANEDVD_Q8_1: return launch_pf_mt<FQ8_0>(a, mt, gateup, st);  // one tile layout
     case ANEDVD_Q4_0: return launch_pf_mt<FQ4_0>(a, mt, gateup, st);
+    case ANEDVD_Q4_1: return launch_pf_mt<FQ4_1>(a, mt, gateup, st);
+    case ANEDVD_Q5_0: return launch_pf_mt<FQ5_0>(a, mt, gateup, st);
+    case ANEDVD_Q5_1: return launch_pf_mt<FQ5_1>(a, mt, gateup, st);
     case ANEDVD_Q4_K: return launch_pf_mt<FQ4_K>(a, mt, gateup, st);
     case ANEDVD_Q5_K: return launch_pf_mt<FQ5_K>(a, mt, gateup, st);
     case ANEDVD_Q6_K: return launch_pf_mt<FQ6_K>(a, mt, gateup, st);

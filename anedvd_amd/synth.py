@@ -83,6 +83,46 @@ def q4_0(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int
     return blk
 
 
+def q8_1(seed: int, stream: int, n_blocks: int, sigma: float = 0.02, offset: int = 0) -> np.ndarray:
+    """Q8_1 blocks: d = f16(|N(0,sigma)|/127), s = f16(d * sum(qs)), qs uniform int8 in [-127, 127]."""
+    b0 = q8_0(seed, stream, n_blocks, sigma, offset)
+    blk = np.empty((n_blocks, 36), dtype=np.uint8)
+    blk[:, 0:2] = b0[:, 0:2]
+    qs = b0[:, 2:].view(np.int8).astype(np.float32)
+    d = b0[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    blk[:, 2:4] = (d * qs.sum(axis=1)).astype(np.float16).view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 4:] = b0[:, 2:]
+    return blk
+
+
+def q4_1(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q4_1 blocks: d = f16(|N(0,sigma)|), m = f16(N(0,sigma) * 8), random nibbles."""
+    blk = np.empty((n_blocks, 20), dtype=np.uint8)
+    blk[:, 0:2] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    m = (normal(seed, stream + 1, n_blocks, offset) * sigma * 8).astype(np.float16)
+    blk[:, 2:4] = m.view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 4:] = rand_bytes(seed, stream + 2, n_blocks * 16, offset * 16).reshape(n_blocks, 16)
+    return blk
+
+
+def q5_0(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q5_0 blocks: d = f16(|N(0,sigma)|), random qh and nibbles."""
+    blk = np.empty((n_blocks, 22), dtype=np.uint8)
+    blk[:, 0:2] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 2:] = rand_bytes(seed, stream + 2, n_blocks * 20, offset * 20).reshape(n_blocks, 20)
+    return blk
+
+
+def q5_1(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q5_1 blocks: d = f16(|N(0,sigma)|), m = f16(N(0,sigma) * 16), random qh and nibbles."""
+    blk = np.empty((n_blocks, 24), dtype=np.uint8)
+    blk[:, 0:2] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset).view(np.uint8).reshape(n_blocks, 2)
+    m = (normal(seed, stream + 1, n_blocks, offset) * sigma * 16).astype(np.float16)
+    blk[:, 2:4] = m.view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 4:] = rand_bytes(seed, stream + 2, n_blocks * 20, offset * 20).reshape(n_blocks, 20)
+    return blk
+
+
 def q4_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
     """Q4_K super-blocks: d, dmin = f16(|N(0,sigma)|); random 12-byte packed 6-bit
     scales/mins; random 4-bit quants."""
@@ -111,7 +151,8 @@ def q5_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int
     return blk
 
 
-_GEN = {W.Q8_0: q8_0, W.Q4_0: q4_0, W.Q4_K: q4_k, W.Q5_K: q5_k, W.Q6_K: q6_k}
+_GEN = {W.Q8_0: q8_0, W.Q8_1: q8_1, W.Q4_0: q4_0, W.Q4_1: q4_1, W.Q5_0: q5_0, W.Q5_1: q5_1, W.Q4_K: q4_k,
+        W.Q5_K: q5_k, W.Q6_K: q6_k}
 
 
 def quant_matrix(t: int, seed: int, stream: int, n_elems: int, sigma: float, elem_offset: int = 0) -> np.ndarray:
