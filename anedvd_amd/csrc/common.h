@@ -107,6 +107,8 @@ __host__ __device__ inline Fmt tile_fmt(int t)
     case ANEDVD_Q4_1: return Fmt{8, 8, 1, 32};
     case ANEDVD_Q5_0: return Fmt{8, 4, 1, 32};
     case ANEDVD_Q5_1: return Fmt{8, 8, 1, 32};
+    case ANEDVD_Q2_K: return Fmt{4, 16, 4, 256};
+    case ANEDVD_Q3_K: return Fmt{4, 16, 4, 256};
     case ANEDVD_Q4_K: return Fmt{8, 16, 4, 256};
     case ANEDVD_Q5_K: return Fmt{8, 16, 4, 256};
     case ANEDVD_Q6_K: return Fmt{8, 16, 4, 256};
@@ -122,7 +124,7 @@ struct QMat {
     int type;
     int rows, cols, n;            // n stacked matrices (experts)
     int steps, units;             // cols / 64, steps / steps-per-unit
-    uint8_t *q, *s, *h, *d;       // quant, scale, (Q5_K, Q6_K) high-bit and (Q6_K) d planes
+    uint8_t *q, *s, *h, *d;       // quant, scale, high-bit (tile_hb) and super-block scale (tile_db) planes
     size_t q_stride, s_stride, h_stride, d_stride;  // bytes per matrix in each plane
 };
 
@@ -137,10 +139,18 @@ __host__ __device__ inline size_t tile_s_off(const Fmt &f, int units, int rb, in
 }
 
 // High-bit plane bytes per lane per (step, tile): Q6_K 2 bits per value, the
-// 5-bit formats 1.
+// 5-bit formats and Q3_K 1.
 __host__ __device__ inline int tile_hb(int type)
 {
-    return type == ANEDVD_Q6_K ? 4 : (type == ANEDVD_Q5_K || type == ANEDVD_Q5_0 || type == ANEDVD_Q5_1) ? 2 : 0;
+    return type == ANEDVD_Q6_K ? 4
+           : (type == ANEDVD_Q5_K || type == ANEDVD_Q5_0 || type == ANEDVD_Q5_1 || type == ANEDVD_Q3_K) ? 2
+                                                                                                          : 0;
+}
+
+// Super-block scale (d plane) bytes per row per scale unit: Q6_K and Q3_K d, Q2_K d and dmin.
+__host__ __device__ inline int tile_db(int type)
+{
+    return (type == ANEDVD_Q6_K || type == ANEDVD_Q3_K) ? 2 : type == ANEDVD_Q2_K ? 4 : 0;
 }
 
 __host__ __device__ inline size_t tile_h_off(int steps, int rb, int s, int t, int lane, int hb)
@@ -148,9 +158,9 @@ __host__ __device__ inline size_t tile_h_off(int steps, int rb, int s, int t, in
     return ((((size_t)rb * steps + s) * 4 + t) * 64 + lane) * (size_t)hb;
 }
 
-__host__ __device__ inline size_t tile_d_off(int units, int rb, int u, int t, int n)
+__host__ __device__ inline size_t tile_d_off(int units, int rb, int u, int t, int n, int db)
 {
-    return ((((size_t)rb * units + u) * 4 + t) * 16 + n) * 2;
+    return ((((size_t)rb * units + u) * 4 + t) * 16 + n) * (size_t)db;
 }
 
 // Column of lane group g's value (j, i) within a 64-column step.

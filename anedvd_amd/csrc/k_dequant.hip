@@ -244,6 +244,15 @@ __global__ void k_dequant_gguf(int t, const uint8_t *__restrict__ src, size_t n_
 // and set_gguf_quant() read and write one element's raw quant in GGUF block
 // bytes, so the repack and its inverse share one statement of each format.
 
+// Raw 6-bit scale k (0..15) of a Q3_K block from its 12 packed bytes (the unpacking
+// of dequantQ3K, gguf.zig:899-906, one scale at a time).
+__device__ inline int q3k_scale(const uint8_t *s12, int k)
+{
+    const int b = k & 3, g = k >> 2;  // g: which of the four unpacked words
+    const int lo = g == 0 ? s12[b] & 0xF : g == 1 ? s12[4 + b] & 0xF : g == 2 ? s12[b] >> 4 : s12[4 + b] >> 4;
+    return lo | (((s12[8 + b] >> (2 * g)) & 3) << 4);
+}
+
 // Raw quant of element e of a GGUF block: Q8_0 / Q8_1 the int8, Q4_0 / Q4_1 / Q4_K
 // the nibble, Q5_0 / Q5_1 / Q5_K the 5-bit value (before Q5_0's -16 offset), Q6_K
 // the 6-bit value (before the -32 offset).
@@ -260,6 +269,14 @@ __device__ inline int gguf_quant(int t, const uint8_t *blk, int e)
         const uint32_t qh = blk[o] | (blk[o + 1] << 8) | (blk[o + 2] << 16) | ((uint32_t)blk[o + 3] << 24);
         const int nib = e < 16 ? blk[o + 4 + e] & 0xF : blk[o + 4 + e - 16] >> 4;
         return nib | (int)(((qh >> e) & 1) << 4);
+    }
+    case ANEDVD_Q2_K: {  // dequantQ2K (gguf.zig:855-889): half e/128, shift 2 (e%128)/32
+        const int h = e >> 7, j = (e & 127) >> 5, l = e & 31;
+        return (blk[16 + 32 * h + l] >> (2 * j)) & 3;
+    }
+    case ANEDVD_Q3_K: {  // dequantQ3K (gguf.zig:891-946): low 2 bits + hmask bit 4 h + j; value u - 4
+        const int h = e >> 7, j = (e & 127) >> 5, l = e & 31;
+        return ((blk[32 + 32 * h + l] >> (2 * j)) & 3) | (((blk[l] >> (4 * h + j)) & 1) << 2);
     }
     case ANEDVD_Q4_K: {  // dequantQ4K: group e/64, low nibbles first, then high
         const int g = e >> 6, l = e & 63;
@@ -301,6 +318,17 @@ __device__ inline void set_gguf_quant(int t, uint8_t *blk, int e, int v)
         h = (uint8_t)((h & ~(1 << (e & 7))) | (((v >> 4) & 1) << (e & 7)));
         break;
     }
+    case ANEDVD_Q2_K:
+    case ANEDVD_Q3_K: {
+        const int h = e >> 7, j = (e & 127) >> 5, l = e & 31;
+        uint8_t &q = blk[(t == ANEDVD_Q3_K ? 32 : 16) + 32 * h + l];
+        q = (uint8_t)((q & ~(3 << (2 * j))) | ((v & 3) << (2 * j)));
+        if (t == ANEDVD_Q3_K) {
+            const int sh = 4 * h + j;
+            blk[l] = (uint8_t)((blk[l] & ~(1 << sh)) | (((v >> 2) & 1) << sh));
+        }
+        break;
+    }
     case ANEDVD_Q4_K: {
         const int g = e >> 6, l = e & 63;
         uint8_t &q = blk[16 + 32 * g + (l & 31)];
@@ -332,6 +360,21 @@ __device__ inline void pack_lane(int t, const int *v, uint8_t *out)
     case ANEDVD_Q8_0:
     case ANEDVD_Q8_1:
         for (int k = 0; k < 16; k++) out[k] = (uint8_t)((v[k] + 128) & 0xFF);
+        break;
+    case ANEDVD_Q2_K:
+    case ANEDVD_Q3_K:  // bits 2 k of byte b: value 8 (k / 2) + 4 (k % 2) + b; Q3_K's third bits as the 5-bit h plane
+        for (int b = 0; b < 4; b++) {
+            int w = 0;
+            for (int k = 0; k < 4; k++) w |= (v[8 * (k >> 1) + 4 * (k & 1) + b] & 3) << (2 * k);
+            out[b] = (uint8_t)w;
+        }
+        if (t == ANEDVD_Q3_K) {
+            int h = 0;
+            for (int k = 0; k < 4; k++)
+                for (int b = 0; b < 4; b++) h |= ((v[8 * (k >> 1) + 4 * (k & 1) + b] >> 2) & 1) << (4 * k + b);
+            out[8] = (uint8_t)(h & 0xFF);
+            out[9] = (uint8_t)(h >> 8);
+        }
         break;
     case ANEDVD_Q4_0:
     case ANEDVD_Q4_1:
@@ -367,6 +410,14 @@ __device__ inline int unpack_lane(int t, const uint8_t *in, int k)
     switch (t) {
     case ANEDVD_Q8_0:
     case ANEDVD_Q8_1: return (int)in[k] - 128;
+    case ANEDVD_Q2_K:
+    case ANEDVD_Q3_K: {
+        const int j = k >> 3, i = k & 7, kk = 2 * j + (i >> 2), b = i & 3;
+        const int lo = (in[b] >> (2 * kk)) & 3;
+        if (t == ANEDVD_Q2_K) return lo;
+        const int bit = 4 * kk + b;
+        return lo | (((in[8 + (bit >> 3)] >> (bit & 7)) & 1) << 2);
+    }
     case ANEDVD_Q4_0:
     case ANEDVD_Q4_1:
     case ANEDVD_Q4_K: {
@@ -444,13 +495,26 @@ __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
             sc[4 + k] = b0[bpb + k];
         }
         break;
+    case ANEDVD_Q2_K: {  // 16 scale|min bytes; d, dmin to the d plane
+        for (int k = 0; k < 16; k++) sc[k] = b0[k];
+        uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n, 4);
+        for (int k = 0; k < 4; k++) dp[k] = b0[80 + k];
+        break;
+    }
+    case ANEDVD_Q3_K: {  // the 12 packed 6-bit scales unpacked to int8 (scale - 32); d to the d plane
+        for (int k = 0; k < 16; k++) sc[k] = (uint8_t)(q3k_scale(b0 + 96, k) - 32);
+        uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n, 2);
+        dp[0] = b0[108];
+        dp[1] = b0[109];
+        break;
+    }
     case ANEDVD_Q4_K:  // d, dmin, 12 scale bytes
     case ANEDVD_Q5_K:
         for (int k = 0; k < 16; k++) sc[k] = b0[k];
         break;
     case ANEDVD_Q6_K: {  // 16 int8 scales; d to the d plane
         for (int k = 0; k < 16; k++) sc[k] = b0[192 + k];
-        uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n);
+        uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n, 2);
         dp[0] = b0[208];
         dp[1] = b0[209];
         break;
@@ -509,9 +573,29 @@ __global__ void k_dequant_tiles(QMat m, int mat, float *__restrict__ out)
     case ANEDVD_Q5_K:
         for (int k = 0; k < 16; k++) blk[k] = sc[k];
         break;
+    case ANEDVD_Q2_K: {
+        for (int k = 0; k < 16; k++) blk[k] = sc[k];
+        const uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n, 4);
+        for (int k = 0; k < 4; k++) blk[80 + k] = dp[k];
+        break;
+    }
+    case ANEDVD_Q3_K: {
+        int raw[16];
+        for (int k = 0; k < 16; k++) raw[k] = ((int)(int8_t)sc[k] + 32) & 63;
+        for (int b = 0; b < 4; b++) {  // the packing dequantQ3K unpacks (gguf.zig:899-906)
+            blk[96 + b] = (uint8_t)((raw[b] & 0xF) | ((raw[8 + b] & 0xF) << 4));
+            blk[100 + b] = (uint8_t)((raw[4 + b] & 0xF) | ((raw[12 + b] & 0xF) << 4));
+            blk[104 + b] = (uint8_t)((raw[b] >> 4) | ((raw[4 + b] >> 4) << 2) | ((raw[8 + b] >> 4) << 4) |
+                                     ((raw[12 + b] >> 4) << 6));
+        }
+        const uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n, 2);
+        blk[108] = dp[0];
+        blk[109] = dp[1];
+        break;
+    }
     case ANEDVD_Q6_K: {
         for (int k = 0; k < 16; k++) blk[192 + k] = sc[k];
-        const uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n);
+        const uint8_t *dp = m.d + (size_t)mat * m.d_stride + tile_d_off(m.units, rb, u, t, n, 2);
         blk[208] = dp[0];
         blk[209] = dp[1];
         break;
@@ -534,7 +618,7 @@ int launch_dequant_gguf(int t, const uint8_t *d_src, size_t n_blocks, float *d_o
 
 // The formats with a tile layout, for the per-format kernel instantiations.
 #define ANEDVD_TILE_TYPES(X) X(ANEDVD_Q8_0) X(ANEDVD_Q8_1) X(ANEDVD_Q4_0) X(ANEDVD_Q4_1) X(ANEDVD_Q5_0) \
-    X(ANEDVD_Q5_1) X(ANEDVD_Q4_K) X(ANEDVD_Q5_K) X(ANEDVD_Q6_K)
+    X(ANEDVD_Q5_1) X(ANEDVD_Q2_K) X(ANEDVD_Q3_K) X(ANEDVD_Q4_K) X(ANEDVD_Q5_K) X(ANEDVD_Q6_K)
 
 int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st)
 {

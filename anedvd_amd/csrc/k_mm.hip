@@ -257,6 +257,84 @@ struct MQ5_K {
     }
 };
 
+// Q2_K (gguf.zig:855-889) and Q3_K (gguf.zig:891-946): 2-bit fields, four per
+// byte (value (j, 4 hh + b) in bits 2 (2 j + hh) of byte b), 16-element sub-blocks
+// (the lane's 8 columns of block j lie in sub-block 4 (s % 4) + 2 j + g / 2).
+// Q3_K: the third bit from the high-bit plane, the int8 sub-block scale folded
+// into the exact f16 weight (u - 4) sc and the super-block d applied to the
+// result.  Q2_K: y = dl v - ml with dl = d (sc & 15), ml = dmin (sc >> 4), formed
+// per lane in f32 and rounded to f16 with the weight (one rounding of each).
+template <bool kThree>
+struct MQ23K {
+    static constexpr bool kDeep = false;  // weights one step ahead
+    static constexpr int kSpu = 4;
+    static constexpr bool kMin = false;
+    struct Raw {
+        uint32_t q[4];
+        uint32_t h[kThree ? 4 : 1];
+        u32x4 sc[4];     // sub-block scales (first step of a unit)
+        uint32_t dm[4];  // d (Q3_K) or d | dmin << 16 (Q2_K) (first step of a unit)
+    };
+    struct State {
+        u32x4 sc[4];
+        float d[4], dmin[4];
+    };
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 4);
+#pragma unroll
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b32(p.q, 4 * lane + 256 * t, qo, kNT);
+        if constexpr (kThree) {
+            const int ho = lane_plane_off(p, rb, s, 2);
+#pragma unroll
+            for (int t = 0; t < 4; t++) r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * t, ho, kNT);
+        }
+        if ((s & 3) == 0) {
+            const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, kThree ? 2 : 4);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * t, so, kNT);
+                if constexpr (kThree)
+                    r.dm[t] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * t, dof, kNT);
+                else
+                    r.dm[t] = __builtin_amdgcn_raw_buffer_load_b32(p.d, 4 * (lane & 15) + 64 * t, dof, kNT);
+            }
+        }
+    }
+    __device__ static inline void begin(const Raw &r, State &st, int s)
+    {
+        if ((s & 3) == 0) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                st.sc[t] = r.sc[t];
+                st.d[t] = f16_bits_to_f32((uint16_t)(r.dm[t] & 0xFFFFu));
+                st.dmin[t] = f16_bits_to_f32((uint16_t)(r.dm[t] >> 16));
+            }
+        }
+    }
+    __device__ static inline void operand(const Raw &r, const State &st, int s, int lane, int t, int j, half8 &b,
+                                          float &d, float &mn)
+    {
+        const uint32_t w = r.q[t];
+        uint32_t lo = (w >> (4 * j)) & 0x03030303u, hi = (w >> (4 * j + 2)) & 0x03030303u;
+        const int sub = 4 * (s & 3) + 2 * j + (lane >> 5);
+        const uint32_t scb = (pick4(st.sc[t], sub >> 2) >> (8 * (sub & 3))) & 0xFFu;
+        mn = 0.0f;
+        if constexpr (kThree) {
+            lo |= bit2_of_bytes(r.h[t] >> (8 * j));
+            hi |= bit2_of_bytes(r.h[t] >> (8 * j + 4));
+            b = (bytes_h8(lo, hi) - (half_t)1028.0f) * (half_t)(float)(int)(int8_t)scb;  // (u - 4) sc, exact
+            d = st.d[t];
+        } else {
+            const float dl = st.d[t] * (float)(scb & 0xFu), ml = st.dmin[t] * (float)(scb >> 4);
+            b = (bytes_h8(lo, hi) - (half_t)1024.0f) * (half_t)dl - (half_t)ml;
+            d = 1.0f;
+        }
+    }
+};
+using MQ2_K = MQ23K<false>;
+using MQ3_K = MQ23K<true>;
+
 // Q6_K: the lane's 8 columns of block j lie in sub-block 4 (s % 4) + 2 j + g / 2;
 // its int8 scale is folded into the f16 weights and the super-block's d applied
 // to the result.
@@ -898,6 +976,8 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
     case ANEDVD_Q4_1: rc = launch_gateup_d<MQ4_1>(a, plan.mt, st); break;
     case ANEDVD_Q5_0: rc = launch_gateup_d<MQ5_0>(a, plan.mt, st); break;
     case ANEDVD_Q5_1: rc = launch_gateup_d<MQ5_1>(a, plan.mt, st); break;
+    case ANEDVD_Q2_K: rc = launch_gateup_d<MQ2_K>(a, plan.mt, st); break;
+    case ANEDVD_Q3_K: rc = launch_gateup_d<MQ3_K>(a, plan.mt, st); break;
     case ANEDVD_Q4_K: rc = launch_gateup_d<MQ4_K>(a, plan.mt, st); break;
     case ANEDVD_Q5_K: rc = launch_gateup_d<MQ5_K>(a, plan.mt, st); break;
     case ANEDVD_Q6_K: rc = launch_gateup_d<MQ6_K>(a, plan.mt, st); break;
@@ -933,6 +1013,8 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
     case ANEDVD_Q4_1: return launch_down_d<MQ4_1>(a, plan.mt, st);
     case ANEDVD_Q5_0: return launch_down_d<MQ5_0>(a, plan.mt, st);
     case ANEDVD_Q5_1: return launch_down_d<MQ5_1>(a, plan.mt, st);
+    case ANEDVD_Q2_K: return launch_down_d<MQ2_K>(a, plan.mt, st);
+    case ANEDVD_Q3_K: return launch_down_d<MQ3_K>(a, plan.mt, st);
     case ANEDVD_Q4_K: return launch_down_d<MQ4_K>(a, plan.mt, st);
     case ANEDVD_Q5_K: return launch_down_d<MQ5_K>(a, plan.mt, st);
     case ANEDVD_Q6_K: return launch_down_d<MQ6_K>(a, plan.mt, st);

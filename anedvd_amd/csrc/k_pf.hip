@@ -253,6 +253,82 @@ struct FQ5_K {
     }
 };
 
+// Q2_K / Q3_K: 2-bit fields four per byte, 16-element sub-blocks (the lane's
+// 8 columns of block j lie in sub-block 4 ss + 2 j + g / 2).  Q3_K: y = (d sc) (u - 4)
+// with d sc formed in f32 and kept as f16, the product rounded once; Q2_K: y = dl v - ml
+// with dl, ml formed in f32 and kept as f16, the f16 FMA rounding once.
+template <bool kThree>
+struct FQ23K {
+    static constexpr int kSpu = 4;
+    static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
+    static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
+    struct Raw {
+        uint32_t q[kPfTiles];
+        uint32_t h[kThree ? kPfTiles : 1];
+        u32x4 sc[kPfTiles];     // sub-block scales (a unit's first step)
+        uint32_t dm[kPfTiles];  // d (Q3_K) or d | dmin << 16 (Q2_K) (a unit's first step)
+    };
+    struct State {
+        half_t dl[kPfTiles][8], ml[kPfTiles][8];  // [tt][2 ss + j] of the lane's sub-block 4 ss + 2 j + g / 2
+    };
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 4);
+#pragma unroll
+        for (int tt = 0; tt < kPfTiles; tt++) {
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.q, 4 * lane + 256 * tt, qo, kNT);
+            if constexpr (kThree)
+                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * tt, lane_plane_off(p, rb, s, 2), kNT);
+        }
+        if ((s & 3) == 0) {
+            const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, kThree ? 2 : 4);
+#pragma unroll
+            for (int tt = 0; tt < kPfTiles; tt++) {
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
+                if constexpr (kThree)
+                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * tt, dof, kNT);
+                else
+                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.d, 4 * (lane & 15) + 64 * tt, dof, kNT);
+            }
+        }
+    }
+    __device__ static inline void begin(const Raw &r, State &st, int ss, int lane)
+    {
+        if (ss) return;
+        const int hg = lane >> 5;
+#pragma unroll
+        for (int tt = 0; tt < kPfTiles; tt++) {
+            const float d = f16_bits_to_f32((uint16_t)(r.dm[tt] & 0xFFFFu));
+            const float dmin = f16_bits_to_f32((uint16_t)(r.dm[tt] >> 16));
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int sub = 2 * k + hg;  // = 4 ss + 2 j + hg with k = 2 ss + j
+                const uint32_t scb = (pick4(r.sc[tt], sub >> 2) >> (8 * (sub & 3))) & 0xFFu;
+                if constexpr (kThree) {
+                    st.dl[tt][k] = (half_t)(d * (float)(int)(int8_t)scb);
+                } else {
+                    st.dl[tt][k] = (half_t)(d * (float)(scb & 0xFu));
+                    st.ml[tt][k] = (half_t)(dmin * (float)(scb >> 4));
+                }
+            }
+        }
+    }
+    __device__ static inline half8 bop(const Raw &r, const State &st, int ss, int tt, int j, int)
+    {
+        const uint32_t w = r.q[tt];
+        uint32_t lo = (w >> (4 * j)) & 0x03030303u, hi = (w >> (4 * j + 2)) & 0x03030303u;
+        if constexpr (kThree) {
+            lo |= bit2_of_bytes(r.h[tt] >> (8 * j));
+            hi |= bit2_of_bytes(r.h[tt] >> (8 * j + 4));
+            return (bytes_h8(lo, hi) - (half_t)1028.0f) * st.dl[tt][2 * ss + j];  // exact u - 4
+        } else {
+            return (bytes_h8(lo, hi) - (half_t)1024.0f) * st.dl[tt][2 * ss + j] - st.ml[tt][2 * ss + j];
+        }
+    }
+};
+using FQ2_K = FQ23K<false>;
+using FQ3_K = FQ23K<true>;
+
 // Q6_K: y = d * sc * q (gguf.zig:1036-1059) with d * sc formed in f32 once per
 // super-block and kept as f16; q - 32 is exact and the product rounds once.  The
 // lane's 8 columns of block j lie in sub-block 4 ss + 2 j + g / 2.
@@ -660,6 +736,8 @@ static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStr
     case ANEDVD_Q4_1: return launch_pf_mt<FQ4_1>(a, mt, gateup, st);
     case ANEDVD_Q5_0: return launch_pf_mt<FQ5_0>(a, mt, gateup, st);
     case ANEDVD_Q5_1: return launch_pf_mt<FQ5_1>(a, mt, gateup, st);
+    case ANEDVD_Q2_K: return launch_pf_mt<FQ2_K>(a, mt, gateup, st);
+    case ANEDVD_Q3_K: return launch_pf_mt<FQ3_K>(a, mt, gateup, st);
     case ANEDVD_Q4_K: return launch_pf_mt<FQ4_K>(a, mt, gateup, st);
     case ANEDVD_Q5_K: return launch_pf_mt<FQ5_K>(a, mt, gateup, st);
     case ANEDVD_Q6_K: return launch_pf_mt<FQ6_K>(a, mt, gateup, st);

@@ -33,6 +33,8 @@ __device__ inline half8 bytes_h8(uint32_t lo, uint32_t hi)
 // Bit b (b < 4) of x -> bit 4 of byte b: the fifth bits of four packed values
 // (one full-rate 24-bit multiply spreads them 7 bits apart per step).
 __device__ inline uint32_t bit4_of_bytes(uint32_t x) { return ((x & 0xFu) * 0x00204081u & 0x01010101u) << 4; }
+// The same to bit 2 (Q3_K's third bits).
+__device__ inline uint32_t bit2_of_bytes(uint32_t x) { return ((x & 0xFu) * 0x00204081u & 0x01010101u) << 2; }
 
 __device__ inline uint32_t pick4(u32x4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 

@@ -100,7 +100,7 @@ int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, si
 {
     const Fmt f = tile_fmt(type);
     if (!mm_supported(type)) {
-        set_error("%s: ggml type %d is not supported by the GPU layout (q8_0, q8_1, q4_0, q4_1, q5_0, q5_1, q4_k, q5_k, q6_k)", what, type);
+        set_error("%s: ggml type %d is not supported by the GPU layout (q8_0, q8_1, q4_0, q4_1, q5_0, q5_1, q2_k, q3_k, q4_k, q5_k, q6_k)", what, type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
     const int unit_cols = kStep * f.spu;
@@ -126,7 +126,7 @@ int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, si
     m.q_stride = (size_t)rows * m.steps * 4 * f.qb;
     m.s_stride = (size_t)rows * m.units * f.sb;
     m.h_stride = (size_t)rows * m.steps * 4 * tile_hb(type);
-    m.d_stride = type == ANEDVD_Q6_K ? (size_t)rows * m.units * 2 : 0;
+    m.d_stride = (size_t)rows * m.units * tile_db(type);
     // The kernels address one matrix's planes with 32-bit buffer offsets.
     if (m.q_stride > ((size_t)1 << 30)) {
         set_error("%s: one %d x %d matrix is %zu bytes; at most 1 GiB per expert matrix", what, rows, cols, m.q_stride);

@@ -151,8 +151,27 @@ def q5_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int
     return blk
 
 
-_GEN = {W.Q8_0: q8_0, W.Q8_1: q8_1, W.Q4_0: q4_0, W.Q4_1: q4_1, W.Q5_0: q5_0, W.Q5_1: q5_1, W.Q4_K: q4_k,
-        W.Q5_K: q5_k, W.Q6_K: q6_k}
+def q2_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q2_K super-blocks: random scale|min bytes[16] and 2-bit quants qs[64];
+    d, dmin = f16(|N(0,sigma)|/8)."""
+    blk = np.empty((n_blocks, 84), dtype=np.uint8)
+    blk[:, 0:80] = rand_bytes(seed, stream + 2, n_blocks * 80, offset * 80).reshape(n_blocks, 80)
+    blk[:, 80:82] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset, 8.0).view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 82:84] = _f16_abs_normal(seed, stream + 1, n_blocks, sigma, offset, 8.0).view(np.uint8).reshape(n_blocks, 2)
+    return blk
+
+
+def q3_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int = 0) -> np.ndarray:
+    """Q3_K super-blocks: random hmask[32], 2-bit quants qs[64] and 12 bytes of packed
+    6-bit scales; d = f16(|N(0,sigma)|/16)."""
+    blk = np.empty((n_blocks, 110), dtype=np.uint8)
+    blk[:, 0:108] = rand_bytes(seed, stream + 1, n_blocks * 108, offset * 108).reshape(n_blocks, 108)
+    blk[:, 108:110] = _f16_abs_normal(seed, stream, n_blocks, sigma, offset, 16.0).view(np.uint8).reshape(n_blocks, 2)
+    return blk
+
+
+_GEN = {W.Q8_0: q8_0, W.Q8_1: q8_1, W.Q4_0: q4_0, W.Q4_1: q4_1, W.Q5_0: q5_0, W.Q5_1: q5_1, W.Q2_K: q2_k,
+        W.Q3_K: q3_k, W.Q4_K: q4_k, W.Q5_K: q5_k, W.Q6_K: q6_k}
 
 
 def quant_matrix(t: int, seed: int, stream: int, n_elems: int, sigma: float, elem_offset: int = 0) -> np.ndarray:
