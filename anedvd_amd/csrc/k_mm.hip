@@ -100,7 +100,7 @@ struct MQ4_0 {
                                           float &mn)
     {
         const uint32_t v = r.q[t][j];
-        b = bytes_h8(v & 0x0F0F0F0Fu, (v >> 4) & 0x0F0F0F0Fu) - (half_t)1032.0f;  // n - 8
+        b = nibbles_h8(v) - (half_t)8.0f;  // n - 8, exact
         d = f16_bits_to_f32((uint16_t)(r.s[t] >> (16 * j)));
         mn = 0.0f;
     }
@@ -143,13 +143,14 @@ struct MQLegacy {
                                           float &mn)
     {
         const uint32_t v = r.q[t][j];
-        uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
         if constexpr (kFive) {
-            lo |= bit4_of_bytes(r.h[t] >> (8 * j));
-            hi |= bit4_of_bytes(r.h[t] >> (8 * j + 4));
+            const uint32_t lo = (v & 0x0F0F0F0Fu) | bit4_of_bytes(r.h[t] >> (8 * j));
+            const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes(r.h[t] >> (8 * j + 4));
+            // Q5_0 values are q - 16; Q5_1's the raw quant
+            b = bytes_h8(lo, hi) - (half_t)(kHasMin ? 1024.0f : 1040.0f);
+        } else {
+            b = nibbles_h8(v);
         }
-        // Q5_0 values are q - 16; the others the raw quant
-        b = bytes_h8(lo, hi) - (half_t)(kFive && !kHasMin ? 1040.0f : 1024.0f);
         if constexpr (kHasMin) {
             const uint32_t dm = r.s[t][j];
             d = f16_bits_to_f32((uint16_t)(dm & 0xFFFFu));
@@ -200,7 +201,7 @@ struct MQ4_K {
                                           float &mn)
     {
         const uint32_t v = r.q[t][j];
-        b = bytes_h8(v & 0x0F0F0F0Fu, (v >> 4) & 0x0F0F0F0Fu) - (half_t)1024.0f;  // n
+        b = nibbles_h8(v);  // n
         const u32x4 sc = st.sc[t];
         int a, m;
         scale_min_k4(2 * (s & 3) + j, sc.y, sc.z, sc.w, a, m);

@@ -45,6 +45,16 @@ __device__ inline half_t h_bits(uint32_t b)
     return h;
 }
 
+// lo and hi rounded to f16 and packed as lo | hi << 16.
+__device__ inline uint32_t pack_h2(float lo, float hi)
+{
+    const half_t a = (half_t)lo, b = (half_t)hi;
+    uint16_t ua, ub;
+    __builtin_memcpy(&ua, &a, 2);
+    __builtin_memcpy(&ub, &b, 2);
+    return (uint32_t)ua | ((uint32_t)ub << 16);
+}
+
 // ------------------------------------------------------------------ decoders
 //
 // A decoder loads one step of a wavefront's four row tiles (a 64-row block): load();
@@ -54,6 +64,7 @@ __device__ inline half_t h_bits(uint32_t b)
 
 struct FQ8_0 {
     static constexpr int kSpu = 1;
+    static constexpr bool kHoistA = false;  // at 176 VGPRs two waves per SIMD instead of three
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     struct Raw {
@@ -80,6 +91,7 @@ struct FQ8_0 {
 
 struct FQ4_0 {
     static constexpr int kSpu = 1;
+    static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     struct Raw {
@@ -100,8 +112,8 @@ struct FQ4_0 {
     __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int)
     {
         const uint32_t v = r.q[tt][j];
-        const half8 q = bytes_h8(v & 0x0F0F0F0Fu, (v >> 4) & 0x0F0F0F0Fu) - (half_t)1032.0f;  // exact n - 8
-        return q * h_bits(r.s[tt] >> (16 * j));
+        const half_t d = h_bits(r.s[tt] >> (16 * j));
+        return nibbles_h8(v) * d + d * (half_t)-8.0f;  // n d - 8 d (exact) rounded once: (n - 8) d
     }
 };
 
@@ -111,6 +123,7 @@ struct FQ4_0 {
 template <bool kFive, bool kHasMin>
 struct FQLegacy {
     static constexpr int kSpu = 1;
+    static constexpr bool kHoistA = !kFive;  // the 5-bit formats: three waves per SIMD without it
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     struct Raw {
@@ -141,12 +154,14 @@ struct FQLegacy {
     __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int)
     {
         const uint32_t v = r.q[tt][j];
-        uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+        half8 q;  // exact
         if constexpr (kFive) {
-            lo |= bit4_of_bytes(r.h[tt] >> (8 * j));
-            hi |= bit4_of_bytes(r.h[tt] >> (8 * j + 4));
+            const uint32_t lo = (v & 0x0F0F0F0Fu) | bit4_of_bytes(r.h[tt] >> (8 * j));
+            const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes(r.h[tt] >> (8 * j + 4));
+            q = bytes_h8(lo, hi) - (half_t)(kHasMin ? 1024.0f : 1040.0f);
+        } else {
+            q = nibbles_h8(v);
         }
-        const half8 q = bytes_h8(lo, hi) - (half_t)(kFive && !kHasMin ? 1040.0f : 1024.0f);  // exact
         if constexpr (kHasMin) {
             const uint32_t dm = r.s[tt][j];
             return q * h_bits(dm) + h_bits(dm >> 16);
@@ -164,6 +179,7 @@ using FQ5_1 = FQLegacy<true, true>;
 // the f16 FMA rounds once, so a weight is within 2^-10 of its scale.
 struct FQ4_K {
     static constexpr int kSpu = 4;
+    static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     struct Raw {
@@ -171,7 +187,7 @@ struct FQ4_K {
         u32x4 sc[kPfTiles];  // d, dmin, scales: loaded on a unit's first step
     };
     struct State {
-        half_t d1[kPfTiles][8], m1[kPfTiles][8];
+        uint32_t dm[kPfTiles][8];  // f16 d1 | f16 (-m1) << 16 per (tile, sub-block)
     };
     __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
@@ -196,16 +212,16 @@ struct FQ4_K {
             for (int sub = 0; sub < 8; sub++) {
                 int a, m;
                 scale_min_k4(sub, r.sc[tt].y, r.sc[tt].z, r.sc[tt].w, a, m);
-                st.d1[tt][sub] = (half_t)(d * (float)a);
-                st.m1[tt][sub] = (half_t)(dmin * (float)m);
+                st.dm[tt][sub] = pack_h2(d * (float)a, -(dmin * (float)m));
             }
         }
     }
     __device__ static inline half8 bop(const Raw &r, const State &st, int ss, int tt, int j, int)
     {
         const uint32_t v = r.q[tt][j];
-        const half8 nib = bytes_h8(v & 0x0F0F0F0Fu, (v >> 4) & 0x0F0F0F0Fu) - (half_t)1024.0f;  // exact n
-        return nib * st.d1[tt][2 * ss + j] - st.m1[tt][2 * ss + j];
+        const half8 nib = nibbles_h8(v);  // exact n
+        const uint32_t dm = st.dm[tt][2 * ss + j];
+        return nib * h_bits(dm) + h_bits(dm >> 16);
     }
 };
 
@@ -213,6 +229,7 @@ struct FQ4_K {
 // each value from the high-bit plane (2 bytes per lane per step).
 struct FQ5_K {
     static constexpr int kSpu = 4;
+    static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     struct Raw {
@@ -249,7 +266,8 @@ struct FQ5_K {
         const uint32_t lo = (v & 0x0F0F0F0Fu) | bit4_of_bytes(hb >> (8 * j));
         const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes(hb >> (8 * j + 4));
         const half8 q = bytes_h8(lo, hi) - (half_t)1024.0f;  // exact q in [0, 31]
-        return q * st.d1[tt][2 * ss + j] - st.m1[tt][2 * ss + j];
+        const uint32_t dm = st.dm[tt][2 * ss + j];
+        return q * h_bits(dm) + h_bits(dm >> 16);
     }
 };
 
@@ -260,6 +278,7 @@ struct FQ5_K {
 template <bool kThree>
 struct FQ23K {
     static constexpr int kSpu = 4;
+    static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     struct Raw {
@@ -334,6 +353,7 @@ using FQ3_K = FQ23K<true>;
 // lane's 8 columns of block j lie in sub-block 4 ss + 2 j + g / 2.
 struct FQ6_K {
     static constexpr int kSpu = 4;
+    static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     struct Raw {
@@ -518,6 +538,17 @@ __device__ inline void pf_loop(const Planes &W, int rb, int steps, int lane, S &
             const int ss = k % F::kSpu;
             F::begin(w[k % R], st, ss, lane);
             const half_t *a = abuf + (k & 1) * BUF + n * kAStride + 16 * g;
+            // The step's activation fragments, read before the dequantisation so their
+            // LDS latency hides behind it (token tiles past the chunk's end read stale
+            // rows of the buffer that no MFMA uses), or, for decoders whose registers
+            // are tight, just before their MFMAs.
+            half8 av[2][MT];
+            if constexpr (F::kHoistA) {
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) av[j][mt] = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
+            }
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 half8 b[kPfTiles];
@@ -526,9 +557,9 @@ __device__ inline void pf_loop(const Planes &W, int rb, int steps, int lane, S &
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     if (mt >= mt_live) break;  // uniform: token tiles past the chunk's end stay zero
-                    const half8 av = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
+                    if constexpr (!F::kHoistA) av[j][mt] = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
 #pragma unroll
-                    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av, b[tt], acc[tt][mt]);
+                    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av[j][mt], b[tt], acc[tt][mt]);
                 }
             }
             if (more) stage_store(stage, (k + 1) % RA, abuf + ((k + 1) & 1) * BUF + srow);

@@ -30,6 +30,23 @@ __device__ inline half8 bytes_h8(uint32_t lo, uint32_t hi)
     return h;
 }
 
+// The 8 nibbles of v as exact f16 integers 0..15, in bytes_h8's order (the low
+// nibbles of bytes 0..3, then the high nibbles).  A byte n < 16 read as OCP e4m3
+// is n * 2^-9 (the denormals and the first binade are evenly spaced 2^-9 apart),
+// and the converter scales by the exponent of its f32 operand, 2^9: one
+// v_cvt_scalef32_pk_f16_fp8 per pair of values.
+__device__ inline half8 nibbles_h8(uint32_t v)
+{
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+    const h2v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false);
+    const h2v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true);
+    const h2v c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false);
+    const h2v d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true);
+    return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // Bit b (b < 4) of x -> bit 4 of byte b: the fifth bits of four packed values
 // (one full-rate 24-bit multiply spreads them 7 bits apart per step).
 __device__ inline uint32_t bit4_of_bytes(uint32_t x) { return ((x & 0xFu) * 0x00204081u & 0x01010101u) << 4; }
