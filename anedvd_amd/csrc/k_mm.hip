@@ -559,8 +559,9 @@ struct MmArgs {
     Dispatch d;
     float *part;     // gate/up K partials [KS][P][2][I] when KS > 1
     ActQ act;        // gate/up output [P][I]
-    float *ypart;    // down output [KS][P][H]
+    float *ypart;    // down output [KS][P][H], rows in (token, slot) order
     int H, I, KS, P, use_gelu;
+    int kk;          // slots per token row of ypart
     int nchunk;      // chunk rows of the grid: blockIdx.x = chunk + nchunk * (row block, K share)
 };
 
@@ -703,7 +704,8 @@ __global__ __launch_bounds__(256) void k_act_reduce(MmArgs a)
 // owns row block 4 x + w of the output (x the workgroup's row-block group), the
 // workgroup's K units and token chunk.  The chunk's positions
 // are consecutive, so tokens past the group's end read other groups' (or, past
-// the last position, out-of-range zero) activations and are not stored.
+// the last position, out-of-range zero) activations and are not stored.  Position
+// p's result goes to row rows[p] * kk + slots[p] of the output.
 template <class D, int MT>
 __global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
 {
@@ -725,6 +727,14 @@ __global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
         A.qoff[mt] = (p0 + 16 * mt + n) * a.I * 2 + 32 * gq;
         A.doff[mt] = (p0 + 16 * mt + 4 * gq) * 4;
     }
+    int orow[MT][4];  // output rows of the lane's positions (loaded before the K loop)
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = min(16 * mt + 4 * gq + i, nt - 1);
+            orow[mt][i] = a.d.rows[p0 + m] * a.kk + a.d.slots[p0 + m];
+        }
     f32x4 acc[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
@@ -737,7 +747,7 @@ __global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
         for (int i = 0; i < 4; i++) {
             const int m = 16 * mt + 4 * gq + i;
             if (m < nt) {
-                float *yp = a.ypart + ((size_t)ks * a.P + p0 + m) * a.H + (size_t)kRowBlock * rb + n;
+                float *yp = a.ypart + ((size_t)ks * a.P + orow[mt][i]) * a.H + (size_t)kRowBlock * rb + n;
 #pragma unroll
                 for (int t = 0; t < 4; t++) yp[16 * t] = acc[mt][t][i];
             }
@@ -750,8 +760,11 @@ constexpr int kCombLanes = 8;   // slot lanes per output column group
 constexpr int kCombCols = 32;   // float4 column groups per workgroup
 constexpr int kMaxKS = 16;      // K partials the combine reads per position
 
-// out[t][h] = sum over slots s of p[t][s] * y[pos(t,s)][h] (+ scale[t] * shared),
-// a deterministic gather, no atomics (main.zig:495-509 / engine.zig:725-777).
+// out[t][h] = sum over slots s of p[t][s] * y[t k + s][h] (+ scale[t] * shared),
+// a deterministic gather, no atomics (main.zig:495-509 / engine.zig:725-777).  The
+// rows of y are in (token, slot) order, so every load's address is known up front;
+// inv[t k + s] < 0 (an expert id out of range, a row nothing wrote) only masks the
+// slot's term.
 // Thread (c, l) of a workgroup takes column group c and the slots s = l, l + 8,
 // ...: it issues the KS partial loads of a slot together (one memory round trip
 // per slot instead of one per partial), adds them in partial order and weights
@@ -770,20 +783,22 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart
     for (int t = blockIdx.y; t < T; t += gridDim.y) {  // uniform over the workgroup
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int s = l; s < k && live; s += kCombLanes) {
-            const int pos = inv[(size_t)t * k + s];
-            if (pos < 0) continue;
-            const float p = probs[(size_t)t * k + s];
+            const size_t ts = (size_t)t * k + s;
+            const int pos = inv[ts];
+            const float p = probs[ts];
             float4 z[kMaxKS];
 #pragma unroll
             for (int q = 0; q < kMaxKS; q++)
-                if (q < KS) z[q] = *(const float4 *)(ypart + ((size_t)q * P + pos) * H + h);
+                if (q < KS) z[q] = *(const float4 *)(ypart + ((size_t)q * P + ts) * H + h);
             float4 y = z[0];
 #pragma unroll
             for (int q = 1; q < kMaxKS; q++)
                 if (q < KS) {
                     y.x += z[q].x; y.y += z[q].y; y.z += z[q].z; y.w += z[q].w;
                 }
-            acc.x += p * y.x; acc.y += p * y.y; acc.z += p * y.z; acc.w += p * y.w;
+            if (pos >= 0) {
+                acc.x += p * y.x; acc.y += p * y.y; acc.z += p * y.z; acc.w += p * y.w;
+            }
         }
         part[l][c] = acc;
         if (l == 0 && shared && live) {  // the shared expert's partials [sKS][T][H], then its scale
@@ -837,10 +852,10 @@ __global__ __launch_bounds__(256) void k_combine_rows(const float *__restrict__ 
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int s = min(s0 + i, k - 1);
-            pos[i] = inv[(size_t)t * k + s];
-            p[i] = probs[(size_t)t * k + s];
-            ok[i] = s0 + i < k && pos[i] >= 0;
-            pos[i] = max(pos[i], 0);
+            pos[i] = (int)((size_t)t * k + s);
+            const int iv = inv[pos[i]];
+            p[i] = probs[pos[i]];
+            ok[i] = s0 + i < k && iv >= 0;
             y[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
         for (int q = 0; q < KS; q++) {
@@ -994,14 +1009,19 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
 }
 
 int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P,
-                       const MmPlan &plan, float *ypart, hipStream_t st)
+                       const MmPlan &plan, float *ypart, int kk, hipStream_t st)
 {
-    if (plan.mt > 1) return launch_grouped_down(down, act, H, I, d, P, plan.mt, plan.nchunk, ypart, st);
+    if (!d.rows || !d.slots || !ypart || kk <= 0) {
+        set_error("down: the dispatch's rows and slots and the output are needed (kk %d)", kk);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    if (plan.mt > 1) return launch_grouped_down(down, act, H, I, d, P, plan.mt, plan.nchunk, ypart, kk, st);
     MmArgs a{};
     a.w0 = down;
     a.x = act;
     a.d = d;
     a.ypart = ypart;
+    a.kk = kk;
     a.H = H;
     a.I = I;
     a.KS = plan.ks_dn;

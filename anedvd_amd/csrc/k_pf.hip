@@ -573,8 +573,9 @@ struct PfArgs {
     ActQ x;       // gate/up input (tokens) or down input (positions)
     Dispatch d;
     ActQ act;     // gate/up output
-    float *ypart; // down output [P][H]
+    float *ypart; // down output [P][H], rows in (token, slot) order
     int H, I, P, nchunk, use_gelu;
+    int kk;       // slots per token row of ypart
 };
 
 // The chunk `ci` of the dispatch's (16 MT)-token work list.
@@ -685,6 +686,7 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
     constexpr int R = MT / 4;
     __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
     __shared__ float ref[16 * MT];
+    __shared__ int orow[16 * MT];  // output rows of the chunk's positions, (token, slot) order
     int e, p0, nt;
     if (!pf_chunk<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;
     const int rbg = (int)(blockIdx.x / a.nchunk);
@@ -697,6 +699,7 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
         float mx = 0.0f;
         for (int gg = 0; gg < G; gg++) mx = fmaxf(mx, a.x.ds[(size_t)gg * ld + pr]);
         ref[m] = mx;
+        orow[m] = a.d.rows[pr] * a.kk + a.d.slots[pr];
     }
     __syncthreads();
     const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
@@ -724,7 +727,7 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
         for (int i = 0; i < 4; i++) {
             const int m = 16 * mt + 4 * g + i;
             if (m < nt) {
-                float *yp = a.ypart + ((size_t)p0 + m) * a.H + (size_t)kRowBlock * rb + n;
+                float *yp = a.ypart + (size_t)orow[m] * a.H + (size_t)kRowBlock * rb + n;
 #pragma unroll
                 for (int tt = 0; tt < kPfTiles; tt++) yp[16 * tt] = acc[tt][mt][i] * ref[m];
             }
@@ -800,13 +803,14 @@ int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H
 }
 
 int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
-                        int nchunk, float *ypart, hipStream_t st)
+                        int nchunk, float *ypart, int kk, hipStream_t st)
 {
     PfArgs a{};
     a.w0 = down;
     a.x = act;
     a.d = d;
     a.ypart = ypart;
+    a.kk = kk;
     a.H = H;
     a.I = I;
     a.P = P;

@@ -9,6 +9,8 @@
 //            expert, tokens ascending within an expert.
 #pragma clang fp contract(off)
 
+#include <type_traits>
+
 #include "common.h"
 #include "expf_exact.h"
 #include "kernels.h"
@@ -17,14 +19,13 @@ namespace anedvd {
 
 __constant__ uint64_t c_exp2_tab[32] = ANEDVD_EXP2_TABLE;
 
-// The exp table is read per lane with data-dependent indices: each routing
-// workgroup copies it to LDS first, so a lookup costs an LDS read rather than a
-// trip to the L2.  Call from every thread, before the first route_token.
-__device__ inline void load_exp_table(uint64_t *tab)
-{
-    if (threadIdx.x < 32) tab[threadIdx.x] = c_exp2_tab[threadIdx.x];
-    __syncthreads();
-}
+// The exp table is read per lane with data-dependent indices straight from
+// constant memory.  Each routing wavefront touches the whole table while its
+// logits load (exp_table_warm, one load per lane beside theirs), so the lookups
+// that follow hit the L1 instead of making a second trip to memory; no LDS copy
+// and no barrier.
+__device__ inline uint64_t exp_table_warm(int lane) { return c_exp2_tab[lane & 31]; }
+__device__ inline void exp_table_ready(uint64_t warm) { asm volatile("" ::"v"(warm)); }
 
 // ------------------------------------------------------------------ router
 
@@ -130,14 +131,13 @@ __device__ inline uint32_t wave_max_u32(uint32_t v)
 // chosen experts, NaNs and lanes past E carry 0.  A slot takes the largest key, then
 // the lowest expert holding it -- the reference's strict `p > best_p` scan in
 // ascending e.  A slot with nothing left gets (0, expert 0), as in the reference.
-// `row` is this wavefront's LDS row of 64 VPL floats.
+// `v` holds the row's logits as route_logits loaded them; `row` is this
+// wavefront's LDS row of 64 VPL floats; `idx2`, when given, gets a second copy of
+// the ids (the fused dispatch's LDS).
 template <int VPL>
-__device__ void route_wave(const float *__restrict__ lg, int E, int k, int norm, float *__restrict__ probs,
-                           uint32_t *__restrict__ idx, int lane, const uint64_t *tab, float *row)
+__device__ void route_wave(const float *v, int E, int k, int norm, float *__restrict__ probs,
+                           uint32_t *__restrict__ idx, int lane, const uint64_t *tab, float *row, uint32_t *idx2)
 {
-    float v[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; j++) v[j] = VPL * lane + j < E ? lg[VPL * lane + j] : -__builtin_inff();
     float mx = v[0];
 #pragma unroll
     for (int j = 1; j < VPL; j++) mx = fmaxf(mx, v[j]);
@@ -150,7 +150,7 @@ __device__ void route_wave(const float *__restrict__ lg, int E, int k, int norm,
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float t = 0.0f;
-    if (lane == 0) {
+    if (lane == 0) {  // the sum in ascending e, by one lane
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
         for (int q = 0; q < (E + 3) / 4; q++) {
             const float4 c = r4[q];
@@ -198,20 +198,43 @@ __device__ void route_wave(const float *__restrict__ lg, int E, int k, int norm,
     if (lane < k) {
         probs[lane] = my_p;
         idx[lane] = my_i;
+        if (idx2) idx2[lane] = my_i;
     }
 }
 
-// Routes token t on this wavefront (t < T); its k slots start at row t of kk.
-__device__ inline void route_token(const float *__restrict__ logits, int t, int E, int k, int kk, int norm,
-                                   float *__restrict__ probs, uint32_t *__restrict__ idx, int lane,
-                                   const uint64_t *tab, float *row)
+// Token t's logits into v (VPL = 1, 2 or 4 per lane as E needs; lanes past E get
+// -inf), issued ahead of the exp table's barrier.  The loads are unconditional
+// (addresses clamped into the row, t clamped to a valid token) so the compiler
+// counts them exactly and waits for the table alone.
+__device__ inline void route_logits(const float *__restrict__ logits, int t, int T, int E, int lane, float (&v)[4])
 {
-    const float *lg = logits + (size_t)t * E;
+    const float *lg = logits + (size_t)min(t, T - 1) * E;
+    auto load = [&](auto vpl_c) {
+        constexpr int VPL = decltype(vpl_c)::value;
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+            const int e = VPL * lane + j;
+            const float x = lg[min(e, E - 1)];
+            v[j] = e < E ? x : -__builtin_inff();
+        }
+    };
+    if (E <= 64) load(std::integral_constant<int, 1>{});
+    else if (E <= 128) load(std::integral_constant<int, 2>{});
+    else load(std::integral_constant<int, 4>{});
+}
+
+// Routes token t on this wavefront (t < T) from its logits in v; its k slots start
+// at row t of kk (of probs, idx and, when given, ids).
+__device__ inline void route_token(const float (&v)[4], int t, int E, int k, int kk, int norm,
+                                   float *__restrict__ probs, uint32_t *__restrict__ idx, int lane,
+                                   const uint64_t *tab, float *row, uint32_t *ids = nullptr)
+{
     float *pr = probs + (size_t)t * kk;
     uint32_t *ix = idx + (size_t)t * kk;
-    if (E <= 64) route_wave<1>(lg, E, k, norm, pr, ix, lane, tab, row);
-    else if (E <= 128) route_wave<2>(lg, E, k, norm, pr, ix, lane, tab, row);
-    else route_wave<4>(lg, E, k, norm, pr, ix, lane, tab, row);
+    uint32_t *i2 = ids ? ids + (size_t)t * kk : nullptr;
+    if (E <= 64) route_wave<1>(v, E, k, norm, pr, ix, lane, tab, row, i2);
+    else if (E <= 128) route_wave<2>(v, E, k, norm, pr, ix, lane, tab, row, i2);
+    else route_wave<4>(v, E, k, norm, pr, ix, lane, tab, row, i2);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -491,6 +514,29 @@ struct RouteArgs {
 constexpr int kRouteWaves = 4;      // tokens per routing workgroup, one per wavefront
 constexpr int kDispThreads = 1024;  // threads of the dispatch workgroup
 
+// Activation row w of the launch's conversion blocks, and the token's shared
+// slots: experts E .. E+n_sh-1 with its shared scale, sigmoid(shared_gate_lin . h)
+// (main.zig:512-515) or 1 (engine.zig:1170).
+__device__ inline void act_row_wave(const RouteArgs &a, size_t w, int lane)
+{
+    act_prep_wave(a.x, a.T, a.H, a.xq, w, lane);
+    if (a.n_sh && w < (size_t)a.T) {
+        float s = 1.0f;
+        if (a.sh_lin) {
+            const float *xr = a.x + w * a.H;
+            float g = 0.0f;
+            for (int i = lane; i < a.H; i += 64) g += f16_bits_to_f32(a.sh_lin[i]) * xr[i];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o, 64);
+            s = shared_sigmoid(g);
+        }
+        if (lane < a.n_sh) {
+            a.probs[w * a.kk + a.k + lane] = s;
+            a.idx[w * a.kk + a.k + lane] = (uint32_t)(a.E + lane);
+        }
+    }
+}
+
 // Blocks [0, n_route_blocks) route kRouteWaves tokens each (one wavefront per
 // token, so no SIMD holds more than one routing wavefront of a workgroup); the
 // blocks after them convert the activations, one row per wavefront.  The dispatch
@@ -499,34 +545,51 @@ constexpr int kDispThreads = 1024;  // threads of the dispatch workgroup
 // against 1.3 us for an empty launch.
 __global__ __launch_bounds__(256) void k_route(RouteArgs a)
 {
-    __shared__ uint64_t tab[32];
     __shared__ __attribute__((aligned(16))) float rows[kRouteWaves][kMaxExperts];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if ((int)blockIdx.x >= a.n_route_blocks) {
-        const size_t w = (size_t)(blockIdx.x - a.n_route_blocks) * kRouteWaves + wv;
-        act_prep_wave(a.x, a.T, a.H, a.xq, w, lane);
-        if (a.n_sh && w < (size_t)a.T) {
-            // the token's shared slots: experts E .. E+n_sh-1 with its shared scale,
-            // sigmoid(shared_gate_lin . h) (main.zig:512-515) or 1 (engine.zig:1170)
-            float s = 1.0f;
-            if (a.sh_lin) {
-                const float *xr = a.x + w * a.H;
-                float g = 0.0f;
-                for (int i = lane; i < a.H; i += 64) g += f16_bits_to_f32(a.sh_lin[i]) * xr[i];
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o, 64);
-                s = shared_sigmoid(g);
-            }
-            if (lane < a.n_sh) {
-                a.probs[w * a.kk + a.k + lane] = s;
-                a.idx[w * a.kk + a.k + lane] = (uint32_t)(a.E + lane);
-            }
-        }
+        act_row_wave(a, (size_t)(blockIdx.x - a.n_route_blocks) * kRouteWaves + wv, lane);
         return;
     }
-    load_exp_table(tab);
     const int t = (int)blockIdx.x * kRouteWaves + wv;
-    if (t < a.T) route_token(a.logits, t, a.E, a.k, a.kk, a.norm, a.probs, a.idx, lane, tab, rows[wv]);
+    if (t >= a.T) return;  // no barriers in this kernel
+    float v[4];
+    route_logits(a.logits, t, a.T, a.E, lane, v);
+    exp_table_ready(exp_table_warm(lane));
+    route_token(v, t, a.E, a.k, a.kk, a.norm, a.probs, a.idx, lane, c_exp2_tab, rows[wv]);
+}
+
+// Up to kFusedTokens tokens routed and dispatched in one launch.  Block 0's
+// wavefront w routes token w; the ids also go to LDS (the shared
+// slots' ids are fixed: E + j), and after a barrier the same workgroup dispatches
+// them from there, with no trip through memory and no second launch.  The blocks
+// after it convert the activations, one row per wavefront.
+constexpr int kFusedTokens = 16;
+constexpr int kFusedIds = kFusedTokens * (kMaxK + 64);
+static_assert(kFusedTokens <= kDispThreads / 64, "one token per wavefront of the fused workgroup");
+
+__global__ __launch_bounds__(kDispThreads) void k_route_dispatch(RouteArgs a, Dispatch d)
+{
+    constexpr int kW = kDispThreads / 64;
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (blockIdx.x > 0) {
+        act_row_wave(a, (size_t)(blockIdx.x - 1) * kW + wv, lane);
+        return;
+    }
+    __shared__ __attribute__((aligned(16))) float rows[kW][kMaxExperts];
+    __shared__ uint32_t ids[kFusedIds];
+    __shared__ DispLds s;
+    if (wv < a.T) {  // T <= kW: one token per wavefront
+        float v[4];
+        route_logits(a.logits, wv, a.T, a.E, lane, v);
+        exp_table_ready(exp_table_warm(lane));
+        route_token(v, wv, a.E, a.k, a.kk, a.norm, a.probs, a.idx, lane, c_exp2_tab, rows[wv], ids);
+    }
+    for (int i = threadIdx.x; i < a.T * a.n_sh; i += kDispThreads)
+        ids[(i / a.n_sh) * a.kk + a.k + i % a.n_sh] = (uint32_t)(a.E + i % a.n_sh);
+    __syncthreads();
+    dispatch_block<kDispThreads>(ids, a.T, a.kk, a.E + a.n_sh, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta,
+                                 d.chunks, d.chunk, d.n_routed, s);
 }
 
 __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
@@ -590,8 +653,25 @@ int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int no
                               const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
                               const SharedSlots &sh)
 {
-    ANEDVD_TRY(launch_route(d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, st, sh));
-    return launch_dispatch(d_idx, T, k + sh.n, E + sh.n, d, st);
+    if (T > kFusedTokens || T <= 0) {
+        ANEDVD_TRY(launch_route(d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, st, sh));
+        return launch_dispatch(d_idx, T, k + sh.n, E + sh.n, d, st);
+    }
+    ANEDVD_TRY(check_route_shape(T, E, k));
+    ANEDVD_TRY(check_route_shape(T, E + sh.n, k + sh.n));
+    if (d_x && H % 64) {
+        set_error("route: hidden %d is not a multiple of 64", H);
+        return ANEDVD_E_INVALID_SHAPE;
+    }
+    if (sh.n && (!d_x || sh.n > 64)) {
+        set_error("route: %d shared pieces need the activations and at most 64 pieces", sh.n);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, 1, k + sh.n, sh.n, sh.lin};
+    const unsigned blocks = 1 + (d_x ? (unsigned)((T + kDispThreads / 64 - 1) / (kDispThreads / 64)) : 0u);
+    hipLaunchKernelGGL(k_route_dispatch, dim3(blocks), dim3(kDispThreads), 0, st, a, d);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
 }
 
 int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st)

@@ -67,15 +67,17 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u);
 // go to `part` [ks][P][2][I] and a second launch finishes them.
 int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
                          const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st);
-// down for every position: ypart [ks_dn][P][H] (the combine adds the K partials).
+// down for every position: ypart [ks_dn][T * kk][H] in (token, slot) order --
+// position p's output row is rows[p] * kk + slots[p] -- so the combine reads a
+// token's slots without going through `inv` (the combine adds the K partials).
 int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P,
-                       const MmPlan &plan, float *ypart, hipStream_t st);
+                       const MmPlan &plan, float *ypart, int kk, hipStream_t st);
 // k_pf.hip -- the grouped GEMM for prefill-sized groups (chunks of 16 mt tokens)
 bool grouped_supported(int H, int I);
 int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
                           int mt, int nchunk, const ActQ &act, int use_gelu, hipStream_t st);
 int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
-                        int nchunk, float *ypart, hipStream_t st);
+                        int nchunk, float *ypart, int kk, hipStream_t st);
 
 int launch_combine(const float *ypart, const int32_t *inv, const float *probs, int T, int k, int H, int KS, int P,
                    const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st);

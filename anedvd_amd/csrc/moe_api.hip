@@ -220,6 +220,7 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
         x.splan = plan_mm(L->sgate.type, L->sdown.type, H, Is, T, 1);
         x.sd.offsets = c.take<int32_t>(2);
         x.sd.rows = c.take<int32_t>(T);
+        x.sd.slots = c.take<int32_t>(T);
         x.sd.active = c.take<int32_t>(1);
         x.sd.meta = c.take<int32_t>(4);
         x.sd.chunks = c.take<int32_t>((size_t)x.splan.nchunk);
@@ -255,6 +256,7 @@ __global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__res
     }
     if (threadIdx.x == 0) {
         d.rows[t] = t;
+        d.slots[t] = 0;
         if (t % d.chunk == 0) d.chunks[t / d.chunk] = t / d.chunk;  // expert 0, chunk j
     }
     if (!lin) return;
@@ -300,7 +302,7 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
         ANEDVD_HIP(hipGetLastError());
         ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, f.xq, H, Is, f.sd, T, f.splan, f.sh_part, f.sact,
                                         L->gelu, ss));
-        return launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_ypart, ss);
+        return launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_ypart, 1, ss);
     };
     if (fork) {
         ANEDVD_TRY(shared());
@@ -308,7 +310,7 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
     }
     ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act, L->gelu, st));
     mark(2);
-    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart, st));
+    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart, kk, st));
     mark(3);
     if (fork) ANEDVD_HIP(hipStreamWaitEvent(st, L->ctx->join, 0));
     else if (separate) ANEDVD_TRY(shared());
@@ -680,6 +682,7 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
     ANEDVD_HIP(hipMemcpyAsync(f.h_in, h, (size_t)H * 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.offsets, off.data(), (size_t)(E + 1) * 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.rows, &zero, 4, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.d.slots, &zero, 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.inv, &zero, 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.active, &act, 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.meta, meta, sizeof meta, hipMemcpyHostToDevice, st));
@@ -687,7 +690,7 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
     ANEDVD_HIP(hipMemcpyAsync(f.probs, &weight, 4, hipMemcpyHostToDevice, st));
     ANEDVD_TRY(launch_act_prep(f.h_in, 1, H, f.xq, st));
     ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, 1, f.plan, f.part, f.act, L->gelu, st));
-    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, 1, f.plan, f.ypart, st));
+    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, 1, f.plan, f.ypart, 1, st));
     ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, 1, 1, H, f.plan.ks_dn, 1, nullptr, nullptr, 0, f.out, st));
     std::vector<float> y(H);
     ANEDVD_HIP(hipMemcpyAsync(y.data(), f.out, (size_t)H * 4, hipMemcpyDeviceToHost, st));
@@ -947,7 +950,8 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
                 const anedvd_moe_layer *L = layers[(size_t)i % n_layers];
                 return s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act,
                                                      L->gelu, st)
-                              : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart, st);
+                              : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart,
+                                                   (int)(L->k + L->n_sh), st);
             };
             for (int i = 0; i < warmup && src == ANEDVD_OK; i++) src = launch(i);
             if (src == ANEDVD_OK && hipEventRecord(a, st) != hipSuccess) src = ANEDVD_E_HIP;
