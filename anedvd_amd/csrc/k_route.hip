@@ -649,11 +649,16 @@ int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &
     return ANEDVD_OK;
 }
 
+bool route_fusable(int T, int)
+{
+    return T > 0 && T <= kFusedTokens;
+}
+
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                               const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
                               const SharedSlots &sh)
 {
-    if (T > kFusedTokens || T <= 0) {
+    if (!route_fusable(T, E)) {
         ANEDVD_TRY(launch_route(d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, st, sh));
         return launch_dispatch(d_idx, T, k + sh.n, E + sh.n, d, st);
     }

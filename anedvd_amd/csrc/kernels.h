@@ -43,9 +43,11 @@ struct SharedSlots {
 int launch_route(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                  const float *d_x, int H, const ActQ &xq, hipStream_t st, const SharedSlots &sh = {});
 int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &d, hipStream_t st);
-// Route, dispatch and (d_x non-null) activation conversion of one forward call:
-// the route launch (one wavefront per token, the conversion beside it), then the
+// Route, dispatch and (d_x non-null) activation conversion of one forward call.
+// route_fusable(T, E): one launch does it all (up to 16 tokens); otherwise the route
+// launch (one wavefront per token, the conversion beside it), then the
 // one-workgroup dispatch launch.
+bool route_fusable(int T, int E);
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                               const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
                               const SharedSlots &sh = {});

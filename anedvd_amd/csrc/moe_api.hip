@@ -603,13 +603,29 @@ int anedvd_moe_route(anedvd_moe_ctx *ctx, const float *logits, size_t T, size_t 
     }
     if (!T) return ANEDVD_OK;
     ANEDVD_HIP(hipSetDevice(ctx->device));
-    ANEDVD_TRY(ensure(ctx->io, T * E * 4 + T * k * 8 + 1024, ctx->stream));
+    ANEDVD_TRY(ensure(ctx->io, T * E * 4 + T * k * 20 + E * 8 + 8192, ctx->stream));
     Carve c{(uint8_t *)ctx->io.base};
     float *dl = c.take<float>(T * E);
     float *dp = c.take<float>(T * k);
     uint32_t *di = c.take<uint32_t>(T * k);
     ANEDVD_HIP(hipMemcpyAsync(dl, logits, T * E * 4, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, norm, dp, di, nullptr, 0, ActQ{}, ctx->stream));
+    if (route_fusable((int)T, (int)E)) {
+        // the layer forward's small-call kernel (routing and dispatch in one launch),
+        // so this entry point checks the routing it does; the dispatch is discarded
+        Dispatch d{};
+        d.offsets = c.take<int32_t>(E + 1);
+        d.rows = c.take<int32_t>(T * k);
+        d.slots = c.take<int32_t>(T * k);
+        d.inv = c.take<int32_t>(T * k);
+        d.active = c.take<int32_t>(E);
+        d.meta = c.take<int32_t>(4);
+        d.chunk = 16;
+        d.n_routed = (int)E;
+        ANEDVD_TRY(launch_route_and_dispatch(dl, (int)T, (int)E, (int)k, norm, dp, di, nullptr, 0, ActQ{}, d,
+                                             ctx->stream, SharedSlots{}));
+    } else {
+        ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, norm, dp, di, nullptr, 0, ActQ{}, ctx->stream));
+    }
     ANEDVD_HIP(hipMemcpyAsync(probs, dp, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(idx, di, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipStreamSynchronize(ctx->stream));

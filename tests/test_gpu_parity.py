@@ -107,8 +107,13 @@ def test_moe_route_reference_kat(ctx):
 
 
 @pytest.mark.parametrize("E,k,norm,T", [(8, 2, True, 64), (128, 8, True, 512), (64, 6, False, 256),
-                                        (60, 4, False, 100), (256, 8, True, 64), (128, 1, False, 64)])
+                                        (60, 4, False, 100), (256, 8, True, 64), (128, 1, False, 64),
+                                        (128, 8, False, 16), (128, 8, True, 17), (64, 6, False, 48),
+                                        (16, 4, True, 33), (100, 24, True, 40)])
 def test_moe_route_bit_exact(ctx, E, k, norm, T):
+    """Up to 16 tokens route in the layer's small-call kernel (routing and dispatch
+    in one launch), beyond that in the route launch: both against cpu.moeRoute bit
+    for bit."""
     lg = (synth.normal(7, E, T * E) * 2.0).astype(np.float32).reshape(T, E)
     lg[::3] = np.round(lg[::3] * 4) / 4   # coarse logits: many exact ties
     lg[1::7] = synth.uniform(8, E, lg[1::7].size).astype(np.float32).reshape(-1, E)
@@ -119,8 +124,9 @@ def test_moe_route_bit_exact(ctx, E, k, norm, T):
         assert np.array_equal(bits(p[t]), bits(op)), t
 
 
+@pytest.mark.parametrize("reps", [1, 4])
 @pytest.mark.parametrize("E", [60, 128, 256])
-def test_moe_route_special_values(ctx, E):
+def test_moe_route_special_values(ctx, E, reps):
     """NaN, +-inf, underflowing exps and all-tied rows route as cpu.moeRoute does
     (cpu.zig:1244-1288: @max skips NaN, NaN probabilities are never chosen, an
     empty slot gets (0, expert 0))."""
@@ -134,7 +140,8 @@ def test_moe_route_special_values(ctx, E):
     r = np.zeros(E, np.float32); r[::2] = -200.0; rows.append(r)          # half the exps underflow
     rows.append(np.zeros(E, np.float32))                                  # all tied
     r = base.copy(); r[-1] = 7.0; r[0] = 7.0; rows.append(r)              # tie between first and last
-    lg = np.stack(rows)
+    lg = np.concatenate([np.stack(rows)] * reps)  # 9 or 36 tokens: the small-call kernel or the route launch
+    rows = rows * reps
     for k, norm in [(8, True), (8, False), (1, False), (32, True)]:
         p, idx = ctx.moe_route(lg, k, norm)
         for t in range(len(rows)):
