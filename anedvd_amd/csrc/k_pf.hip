@@ -45,15 +45,20 @@ __device__ inline half_t h_bits(uint32_t b)
     return h;
 }
 
-// lo and hi rounded to f16 and packed as lo | hi << 16.
-__device__ inline uint32_t pack_h2(float lo, float hi)
+__device__ inline h2 as_h2(uint32_t b)
 {
-    const half_t a = (half_t)lo, b = (half_t)hi;
-    uint16_t ua, ub;
-    __builtin_memcpy(&ua, &a, 2);
-    __builtin_memcpy(&ub, &b, 2);
-    return (uint32_t)ua | ((uint32_t)ub << 16);
+    h2 h;
+    __builtin_memcpy(&h, &b, 4);
+    return h;
 }
+
+__device__ inline uint32_t h2_bits(h2 h)
+{
+    uint32_t b;
+    __builtin_memcpy(&b, &h, 4);
+    return b;
+}
+
 
 // ------------------------------------------------------------------ decoders
 //
@@ -201,18 +206,33 @@ struct FQ4_K {
                 r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
         }
     }
+    // The 6-bit scales and mins of getScaleMinK4 (gguf.zig:948-958) for all eight
+    // sub-blocks at once, a byte each: a_lo / m_lo for sub-blocks 0..3 (bytes 0..3
+    // and 4..7 of the packed 12), a_hi / m_hi for 4..7 (the low or high nibble of
+    // bytes 8..11 with the top two bits of bytes 0..3 or 4..7).  Each (a, m) pair
+    // becomes the exact f16 pair (a, m) by the 0x64 exponent trick, and one packed
+    // f16 multiply by (d, -dmin) gives (d a, -dmin m): the exact product rounded once,
+    // as rounding the f32 product d * a to f16 does.
     __device__ static inline void begin(const Raw &r, State &st, int ss, int)
     {
         if (ss) return;
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            const float d = f16_bits_to_f32((uint16_t)(r.sc[tt].x & 0xFFFFu));
-            const float dmin = f16_bits_to_f32((uint16_t)(r.sc[tt].x >> 16));
+            const uint32_t y = r.sc[tt].y, z = r.sc[tt].z, w = r.sc[tt].w;
+            const uint32_t a_lo = y & 0x3F3F3F3Fu, m_lo = z & 0x3F3F3F3Fu;
+            const uint32_t a_hi = (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
+            const uint32_t m_hi = ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
+            // (a_j, m_j, a_j+1, m_j+1) byte pairs
+            const uint32_t am[4] = {__builtin_amdgcn_perm(m_lo, a_lo, 0x05010400u),
+                                    __builtin_amdgcn_perm(m_lo, a_lo, 0x07030602u),
+                                    __builtin_amdgcn_perm(m_hi, a_hi, 0x05010400u),
+                                    __builtin_amdgcn_perm(m_hi, a_hi, 0x07030602u)};
+            const h2 dd = as_h2(r.sc[tt].x ^ 0x80000000u);  // (d, -dmin)
 #pragma unroll
             for (int sub = 0; sub < 8; sub++) {
-                int a, m;
-                scale_min_k4(sub, r.sc[tt].y, r.sc[tt].z, r.sc[tt].w, a, m);
-                st.dm[tt][sub] = pack_h2(d * (float)a, -(dmin * (float)m));
+                const uint32_t biased = (sub & 1) ? pair23(am[sub >> 1]) : pair01(am[sub >> 1]);  // 1024 + a, 1024 + m
+                const h2 dm = dd * (as_h2(biased) - (h2)1024.0f);
+                st.dm[tt][sub] = h2_bits(dm);
             }
         }
     }
@@ -363,7 +383,7 @@ struct FQ6_K {
         uint16_t d[kPfTiles];  // f16 d (a unit's first step)
     };
     struct State {
-        half_t dsc[kPfTiles][8];  // [tt][2 ss + j]: d * sc of the lane's sub-block 4 ss + 2 j + g / 2
+        uint32_t dsc[kPfTiles][4];  // f16 pairs; [tt][k / 2] half k % 2 (k = 2 ss + j): d * sc of the lane's sub-block 2 k + g / 2
     };
     __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
     {
@@ -382,18 +402,21 @@ struct FQ6_K {
             }
         }
     }
+    // d * sc for two sub-blocks at once: the int8 scales become exact f16 by the
+    // 0x64 exponent trick (bias 1024 + 128), and one packed f16 multiply by (d, d)
+    // gives the exact products rounded once, as rounding the f32 product does.
     __device__ static inline void begin(const Raw &r, State &st, int ss, int lane)
     {
         if (ss) return;
-        const int hg = lane >> 5;
+        const uint32_t sel = (lane >> 5) ? 0x04030401u : 0x04020400u;  // bytes g/2 and 2 + g/2 of a dword
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            const float d = f16_bits_to_f32(r.d[tt]);
+            const h2 dd = as_h2((uint32_t)r.d[tt] * 0x10001u);
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int sub = 2 * k + hg;  // = 4 ss + 2 j + hg with k = 2 ss + j
-                const int sc = (int)(int8_t)((pick4(r.sc[tt], sub >> 2) >> (8 * (sub & 3))) & 0xFFu);
-                st.dsc[tt][k] = (half_t)(d * (float)sc);
+            for (int q = 0; q < 4; q++) {
+                const uint32_t u = pick4(r.sc[tt], q) ^ 0x80808080u;  // sc + 128
+                const h2 v = as_h2(__builtin_amdgcn_perm(0x64646464u, u, sel)) - (h2)1152.0f;
+                st.dsc[tt][q] = h2_bits(dd * v);
             }
         }
     }
@@ -403,7 +426,7 @@ struct FQ6_K {
         const uint32_t lo = (v & 0x0F0F0F0Fu) | (((hb >> (4 * j)) & 0x03030303u) << 4);
         const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) | (((hb >> (4 * j + 2)) & 0x03030303u) << 4);
         const half8 q = bytes_h8(lo, hi) - (half_t)1056.0f;  // exact q - 32
-        return q * st.dsc[tt][2 * ss + j];
+        return q * h_bits(st.dsc[tt][ss] >> (16 * j));
     }
 };
 
