@@ -135,7 +135,7 @@ __device__ inline uint32_t wave_max_u32(uint32_t v)
 // wavefront's LDS row of 64 VPL floats; `idx2`, when given, gets a second copy of
 // the ids (the fused dispatch's LDS).
 template <int VPL>
-__device__ void route_wave(const float *v, int E, int k, int norm, float *__restrict__ probs,
+__device__ __forceinline__ void route_wave(const float *v, int E, int k, int norm, float *__restrict__ probs,
                            uint32_t *__restrict__ idx, int lane, const uint64_t *tab, float *row, uint32_t *idx2)
 {
     float mx = v[0];
@@ -246,10 +246,12 @@ __device__ inline void route_token(const float (&v)[4], int t, int E, int k, int
 //   2. entries are ranked within their expert through a bitmap: each entry sets
 //      bit (entry - chunk start) of its expert's row; the count of earlier
 //      entries of the same expert before a word, plus the popcount of the lower
-//      bits of the entry's own word, is its rank.  When E rows of ceil(P/32)
-//      words fit in LDS, one pass does it all (row prefixes per expert, three
-//      barriers); otherwise the entries go in chunks of C, and a block-wide scan
-//      of the popcounts of the flattened bitmap gives the counts.
+//      bits of the entry's own word, is its rank.  When there are no more
+//      entries than threads and E rows of ceil(P/32) words fit in LDS, one pass
+//      does it all (row prefixes per expert, three barriers).  Larger calls up to
+//      16384 entries rank by segments instead (dispatch_segments: no atomics, the
+//      ids loaded once); beyond that the entries go in chunks of C, and a
+//      block-wide scan of the popcounts of the flattened bitmap gives the counts.
 // Outputs: offsets[E+1]; rows/slots[T*k] grouped by expert, tokens ascending;
 // inv[t*k+s] = position of (t, s) or -1 for an expert id >= E; active[0..n) =
 // experts with tokens, ascending; meta[0] = n, meta[1] = largest group,
@@ -262,8 +264,13 @@ struct DispLds {
     int32_t cnt[kMaxExperts];
     int32_t off[kMaxExperts];
     int32_t base[kMaxExperts];
-    uint32_t bits[kDispWords];
-    int32_t pre[kDispWords + 1];
+    union {
+        struct {
+            uint32_t bits[kDispWords];
+            int32_t pre[kDispWords + 1];
+        };
+        int32_t perm[2 * kDispWords + 1];  // dispatch_segments: the entry at each position
+    };
     int32_t wsum[16];
     int32_t bad;
 };
@@ -290,7 +297,7 @@ __device__ inline int wave_incl_scan(int v, int)
 // Wavefront 0 of the dispatch: offsets[E+1], the active experts, the chunk list
 // and meta from the per-expert counts in s.cnt (4 experts per lane, E <= 256);
 // s.off gets the offsets.
-__device__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets, int32_t *__restrict__ active,
+__device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets, int32_t *__restrict__ active,
                                  int32_t *__restrict__ meta, int32_t *__restrict__ chunks, int chunk, int n_routed,
                                  DispLds &s)
 {
@@ -334,8 +341,118 @@ __device__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets,
     }
 }
 
+// Calls of more entries than threads (or too many for the one-pass bitmap), up to
+// (NTH / 64) * 64 * kSegBatches entries: wavefront w takes the w-th contiguous segment of entries, 64 at a time.
+// The lanes holding the same expert id are found with nine ballots (one per bit
+// of the id; padding and ids >= E share an id no expert has), so each entry's rank
+// among its segment's earlier entries of the same expert is the running count of
+// that expert in the wavefront's LDS row plus the lanes below it in its batch; the
+// group's lowest lane then advances the count.  A scan over the wavefronts' rows
+// gives each segment's base per expert: position = offset[e] + base[w][e] + rank,
+// the same stable order (entries ascending within an expert) with two barriers
+// after the counting.
+constexpr int kSegBatches = 16;
+
 template <int NTH>
-__device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
+__device__ __forceinline__ void dispatch_segments(const uint32_t *__restrict__ idx, int P, int k, int E,
+                                  int32_t *__restrict__ offsets, int32_t *__restrict__ rows,
+                                  int32_t *__restrict__ slots, int32_t *__restrict__ inv, int32_t *__restrict__ active,
+                                  int32_t *__restrict__ meta, int32_t *__restrict__ chunks, int chunk, int n_routed,
+                                  DispLds &s)
+{
+    constexpr int NW = NTH / 64;
+    static_assert(NW * kMaxExperts <= kDispWords, "per-wavefront counts live in the bitmap's words");
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nb = (P + NW * 64 - 1) / (NW * 64);  // batches per wavefront, <= kSegBatches
+    const int seg0 = wv * nb * 64;
+    int32_t *wcnt = reinterpret_cast<int32_t *>(s.bits) + wv * kMaxExperts;  // this wavefront's row
+    for (int e = lane; e < E; e += 64) wcnt[e] = 0;
+    if (tid == 0) s.bad = 0;
+    __syncthreads();
+    uint32_t key[kSegBatches];  // the id (9 bits), then the rank << 16 as well
+    int bad = 0;
+    const uint64_t below_mask = (1ull << lane) - 1ull;
+    // every batch's ids first: one memory round trip, not one per batch
+#pragma unroll
+    for (int b = 0; b < kSegBatches; b++) {
+        const int i = seg0 + 64 * b + lane;
+        key[b] = b < nb && i < P ? idx[i] : 0x1FFu;
+    }
+#pragma unroll
+    for (int b = 0; b < kSegBatches; b++) {
+        if (b >= nb) continue;  // uniform; the loop stays fully unrolled, key and rank in registers
+        const int i = seg0 + 64 * b + lane;
+        uint32_t e = key[b];
+        if (e >= (uint32_t)E) {
+            bad += i < P;
+            e = 0x1FFu;
+        }
+        uint64_t same = ~0ull;
+#pragma unroll
+        for (int bit = 0; bit < 9; bit++) {
+            const bool on = (e >> bit) & 1u;
+            const uint64_t bb = __ballot(on);
+            same &= on ? bb : ~bb;
+        }
+        const int below = __popcll(same & below_mask);
+        const int base = e < (uint32_t)E ? wcnt[e] : 0;
+        key[b] = e | (uint32_t)(base + below) << 16;
+        if (e < (uint32_t)E && below == 0) wcnt[e] = base + __popcll(same);
+    }
+    if (bad) atomicAdd(&s.bad, bad);
+    __syncthreads();
+    // per expert: the wavefronts' exclusive prefix in place, the total to cnt
+    for (int e = tid; e < E; e += NTH) {
+        int run = 0;
+        for (int w = 0; w < NW; w++) {
+            int32_t *c = reinterpret_cast<int32_t *>(s.bits) + w * kMaxExperts + e;
+            const int v = *c;
+            *c = run;
+            run += v;
+        }
+        s.cnt[e] = run;
+    }
+    __syncthreads();
+    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, s);
+    __syncthreads();
+    // Each entry's position (inv, written in entry order); the entries go to LDS by
+    // position, so rows and slots are written in position order (coalesced) rather
+    // than scattered, when P positions fit in the bitmap's words.
+    int pos[kSegBatches];
+#pragma unroll
+    for (int b = 0; b < kSegBatches; b++) {
+        const int i = seg0 + 64 * b + lane;
+        pos[b] = -1;
+        if (b >= nb || i >= P) continue;
+        const uint32_t e = key[b] & 0xFFFFu;
+        if (e < (uint32_t)E) pos[b] = s.off[e] + wcnt[e] + (int)(key[b] >> 16);
+        inv[i] = pos[b];
+    }
+    const bool staged = P <= 2 * kDispWords + 1;
+    if (staged) __syncthreads();  // uniform: every wavefront is done with the counts
+#pragma unroll
+    for (int b = 0; b < kSegBatches; b++) {
+        const int i = seg0 + 64 * b + lane;
+        if (b >= nb || pos[b] < 0) continue;
+        if (staged) {
+            s.perm[pos[b]] = i;
+        } else {
+            rows[pos[b]] = i / k;
+            slots[pos[b]] = i % k;
+        }
+    }
+    if (!staged) return;
+    __syncthreads();
+    const int n = P - s.bad;  // positions filled
+    for (int p = tid; p < n; p += NTH) {
+        const int i = s.perm[p];
+        rows[p] = i / k;
+        slots[p] = i % k;
+    }
+}
+
+template <int NTH>
+__device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
                                int32_t *__restrict__ rows, int32_t *__restrict__ slots, int32_t *__restrict__ inv,
                                int32_t *__restrict__ active, int32_t *__restrict__ meta, int32_t *__restrict__ chunks,
                                int chunk, int n_routed, DispLds &s)
@@ -343,7 +460,7 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
     static_assert(NTH >= 128, "wavefront 0 computes the offsets while the others prefix the bitmap");
     const int P = T * k, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int W1 = (P + 31) / 32;  // bitmap words per expert if every entry fits at once
-    if (E * W1 <= kDispWords) {
+    if (P <= NTH && E * W1 <= kDispWords) {
         // One pass: the counts and the bitmap in the same sweep; then wavefront 0
         // takes the offsets while the others prefix each expert's row of the bitmap
         // (pre[e W + w] = entries of e before word w); an entry's rank is its row
@@ -388,6 +505,10 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
             slots[pos] = i % k;
             inv[i] = pos;
         }
+        return;
+    }
+    if (P <= (NTH / 64) * 64 * kSegBatches) {
+        dispatch_segments<NTH>(idx, P, k, E, offsets, rows, slots, inv, active, meta, chunks, chunk, n_routed, s);
         return;
     }
     for (int e = tid; e < E; e += NTH) {
@@ -463,7 +584,7 @@ __device__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, i
 // per row: wavefront w takes row w, finds its largest magnitude, then converts
 // it; every group's descale ds[g * ld + row] holds the row's, so the grouped GEMM
 // can accumulate a whole row's K in the MFMA.
-__device__ void act_prep_wave(const float *__restrict__ x, int rows, int K, const ActQ &xq, size_t w, int lane)
+__device__ __forceinline__ void act_prep_wave(const float *__restrict__ x, int rows, int K, const ActQ &xq, size_t w, int lane)
 {
     if (w >= (size_t)rows) return;
     const float *xr = x + w * K;

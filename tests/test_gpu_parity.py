@@ -150,8 +150,12 @@ def test_moe_route_special_values(ctx, E, reps):
             assert np.array_equal(bits(p[t]), bits(op)), (t, k, norm)
 
 
-@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (16, 8, 2), (64, 128, 8), (512, 128, 8), (2048, 8, 2), (1024, 64, 6)])
+@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (16, 8, 2), (64, 128, 8), (512, 128, 8), (2048, 8, 2), (1024, 64, 6),
+                                   (1000, 256, 16), (4096, 128, 8)])
 def test_dispatch_bit_exact(ctx, T, E, k):
+    """Stable counting sort, against the oracle: the one-pass bitmap (decode sizes),
+    the per-wavefront segments (up to 16384 entries; 512x8 of 128, 1024x6 of 64,
+    1000x16 of 256) and the chunked bitmap beyond (4096x8 of 128)."""
     lg = synth.normal(11, T, T * E).astype(np.float32).reshape(T, E)
     idx = np.stack([O.moe_route(lg[t], k, True)[1] for t in range(T)])
     got = ctx.dispatch(idx, T, k, E)
@@ -160,9 +164,12 @@ def test_dispatch_bit_exact(ctx, T, E, k):
         assert np.array_equal(g, w)
 
 
-def test_dispatch_rejects_bad_expert_ids(ctx):
+@pytest.mark.parametrize("T,k,E", [(1, 2, 8), (512, 8, 128), (4096, 8, 128)])
+def test_dispatch_rejects_bad_expert_ids(ctx, T, k, E):
+    idx = (np.arange(T * k, dtype=np.uint32) % E).reshape(T, k)
+    idx[T // 2, k - 1] = E + 1
     with pytest.raises(moe.MoeError):
-        ctx.dispatch(np.array([[0, 9]], dtype=np.uint32), 1, 2, 8)
+        ctx.dispatch(idx, T, k, E)
 
 
 @pytest.mark.parametrize("spec,T", [(W.TINY_Q8_0, 16), (W.QWEN3_30B_A3B_Q8_0, 64)])
