@@ -634,6 +634,7 @@ template <class F, int MT>
 __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
 {
     constexpr int R = MT / 4;
+    __shared__ float dvs[16 * MT];
     __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kBytes];
     int e, p0, nt;
     if (!pf_chunk<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;  // uniform over the workgroup
@@ -652,17 +653,21 @@ __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
     for (int tt = 0; tt < kPfTiles; tt++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    // token m's descale for the epilogue, loaded by thread m before the K loop
+    const float tdv = (int)threadIdx.x < 16 * MT ? a.x.ds[a.d.rows[p0 + min((int)threadIdx.x, nt - 1)]] : 0.0f;
     pf_loop<F, MT>(W, rb, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q,
                    __builtin_amdgcn_readfirstlane((nt + 15) / 16), acc);
 
-    // results * the tokens' descales -> LDS [mat][token][row]: one row block and 64
-    // tokens per pass
-    float *res = (float *)smem;
+    if ((int)threadIdx.x < 16 * MT) dvs[threadIdx.x] = tdv;
+    __syncthreads();
     float dv[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) dv[mt][i] = a.x.ds[a.d.rows[p0 + min(16 * mt + 4 * g + i, nt - 1)]];
+        for (int i = 0; i < 4; i++) dv[mt][i] = dvs[16 * mt + 4 * g + i];
+    // results * the tokens' descales -> LDS [mat][token][row]: one row block and 64
+    // tokens per pass
+    float *res = (float *)smem;
 #pragma unroll
     for (int hb = 0; hb < 2; hb++) {
 #pragma unroll
@@ -710,6 +715,7 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
     __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
     __shared__ float ref[16 * MT];
     __shared__ int orow[16 * MT];  // output rows of the chunk's positions, (token, slot) order
+    __shared__ float ref4[4][16 * MT];
     int e, p0, nt;
     if (!pf_chunk<MT>(a.d, (int)(blockIdx.x % a.nchunk), e, p0, nt)) return;
     const int rbg = (int)(blockIdx.x / a.nchunk);
@@ -717,14 +723,26 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
     const int rb = 4 * rbg + wv;
     const Planes W = planes(a.w0, e);
     const int G = a.I / kStep, ld = a.x.ld;
-    for (int m = threadIdx.x; m < 16 * MT; m += 256) {  // the row references
+    {
+        // the row references: thread (part, m) takes every 4th group of position m,
+        // eight loads in flight at a time, and the four partial maxima meet in LDS
+        static_assert(16 * MT * 4 == 256, "four threads per chunk position");
+        const int m = threadIdx.x % (16 * MT), part = threadIdx.x / (16 * MT);
         const int pr = min(p0 + m, a.P - 1);
+        if (part == 0) orow[m] = a.d.rows[pr] * a.kk + a.d.slots[pr];
         float mx = 0.0f;
-        for (int gg = 0; gg < G; gg++) mx = fmaxf(mx, a.x.ds[(size_t)gg * ld + pr]);
-        ref[m] = mx;
-        orow[m] = a.d.rows[pr] * a.kk + a.d.slots[pr];
+        for (int g0 = part; g0 < G; g0 += 4 * 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = g0 + 4 * i < G ? a.x.ds[(size_t)(g0 + 4 * i) * ld + pr] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) mx = fmaxf(mx, v[i]);
+        }
+        ref4[part][m] = mx;
+        __syncthreads();
+        if (part == 0) ref[m] = fmaxf(fmaxf(ref4[0][m], ref4[1][m]), fmaxf(ref4[2][m], ref4[3][m]));
+        __syncthreads();
     }
-    __syncthreads();
     const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
     StageAct<R, F::kStageDepth == 1 ? 2 : 4> stage;
     stage.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
