@@ -605,11 +605,12 @@ struct PfArgs {
 template <int MT>
 __device__ inline bool pf_chunk(const Dispatch &d, int ci, int &e, int &p0, int &nt)
 {
-    if (ci >= d.meta[3]) return false;
-    const int c = d.chunks[ci];
-    e = c >> 16;
-    p0 = d.offsets[e] + (c & 0xFFFF) * 16 * MT;
-    nt = min(16 * MT, d.offsets[e + 1] - p0);
+    const int n = d.meta[3];
+    const uint64_t c = d.chunks[ci];  // ci < the list's capacity: loaded beside the count
+    if (ci >= n) return false;
+    e = (int)(c & 0xFFu);
+    nt = (int)((c >> 8) & 0xFFu);
+    p0 = (int)(c >> 16);
     return true;
 }
 

@@ -256,8 +256,9 @@ __device__ inline void route_token(const float (&v)[4], int t, int E, int k, int
 // inv[t*k+s] = position of (t, s) or -1 for an expert id >= E; active[0..n) =
 // experts with tokens, ascending; meta[0] = n, meta[1] = largest group,
 // meta[2] = entries with expert id >= E (never written out of bounds); and, when
-// `chunks` is given, the grouped GEMM's work list: chunks[c] = (e << 16) | j for
-// the j-th `chunk`-token slice of expert e, experts ascending, meta[3] = their count.
+// `chunks` is given, the expert kernels' work list: chunks[c] = chunk_entry(e, p0,
+// nt) for each `chunk`-token slice of expert e's group (first position p0, nt
+// tokens), experts ascending, meta[3] = their count.
 constexpr int kDispWords = 4096;
 
 struct DispLds {
@@ -298,7 +299,7 @@ __device__ inline int wave_incl_scan(int v, int)
 // and meta from the per-expert counts in s.cnt (4 experts per lane, E <= 256);
 // s.off gets the offsets.
 __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets, int32_t *__restrict__ active,
-                                 int32_t *__restrict__ meta, int32_t *__restrict__ chunks, int chunk, int n_routed,
+                                 int32_t *__restrict__ meta, uint64_t *__restrict__ chunks, int chunk, int n_routed,
                                  DispLds &s)
 {
     int c[4], tot = 0, nz = 0, mx = 0;
@@ -323,9 +324,9 @@ __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__res
             s.off[e] = run;
             offsets[e] = run;
             if (c[q]) active[runa++] = e;
-            run += c[q];
             if (chunks)
-                for (int j = 0; j * chunk < c[q]; j++) chunks[runc++] = (e << 16) | j;
+                for (int j = 0; j * chunk < c[q]; j++) chunks[runc++] = chunk_entry(e, run + j * chunk, min(chunk, c[q] - j * chunk));
+            run += c[q];
         }
     }
 #pragma unroll
@@ -357,7 +358,7 @@ template <int NTH>
 __device__ __forceinline__ void dispatch_segments(const uint32_t *__restrict__ idx, int P, int k, int E,
                                   int32_t *__restrict__ offsets, int32_t *__restrict__ rows,
                                   int32_t *__restrict__ slots, int32_t *__restrict__ inv, int32_t *__restrict__ active,
-                                  int32_t *__restrict__ meta, int32_t *__restrict__ chunks, int chunk, int n_routed,
+                                  int32_t *__restrict__ meta, uint64_t *__restrict__ chunks, int chunk, int n_routed,
                                   DispLds &s)
 {
     constexpr int NW = NTH / 64;
@@ -454,7 +455,7 @@ __device__ __forceinline__ void dispatch_segments(const uint32_t *__restrict__ i
 template <int NTH>
 __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
                                int32_t *__restrict__ rows, int32_t *__restrict__ slots, int32_t *__restrict__ inv,
-                               int32_t *__restrict__ active, int32_t *__restrict__ meta, int32_t *__restrict__ chunks,
+                               int32_t *__restrict__ active, int32_t *__restrict__ meta, uint64_t *__restrict__ chunks,
                                int chunk, int n_routed, DispLds &s)
 {
     static_assert(NTH >= 128, "wavefront 0 computes the offsets while the others prefix the bitmap");

@@ -17,13 +17,22 @@ struct ActQ {
 // offsets[E+1]; rows/slots[T*k] grouped by expert, tokens ascending; inv[T*k] =
 // position of (t, s); active[] = experts with tokens, ascending; meta[0] = number
 // of active experts, meta[1] = largest group, meta[2] = ids >= E, meta[3] = number
-// of chunks; chunks[] (optional) = (e << 16) | j for each `chunk`-token slice j of
-// expert e's group, experts ascending -- the expert kernels' work list.
+// of chunks; chunks[] (optional) = chunk_entry(e, p0, nt) for each `chunk`-token
+// slice of expert e's group, experts ascending -- the expert kernels' work list.
 struct Dispatch {
-    int32_t *offsets, *rows, *slots, *inv, *active, *meta, *chunks;
+    int32_t *offsets, *rows, *slots, *inv, *active, *meta;
+    uint64_t *chunks;  // the work list: chunk_entry(e, first position, tokens) per chunk
     int chunk;
     int n_routed;  // meta[1] counts experts below this one only (0 = all): merged shared pieces are not groups
 };
+
+// A work-list entry: expert e (< 256), the chunk's first position p0 and its
+// tokens nt (<= 255), one 8-byte load for the kernels that take it.
+__host__ __device__ inline uint64_t chunk_entry(int e, int p0, int nt)
+{
+    return (uint64_t)(uint32_t)e | (uint64_t)(uint32_t)nt << 8 | (uint64_t)(uint32_t)p0 << 16;
+}
+
 
 // k_dequant.hip
 int launch_dequant_gguf(int type, const uint8_t *d_src, size_t n_blocks, float *d_out, hipStream_t st);

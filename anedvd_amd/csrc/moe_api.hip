@@ -208,7 +208,7 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     x.d.inv = c.take<int32_t>(P);
     x.d.active = c.take<int32_t>(E);
     x.d.meta = c.take<int32_t>(4);
-    x.d.chunks = c.take<int32_t>((size_t)x.plan.nchunk);
+    x.d.chunks = c.take<uint64_t>((size_t)x.plan.nchunk);
     x.d.chunk = x.plan.chunk;
     x.d.n_routed = L->E;
     x.xq = ActQ{c.take<half_t>((size_t)T * H), c.take<float>((size_t)T * (H / kStep)), T};
@@ -223,7 +223,7 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
         x.sd.slots = c.take<int32_t>(T);
         x.sd.active = c.take<int32_t>(1);
         x.sd.meta = c.take<int32_t>(4);
-        x.sd.chunks = c.take<int32_t>((size_t)x.splan.nchunk);
+        x.sd.chunks = c.take<uint64_t>((size_t)x.splan.nchunk);
         x.sd.chunk = x.splan.chunk;
         x.sact = ActQ{c.take<half_t>((size_t)T * Is), c.take<float>((size_t)T * (Is / kStep)), T};
         x.sh_part = x.splan.ks_gu > 1 ? c.take<float>((size_t)x.splan.ks_gu * T * 2 * Is) : nullptr;
@@ -257,7 +257,7 @@ __global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__res
     if (threadIdx.x == 0) {
         d.rows[t] = t;
         d.slots[t] = 0;
-        if (t % d.chunk == 0) d.chunks[t / d.chunk] = t / d.chunk;  // expert 0, chunk j
+        if (t % d.chunk == 0) d.chunks[t / d.chunk] = chunk_entry(0, t, min(d.chunk, T - t));  // expert 0
     }
     if (!lin) return;
     // one wavefront per token; sigmoid as cpu.sigmoid (cpu.zig:1223-1230)
@@ -693,7 +693,8 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
     fwd_layout(L, 1, 1, &f, (uint8_t *)ctx->ws.base, true);
     std::vector<int32_t> off(E + 1);
     for (int e = 0; e <= E; e++) off[e] = e > (int)expert ? 1 : 0;
-    const int32_t zero = 0, act = (int32_t)expert, meta[4] = {1, 1, 0, 1}, chunk0 = (int32_t)(expert << 16);
+    const int32_t zero = 0, act = (int32_t)expert, meta[4] = {1, 1, 0, 1};
+    const uint64_t chunk0 = chunk_entry((int)expert, 0, 1);
     hipStream_t st = ctx->stream;
     ANEDVD_HIP(hipMemcpyAsync(f.h_in, h, (size_t)H * 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.offsets, off.data(), (size_t)(E + 1) * 4, hipMemcpyHostToDevice, st));
@@ -702,7 +703,7 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
     ANEDVD_HIP(hipMemcpyAsync(f.d.inv, &zero, 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.active, &act, 4, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.d.meta, meta, sizeof meta, hipMemcpyHostToDevice, st));
-    ANEDVD_HIP(hipMemcpyAsync(f.d.chunks, &chunk0, 4, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(f.d.chunks, &chunk0, sizeof chunk0, hipMemcpyHostToDevice, st));
     ANEDVD_HIP(hipMemcpyAsync(f.probs, &weight, 4, hipMemcpyHostToDevice, st));
     ANEDVD_TRY(launch_act_prep(f.h_in, 1, H, f.xq, st));
     ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, 1, f.plan, f.part, f.act, L->gelu, st));
