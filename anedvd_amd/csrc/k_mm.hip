@@ -52,7 +52,6 @@ constexpr int kWaves = 4;
 // MFMA result r then contributes d * r - mn * (activation block sum).
 
 struct MQ8_0 {
-    static constexpr bool kDeep = true;  // weights two steps ahead
     static constexpr int kSpu = 1;
     static constexpr bool kMin = false;
     struct Raw {
@@ -79,7 +78,6 @@ struct MQ8_0 {
 };
 
 struct MQ4_0 {
-    static constexpr bool kDeep = true;  // weights two steps ahead
     static constexpr int kSpu = 1;
     static constexpr bool kMin = false;
     struct Raw {
@@ -111,7 +109,6 @@ struct MQ4_0 {
 // fifth bits in the high-bit plane.  The min coefficient is -m.
 template <bool kFive, bool kHasMin>
 struct MQLegacy {
-    static constexpr bool kDeep = true;  // weights two steps ahead
     static constexpr int kSpu = 1;
     static constexpr bool kMin = kHasMin;
     struct Raw {
@@ -168,7 +165,6 @@ using MQ5_1 = MQLegacy<true, true>;
 // Q4_K: step s covers sub-blocks 2 (s % 4) + j; y = d1 n - m1 with d1 = d * sc,
 // m1 = dmin * m.
 struct MQ4_K {
-    static constexpr bool kDeep = false;  // weights one step ahead
     static constexpr int kSpu = 4;
     static constexpr bool kMin = true;
     struct Raw {
@@ -212,7 +208,6 @@ struct MQ4_K {
 
 // Q5_K: the Q4_K scheme on 5-bit values, the fifth bit from the high-bit plane.
 struct MQ5_K {
-    static constexpr bool kDeep = false;  // weights one step ahead
     static constexpr int kSpu = 4;
     static constexpr bool kMin = true;
     struct Raw {
@@ -267,7 +262,6 @@ struct MQ5_K {
 // per lane in f32 and rounded to f16 with the weight (one rounding of each).
 template <bool kThree>
 struct MQ23K {
-    static constexpr bool kDeep = false;  // weights one step ahead
     static constexpr int kSpu = 4;
     static constexpr bool kMin = false;
     struct Raw {
@@ -340,7 +334,6 @@ using MQ3_K = MQ23K<true>;
 // its int8 scale is folded into the f16 weights and the super-block's d applied
 // to the result.
 struct MQ6_K {
-    static constexpr bool kDeep = false;  // weights one step ahead
     static constexpr int kSpu = 4;
     static constexpr bool kMin = false;
     struct Raw {
@@ -490,12 +483,11 @@ __device__ inline void mm_step(const typename D::Raw &w, typename D::State &st, 
 // Streams steps [s0, s1) of the wavefront's four tiles (row block rb of the
 // matrix whose planes are W).
 //
-// MT = 1 with a two-step-ahead decoder (Q8_0, Q4_0): weights are loaded two steps
-// ahead of the MFMAs that use them (three register buffers in rotation) and
-// activations one step ahead, issued before the weights so that waiting for them
-// never waits for the later weight loads.  Otherwise (more token tiles, or the
-// super-block formats, which carry more state per buffer) everything is loaded
-// one step ahead.
+// Weights and activations are loaded one step ahead of the MFMAs that use them (two
+// register buffers in rotation), the activations first, so that waiting for them
+// never waits for the later weight loads.  (Weights two steps ahead, through three
+// buffers, cost the Q8_0 kernels 24-28 more VGPRs -- one wavefront per SIMD -- and
+// measured slower at every decode batch.)
 //
 // Loads are unconditional, so every trip through the loop issues the same loads
 // in the same order and the compiler's wait counts stay exact (a skipped load would
@@ -512,44 +504,20 @@ __device__ inline void mm_steps(const Planes &W, int rb, int s0, int s1, int lan
     const int sl = s1 - 1, so = (W.nrb - rb) * W.steps;
     auto ws = [&](int x) { return x < s1 ? x : so; };
     typename D::State st;
-    if (!D::kDeep || MT > 1) {
-        typename D::Raw w0, w1;
-        AStep<MT, MODE> x0, x1;
-        load_a(x0, A, s0);
-        D::load(w0, W, rb, s0, lane);
-        for (int s = s0; s < s1; s += 2) {
-            load_a(x1, A, min(s + 1, sl));
-            D::load(w1, W, rb, ws(s + 1), lane);
-            __builtin_amdgcn_sched_barrier(0);
-            mm_step<D, MT, MODE>(w0, st, x0, s, lane, acc);
-            if (s + 1 >= s1) break;
-            load_a(x0, A, min(s + 2, sl));
-            D::load(w0, W, rb, ws(s + 2), lane);
-            __builtin_amdgcn_sched_barrier(0);
-            mm_step<D, MT, MODE>(w1, st, x1, s + 1, lane, acc);
-        }
-        return;
-    }
-    typename D::Raw w0, w1, w2;
-    AStep<MT, MODE> x0, x1, x2;
+    typename D::Raw w0, w1;
+    AStep<MT, MODE> x0, x1;
     load_a(x0, A, s0);
     D::load(w0, W, rb, s0, lane);
-    D::load(w1, W, rb, ws(s0 + 1), lane);
-    for (int s = s0; s < s1; s += 3) {
+    for (int s = s0; s < s1; s += 2) {
         load_a(x1, A, min(s + 1, sl));
-        D::load(w2, W, rb, ws(s + 2), lane);
+        D::load(w1, W, rb, ws(s + 1), lane);
         __builtin_amdgcn_sched_barrier(0);
         mm_step<D, MT, MODE>(w0, st, x0, s, lane, acc);
         if (s + 1 >= s1) break;
-        load_a(x2, A, min(s + 2, sl));
-        D::load(w0, W, rb, ws(s + 3), lane);
+        load_a(x0, A, min(s + 2, sl));
+        D::load(w0, W, rb, ws(s + 2), lane);
         __builtin_amdgcn_sched_barrier(0);
         mm_step<D, MT, MODE>(w1, st, x1, s + 1, lane, acc);
-        if (s + 2 >= s1) break;
-        load_a(x0, A, min(s + 3, sl));
-        D::load(w1, W, rb, ws(s + 4), lane);
-        __builtin_amdgcn_sched_barrier(0);
-        mm_step<D, MT, MODE>(w2, st, x2, s + 2, lane, acc);
     }
 }
 
