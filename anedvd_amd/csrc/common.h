@@ -112,6 +112,7 @@ __host__ __device__ inline Fmt tile_fmt(int t)
     case ANEDVD_Q4_K: return Fmt{8, 16, 4, 256};
     case ANEDVD_Q5_K: return Fmt{8, 16, 4, 256};
     case ANEDVD_Q6_K: return Fmt{8, 16, 4, 256};
+    case ANEDVD_F16: return Fmt{32, 0, 1, 1};  // the f16 values themselves, no scales
     default: return Fmt{0, 0, 0, 0};
     }
 }

@@ -259,6 +259,7 @@ __device__ inline int q3k_scale(const uint8_t *s12, int k)
 __device__ inline int gguf_quant(int t, const uint8_t *blk, int e)
 {
     switch (t) {
+    case ANEDVD_F16: return rd16(blk + 2 * e);  // the value's 16 bits
     case ANEDVD_Q8_0: return (int)(int8_t)blk[2 + e];
     case ANEDVD_Q8_1: return (int)(int8_t)blk[4 + e];  // dequantQ8_1: qs after d and s
     case ANEDVD_Q4_0: return e < 16 ? blk[2 + e] & 0xF : blk[2 + e - 16] >> 4;  // dequantQ4_0
@@ -300,6 +301,10 @@ __device__ inline int gguf_quant(int t, const uint8_t *blk, int e)
 __device__ inline void set_gguf_quant(int t, uint8_t *blk, int e, int v)
 {
     switch (t) {
+    case ANEDVD_F16:
+        blk[2 * e] = (uint8_t)(v & 0xFF);
+        blk[2 * e + 1] = (uint8_t)((v >> 8) & 0xFF);
+        break;
     case ANEDVD_Q8_0: blk[2 + e] = (uint8_t)v; break;
     case ANEDVD_Q8_1: blk[4 + e] = (uint8_t)v; break;
     case ANEDVD_Q4_0:
@@ -357,6 +362,12 @@ __device__ inline void set_gguf_quant(int t, uint8_t *blk, int e, int v)
 __device__ inline void pack_lane(int t, const int *v, uint8_t *out)
 {
     switch (t) {
+    case ANEDVD_F16:  // the 16 values in order, 2 bytes each: block j in bytes 16 j .. 16 j + 15
+        for (int k = 0; k < 16; k++) {
+            out[2 * k] = (uint8_t)(v[k] & 0xFF);
+            out[2 * k + 1] = (uint8_t)((v[k] >> 8) & 0xFF);
+        }
+        break;
     case ANEDVD_Q8_0:
     case ANEDVD_Q8_1:
         for (int k = 0; k < 16; k++) out[k] = (uint8_t)((v[k] + 128) & 0xFF);
@@ -408,6 +419,7 @@ __device__ inline void pack_lane(int t, const int *v, uint8_t *out)
 __device__ inline int unpack_lane(int t, const uint8_t *in, int k)
 {
     switch (t) {
+    case ANEDVD_F16: return in[2 * k] | (in[2 * k + 1] << 8);
     case ANEDVD_Q8_0:
     case ANEDVD_Q8_1: return (int)in[k] - 128;
     case ANEDVD_Q2_K:
@@ -466,7 +478,7 @@ __global__ void k_repack(QMat m, const uint8_t *__restrict__ src)
                 const int c = kStep * s + mma_col(g, k >> 3, k & 7);
                 v[k] = gguf_quant(m.type, row + (size_t)(c / epb) * bpb, c % epb);
             }
-            uint8_t lb[16];  // Q8_0: 16 quant bytes; Q5_K / Q6_K: 8 quant + 2 / 4 high-bit bytes
+            uint8_t lb[32];  // F16: 32 value bytes; Q8_0: 16 quant bytes; Q5_K / Q6_K: 8 quant + 2 / 4 high-bit bytes
             pack_lane(m.type, v, lb);
             uint8_t *dst = q + tile_q_off(f, m.steps, rb, s, t, 16 * g + n);
             for (int k = 0; k < f.qb; k++) dst[k] = lb[k];
@@ -542,7 +554,7 @@ __global__ void k_dequant_tiles(QMat m, int mat, float *__restrict__ out)
     for (int e = 0; e < epb; e++) {
         const int c = b * epb + e, s = c / kStep, w = c % kStep;
         const int j = w >> 5, g = (w & 31) >> 3, i = w & 7;
-        uint8_t lb[16];  // Q8_0: 16 quant bytes; Q5_K / Q6_K: 8 quant + 2 / 4 high-bit bytes
+        uint8_t lb[32];  // F16: 32 value bytes; Q8_0: 16 quant bytes; Q5_K / Q6_K: 8 quant + 2 / 4 high-bit bytes
         const uint8_t *src = q + tile_q_off(f, m.steps, rb, s, t, 16 * g + n);
         for (int k = 0; k < f.qb; k++) lb[k] = src[k];
         if (const int hb = tile_hb(m.type)) {
@@ -618,7 +630,7 @@ int launch_dequant_gguf(int t, const uint8_t *d_src, size_t n_blocks, float *d_o
 
 // The formats with a tile layout, for the per-format kernel instantiations.
 #define ANEDVD_TILE_TYPES(X) X(ANEDVD_Q8_0) X(ANEDVD_Q8_1) X(ANEDVD_Q4_0) X(ANEDVD_Q4_1) X(ANEDVD_Q5_0) \
-    X(ANEDVD_Q5_1) X(ANEDVD_Q2_K) X(ANEDVD_Q3_K) X(ANEDVD_Q4_K) X(ANEDVD_Q5_K) X(ANEDVD_Q6_K)
+    X(ANEDVD_Q5_1) X(ANEDVD_Q2_K) X(ANEDVD_Q3_K) X(ANEDVD_Q4_K) X(ANEDVD_Q5_K) X(ANEDVD_Q6_K) X(ANEDVD_F16)
 
 int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st)
 {

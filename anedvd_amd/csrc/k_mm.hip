@@ -51,6 +51,35 @@ constexpr int kWaves = 4;
 // t, block j) with the block's scale d and min coefficient mn (operand); the
 // MFMA result r then contributes d * r - mn * (activation block sum).
 
+// F16 experts (the eager path's weights, cpu.moeExpertAccum with matmulF16,
+// cpu.zig:1141-1185): the tile holds the values themselves, the B operand without
+// any conversion.
+struct MF16 {
+    static constexpr int kSpu = 1;
+    static constexpr bool kMin = false;
+    struct Raw {
+        u32x4 q[4][2];
+    };
+    struct State {};
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 32);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                r.q[t][j] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 32 * lane + 2048 * t + 16 * j, qo, kNT);
+    }
+    __device__ static inline void begin(const Raw &, State &, int) {}
+    __device__ static inline void operand(const Raw &r, const State &, int, int, int t, int j, half8 &b, float &d,
+                                          float &mn)
+    {
+        b = as_h8(r.q[t][j]);
+        d = 1.0f;
+        mn = 0.0f;
+    }
+};
+
 struct MQ8_0 {
     static constexpr int kSpu = 1;
     static constexpr bool kMin = false;
@@ -957,6 +986,7 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
     switch (gate.type) {
     case ANEDVD_Q8_0:
     case ANEDVD_Q8_1: rc = launch_gateup_d<MQ8_0>(a, plan.mt, st); break;  // one tile layout
+    case ANEDVD_F16: rc = launch_gateup_d<MF16>(a, plan.mt, st); break;
     case ANEDVD_Q4_0: rc = launch_gateup_d<MQ4_0>(a, plan.mt, st); break;
     case ANEDVD_Q4_1: rc = launch_gateup_d<MQ4_1>(a, plan.mt, st); break;
     case ANEDVD_Q5_0: rc = launch_gateup_d<MQ5_0>(a, plan.mt, st); break;
@@ -999,6 +1029,7 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
     switch (down.type) {
     case ANEDVD_Q8_0:
     case ANEDVD_Q8_1: return launch_down_d<MQ8_0>(a, plan.mt, st);
+    case ANEDVD_F16: return launch_down_d<MF16>(a, plan.mt, st);
     case ANEDVD_Q4_0: return launch_down_d<MQ4_0>(a, plan.mt, st);
     case ANEDVD_Q4_1: return launch_down_d<MQ4_1>(a, plan.mt, st);
     case ANEDVD_Q5_0: return launch_down_d<MQ5_0>(a, plan.mt, st);

@@ -67,6 +67,29 @@ __device__ inline uint32_t h2_bits(h2 h)
 // and yields the f16 B operand of (tile tt, block j) at step `ss` of the unit:
 // bop().  Lane l = 16 g + n holds row n of the tile and the 8 columns 32 j + 8 g + i.
 
+// F16 experts: the tile holds the values themselves.
+struct FF16 {
+    static constexpr int kSpu = 1;
+    static constexpr bool kHoistA = false;  // 32 VGPRs of values per ring slot already
+    static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
+    static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
+    struct Raw {
+        u32x4 q[kPfTiles][2];
+    };
+    struct State {};
+    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    {
+        const int qo = lane_plane_off(p, rb, s, 32);
+#pragma unroll
+        for (int tt = 0; tt < kPfTiles; tt++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                r.q[tt][j] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 32 * lane + 2048 * tt + 16 * j, qo, kNT);
+    }
+    __device__ static inline void begin(const Raw &, State &, int, int) {}
+    __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int) { return as_h8(r.q[tt][j]); }
+};
+
 struct FQ8_0 {
     static constexpr int kSpu = 1;
     static constexpr bool kHoistA = false;  // at 176 VGPRs two waves per SIMD instead of three
@@ -808,6 +831,7 @@ static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStr
     switch (type) {
     case ANEDVD_Q8_0:
     case ANEDVD_Q8_1: return launch_pf_mt<FQ8_0>(a, mt, gateup, st);  // one tile layout
+    case ANEDVD_F16: return launch_pf_mt<FF16>(a, mt, gateup, st);
     case ANEDVD_Q4_0: return launch_pf_mt<FQ4_0>(a, mt, gateup, st);
     case ANEDVD_Q4_1: return launch_pf_mt<FQ4_1>(a, mt, gateup, st);
     case ANEDVD_Q5_0: return launch_pf_mt<FQ5_0>(a, mt, gateup, st);

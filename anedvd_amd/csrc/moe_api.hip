@@ -100,7 +100,7 @@ int make_qmat(QMat &m, int type, int rows, int cols, int n, const void *host, si
 {
     const Fmt f = tile_fmt(type);
     if (!mm_supported(type)) {
-        set_error("%s: ggml type %d is not supported by the GPU layout (q8_0, q8_1, q4_0, q4_1, q5_0, q5_1, q2_k, q3_k, q4_k, q5_k, q6_k)", what, type);
+        set_error("%s: ggml type %d is not supported by the GPU layout (f16, q8_0, q8_1, q4_0, q4_1, q5_0, q5_1, q2_k, q3_k, q4_k, q5_k, q6_k)", what, type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
     const int unit_cols = kStep * f.spu;

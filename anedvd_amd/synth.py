@@ -170,7 +170,13 @@ def q3_k(seed: int, stream: int, n_blocks: int, sigma: float = 0.01, offset: int
     return blk
 
 
-_GEN = {W.Q8_0: q8_0, W.Q8_1: q8_1, W.Q4_0: q4_0, W.Q4_1: q4_1, W.Q5_0: q5_0, W.Q5_1: q5_1, W.Q2_K: q2_k,
+def f16(seed: int, stream: int, n_blocks: int, sigma: float = 0.02, offset: int = 0) -> np.ndarray:
+    """F16 weights (blocks of one value): N(0, sigma) rounded to f16."""
+    v = (normal(seed, stream, n_blocks, offset) * sigma).astype(np.float16)
+    return v.view(np.uint8).reshape(n_blocks, 2)
+
+
+_GEN = {W.F16: f16, W.Q8_0: q8_0, W.Q8_1: q8_1, W.Q4_0: q4_0, W.Q4_1: q4_1, W.Q5_0: q5_0, W.Q5_1: q5_1, W.Q2_K: q2_k,
         W.Q3_K: q3_k, W.Q4_K: q4_k, W.Q5_K: q5_k, W.Q6_K: q6_k}
 
 

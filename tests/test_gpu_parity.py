@@ -65,7 +65,8 @@ def test_dequant_random_blocks_bit_exact(ctx, t):
 
 @pytest.mark.parametrize("types", [(W.Q8_0, W.Q8_0, W.Q8_0), (W.Q4_K, W.Q4_K, W.Q6_K), (W.Q4_0, W.Q4_0, W.Q4_0),
                                    (W.Q5_K, W.Q5_K, W.Q6_K), (W.Q5_K, W.Q5_K, W.Q5_K), (W.Q4_1, W.Q4_1, W.Q8_1),
-                                   (W.Q5_0, W.Q5_0, W.Q5_1), (W.Q2_K, W.Q2_K, W.Q3_K), (W.Q3_K, W.Q3_K, W.Q2_K)])
+                                   (W.Q5_0, W.Q5_0, W.Q5_1), (W.Q2_K, W.Q2_K, W.Q3_K), (W.Q3_K, W.Q3_K, W.Q2_K),
+                                   (W.F16, W.F16, W.F16)])
 def test_resident_experts_bit_exact(ctx, types):
     """The tile repack keeps every dequantised weight: readExpertF32 of the
     resident layer equals the oracle's on the GGUF payload, all three projections."""
@@ -308,7 +309,8 @@ def test_forward_zero_input_gives_zero(ctx):
 
 FORMATS = [(W.Q4_0, W.Q4_0, W.Q4_0), (W.Q4_K, W.Q4_K, W.Q6_K), (W.Q8_0, W.Q8_0, W.Q6_K), (W.Q4_K, W.Q4_K, W.Q4_K),
            (W.Q6_K, W.Q6_K, W.Q8_0), (W.Q5_K, W.Q5_K, W.Q6_K), (W.Q8_0, W.Q8_0, W.Q5_K), (W.Q4_1, W.Q4_1, W.Q5_1),
-           (W.Q5_0, W.Q5_0, W.Q8_1), (W.Q2_K, W.Q2_K, W.Q3_K), (W.Q3_K, W.Q3_K, W.Q4_K)]
+           (W.Q5_0, W.Q5_0, W.Q8_1), (W.Q2_K, W.Q2_K, W.Q3_K), (W.Q3_K, W.Q3_K, W.Q4_K), (W.F16, W.F16, W.F16),
+           (W.F16, W.F16, W.Q8_0)]
 
 
 @pytest.mark.parametrize("types", FORMATS, ids=lambda t: "/".join(W.TYPE_NAMES[x] for x in t))
