@@ -50,6 +50,10 @@ constexpr int kWaves = 4;
 // stays valid for a whole scale unit (begin), and yields the B operand of (tile
 // t, block j) with the block's scale d and min coefficient mn (operand); the
 // MFMA result r then contributes d * r - mn * (activation block sum).
+//
+// A load's per-lane offset is one VGPR shared by the four tiles; the tile's
+// constant offset goes into the scalar offset.  (Written as VGPR sums, the
+// hoisted loop invariants took a register per tile: 6-8 more VGPRs per kernel.)
 
 // F16 experts (the eager path's weights, cpu.moeExpertAccum with matmulF16,
 // cpu.zig:1141-1185): the tile holds the values themselves, the B operand without
@@ -68,7 +72,7 @@ struct MF16 {
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int j = 0; j < 2; j++)
-                r.q[t][j] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 32 * lane + 2048 * t + 16 * j, qo, kNT);
+                r.q[t][j] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 32 * lane, qo + 2048 * t + 16 * j, kNT);
     }
     __device__ static inline void begin(const Raw &, State &, int) {}
     __device__ static inline void operand(const Raw &r, const State &, int, int, int t, int j, half8 &b, float &d,
@@ -92,9 +96,9 @@ struct MQ8_0 {
     {
         const int qo = lane_plane_off(p, rb, s, 16), so = row_plane_off(p, rb, s, 4);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane + 1024 * t, qo, kNT);
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane, qo + 1024 * t, kNT);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.s[t] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * t, so, kNT);
+        for (int t = 0; t < 4; t++) r.s[t] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * t, kNT);
     }
     __device__ static inline void begin(const Raw &, State &, int) {}
     __device__ static inline void operand(const Raw &r, const State &, int, int, int t, int j, half8 &b, float &d,
@@ -118,9 +122,9 @@ struct MQ4_0 {
     {
         const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, 4);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * t, kNT);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.s[t] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * t, so, kNT);
+        for (int t = 0; t < 4; t++) r.s[t] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * t, kNT);
     }
     __device__ static inline void begin(const Raw &, State &, int) {}
     __device__ static inline void operand(const Raw &r, const State &, int, int, int t, int j, half8 &b, float &d,
@@ -150,18 +154,18 @@ struct MQLegacy {
     {
         const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, kHasMin ? 8 : 4);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * t, kNT);
         if constexpr (kFive) {
             const int ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
-            for (int t = 0; t < 4; t++) r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * t, ho, kNT);
+            for (int t = 0; t < 4; t++) r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, ho + 128 * t, kNT);
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             if constexpr (kHasMin)
-                r.s[t] = __builtin_amdgcn_raw_buffer_load_b64(p.s, 8 * (lane & 15) + 128 * t, so, kNT);
+                r.s[t] = __builtin_amdgcn_raw_buffer_load_b64(p.s, 8 * (lane & 15), so + 128 * t, kNT);
             else
-                r.s[t].x = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * t, so, kNT);
+                r.s[t].x = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * t, kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int) {}
@@ -207,12 +211,12 @@ struct MQ4_K {
     {
         const int qo = lane_plane_off(p, rb, s, 8);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * t, kNT);
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int t = 0; t < 4; t++)
-                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * t, so, kNT);
+                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * t, kNT);
         }
     }
     __device__ static inline void begin(const Raw &r, State &st, int s)
@@ -250,14 +254,14 @@ struct MQ5_K {
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
-            r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * t, ho, kNT);
+            r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * t, kNT);
+            r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, ho + 128 * t, kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int t = 0; t < 4; t++)
-                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * t, so, kNT);
+                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * t, kNT);
         }
     }
     __device__ static inline void begin(const Raw &r, State &st, int s)
@@ -307,21 +311,21 @@ struct MQ23K {
     {
         const int qo = lane_plane_off(p, rb, s, 4);
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b32(p.q, 4 * lane + 256 * t, qo, kNT);
+        for (int t = 0; t < 4; t++) r.q[t] = __builtin_amdgcn_raw_buffer_load_b32(p.q, 4 * lane, qo + 256 * t, kNT);
         if constexpr (kThree) {
             const int ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
-            for (int t = 0; t < 4; t++) r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * t, ho, kNT);
+            for (int t = 0; t < 4; t++) r.h[t] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, ho + 128 * t, kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, kThree ? 2 : 4);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * t, so, kNT);
+                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * t, kNT);
                 if constexpr (kThree)
-                    r.dm[t] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * t, dof, kNT);
+                    r.dm[t] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15), dof + 32 * t, kNT);
                 else
-                    r.dm[t] = __builtin_amdgcn_raw_buffer_load_b32(p.d, 4 * (lane & 15) + 64 * t, dof, kNT);
+                    r.dm[t] = __builtin_amdgcn_raw_buffer_load_b32(p.d, 4 * (lane & 15), dof + 64 * t, kNT);
             }
         }
     }
@@ -380,15 +384,15 @@ struct MQ6_K {
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * t, qo, kNT);
-            r.h[t] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane + 256 * t, ho, kNT);
+            r.q[t] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * t, kNT);
+            r.h[t] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane, ho + 256 * t, kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, 2);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * t, so, kNT);
-                r.d[t] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * t, dof, kNT);
+                r.sc[t] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * t, kNT);
+                r.d[t] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15), dof + 32 * t, kNT);
             }
         }
     }
@@ -457,7 +461,7 @@ __device__ inline void load_a(AStep<MT, MODE> &x, const AOp<MT> &a, int s)
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         x.a0[mt] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff[mt], s * 2 * kStep, 0));
-        x.a1[mt] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff[mt] + 16, s * 2 * kStep, 0));
+        x.a1[mt] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(a.q, a.qoff[mt], s * 2 * kStep + 16, 0));
     }
     if (MODE == kStepDs) {
 #pragma unroll
@@ -515,8 +519,8 @@ __device__ inline void mm_step(const typename D::Raw &w, typename D::State &st, 
 // Weights and activations are loaded one step ahead of the MFMAs that use them (two
 // register buffers in rotation), the activations first, so that waiting for them
 // never waits for the later weight loads.  (Weights two steps ahead, through three
-// buffers, cost the Q8_0 kernels 24-28 more VGPRs -- one wavefront per SIMD -- and
-// measured slower at every decode batch.)
+// buffers, measured slower: at 5 and 4 wavefronts per SIMD alike, the Q8_0 down
+// kernel was no faster at 64 tokens and 3-9 % slower at 1 and 8.)
 //
 // Loads are unconditional, so every trip through the loop issues the same loads
 // in the same order and the compiler's wait counts stay exact (a skipped load would

@@ -84,7 +84,7 @@ struct FF16 {
         for (int tt = 0; tt < kPfTiles; tt++)
 #pragma unroll
             for (int j = 0; j < 2; j++)
-                r.q[tt][j] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 32 * lane + 2048 * tt + 16 * j, qo, kNT);
+                r.q[tt][j] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 32 * lane, qo + 2048 * tt + 16 * j, kNT);
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
     __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int) { return as_h8(r.q[tt][j]); }
@@ -105,8 +105,8 @@ struct FQ8_0 {
         const int qo = lane_plane_off(p, rb, s, 16), so = row_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane + 1024 * tt, qo, kNT);
-            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * tt, so, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane, qo + 1024 * tt, kNT);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * tt, kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -132,8 +132,8 @@ struct FQ4_0 {
         const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
-            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * tt, so, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * tt, kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -165,17 +165,17 @@ struct FQLegacy {
         const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, kHasMin ? 8 : 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
             if constexpr (kHasMin)
-                r.s[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.s, 8 * (lane & 15) + 128 * tt, so, kNT);
+                r.s[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.s, 8 * (lane & 15), so + 128 * tt, kNT);
             else
-                r.s[tt].x = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15) + 64 * tt, so, kNT);
+                r.s[tt].x = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * tt, kNT);
         }
         if constexpr (kFive) {
             const int ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * tt, ho, kNT);
+                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, ho + 128 * tt, kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -221,12 +221,12 @@ struct FQ4_K {
     {
         const int qo = lane_plane_off(p, rb, s, 8);
 #pragma unroll
-        for (int tt = 0; tt < kPfTiles; tt++) r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
+        for (int tt = 0; tt < kPfTiles; tt++) r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * tt, kNT);
         }
     }
     // The 6-bit scales and mins of getScaleMinK4 (gguf.zig:948-958) for all eight
@@ -286,14 +286,14 @@ struct FQ5_K {
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
-            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * tt, ho, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, ho + 128 * tt, kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * tt, kNT);
         }
     }
     __device__ static inline void begin(const Raw &r, State &st, int ss, int lane)
@@ -338,19 +338,19 @@ struct FQ23K {
         const int qo = lane_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.q, 4 * lane + 256 * tt, qo, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.q, 4 * lane, qo + 256 * tt, kNT);
             if constexpr (kThree)
-                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane + 128 * tt, lane_plane_off(p, rb, s, 2), kNT);
+                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, lane_plane_off(p, rb, s, 2) + 128 * tt, kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, kThree ? 2 : 4);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++) {
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * tt, kNT);
                 if constexpr (kThree)
-                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * tt, dof, kNT);
+                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15), dof + 32 * tt, kNT);
                 else
-                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.d, 4 * (lane & 15) + 64 * tt, dof, kNT);
+                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.d, 4 * (lane & 15), dof + 64 * tt, kNT);
             }
         }
     }
@@ -413,15 +413,15 @@ struct FQ6_K {
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane + 512 * tt, qo, kNT);
-            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane + 256 * tt, ho, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane, ho + 256 * tt, kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, 2);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++) {
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15) + 256 * tt, so, kNT);
-                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15) + 32 * tt, dof, kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * tt, kNT);
+                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15), dof + 32 * tt, kNT);
             }
         }
     }
@@ -472,7 +472,7 @@ struct StageX {  // gate/up: token rows gathered through the dispatch; x has per
 #pragma unroll
         for (int h = 0; h < R; h++) {
             v[B][h][0] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep, 0);
-            v[B][h][1] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h] + 16, s * 2 * kStep, 0);
+            v[B][h][1] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep + 16, 0);
         }
     }
     template <int B>
@@ -500,7 +500,7 @@ struct StageAct {  // down: consecutive positions, rescaled from their group's d
 #pragma unroll
         for (int h = 0; h < R; h++) {
             v[B][h][0] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep, 0);
-            v[B][h][1] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h] + 16, s * 2 * kStep, 0);
+            v[B][h][1] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep + 16, 0);
             dg[B][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ds, doff[h], s * ld4, 0));
         }
     }
