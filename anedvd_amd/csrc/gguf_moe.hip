@@ -339,6 +339,8 @@ int moe_config(const Parsed &g, anedvd_gguf_moe_cfg &info)
         info.shared_inter = !s ? 0 : (s->dims.size() >= 2 ? (uint32_t)s->dims[1] : inter);
     }
     if (info.inter == 0) return fail(ANEDVD_E_INVALID_METADATA, "IncompleteConfig: no expert width");
+    // Gemma's FFN activation is gelu_pytorch_tanh (load_gguf.zig:145-158).
+    info.use_gelu = arch.compare(0, 5, "gemma") == 0;
     return ANEDVD_OK;
 }
 
@@ -395,23 +397,33 @@ int block_shapes(const Parsed &g, uint32_t layer, anedvd_gguf_moe_cfg &info)
     info.shared_type = -1;
     info.has_shared_gate_lin = 0;
     if (Is) {
+        // loadLinear (load_gguf.zig:358-386) takes {in, out} as stored or {out, in}
+        // transposed, of any type, and keeps the result as f16 [out][in].  Stored
+        // {in, out} with one block type for the three, the payloads go to the GPU
+        // as they are; otherwise they are read as f16 and transposed as loadLinear
+        // does (shared_as_f16).
         int32_t ty[3];
+        bool transposed = false;
         const char *names[3] = {"ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp"};
         for (int j = 0; j < 3; j++) {
             ANEDVD_TRY(find(g, blk(layer, names[j]), t));
             const uint64_t a = j < 2 ? H : Is, b = j < 2 ? Is : H;
-            if (t->dims.size() != 2 || t->dims[0] != a || t->dims[1] != b) {
-                set_error("gguf: %s has dims other than {%llu, %llu}", t->name.c_str(), (unsigned long long)a,
-                          (unsigned long long)b);
+            const bool as_stored = t->dims.size() >= 2 && t->dims[0] == a && t->dims[1] == b;
+            const bool swapped = t->dims.size() >= 2 && t->dims[0] == b && t->dims[1] == a;
+            if (t->elems() != a * b || !(as_stored || swapped)) {
+                set_error("gguf: %s is not a %llu x %llu matrix", t->name.c_str(), (unsigned long long)b,
+                          (unsigned long long)a);
                 return ANEDVD_E_DIMENSION;
+            }
+            if (!as_stored) transposed = true;
+            if (!block_elems(t->type)) {
+                set_error("gguf: %s has unknown ggml type %d", t->name.c_str(), (int)t->type);
+                return ANEDVD_E_UNSUPPORTED_TYPE;
             }
             ty[j] = t->type;
         }
-        if (ty[0] != ty[1] || ty[0] != ty[2]) {
-            set_error("gguf: shared expert tensors of types %d/%d/%d; one type is supported", ty[0], ty[1], ty[2]);
-            return ANEDVD_E_UNSUPPORTED_TYPE;
-        }
         info.shared_type = ty[0];
+        info.shared_as_f16 = transposed || ty[0] != ty[1] || ty[0] != ty[2] || !mm_supported(ty[0]);
         // The gate vector is mandatory once there is a shared expert (load_gguf.zig:818-823).
         ANEDVD_TRY(find(g, blk(layer, "ffn_gate_inp_shexp"), t));
         if (t->elems() != H) {
@@ -516,10 +528,10 @@ int anedvd_moe_layer_create_gguf(anedvd_moe_ctx *ctx, const void *gguf, size_t l
     d.inter = info.inter;
     d.n_experts = E;
     d.k = info.k;
-    // The GGUF loader leaves norm_topk_prob and use_gelu at their defaults (false)
-    // for the MoE architectures; a caller may override them.
+    // The GGUF loader leaves norm_topk_prob false and sets use_gelu for the gemma
+    // architectures only (load_gguf.zig:145-158); a caller may override either.
     d.norm_topk_prob = opts && opts->norm_topk_prob >= 0 ? opts->norm_topk_prob : 0;
-    d.use_gelu = opts && opts->use_gelu >= 0 ? opts->use_gelu : 0;
+    d.use_gelu = opts && opts->use_gelu >= 0 ? opts->use_gelu : info.use_gelu;
     const Tensor *t;
     const uint8_t *p;
     size_t n;
@@ -543,19 +555,31 @@ int anedvd_moe_layer_create_gguf(anedvd_moe_ctx *ctx, const void *gguf, size_t l
         router.swap(tr);
     }
     d.router = router.data();
-    std::vector<uint16_t> lin;
+    std::vector<uint16_t> lin, sh16[3];
     if (info.shared_inter) {
         d.shared_inter = info.shared_inter;
-        d.shared_type = info.shared_type;
-        ANEDVD_TRY(find(g, blk(layer, "ffn_gate_shexp"), t));
-        ANEDVD_TRY(tensor_bytes(g, *t, p, n));
-        d.shared_gate = p, d.shared_gate_bytes = n;
-        ANEDVD_TRY(find(g, blk(layer, "ffn_up_shexp"), t));
-        ANEDVD_TRY(tensor_bytes(g, *t, p, n));
-        d.shared_up = p, d.shared_up_bytes = n;
-        ANEDVD_TRY(find(g, blk(layer, "ffn_down_shexp"), t));
-        ANEDVD_TRY(tensor_bytes(g, *t, p, n));
-        d.shared_down = p, d.shared_down_bytes = n;
+        d.shared_type = info.shared_as_f16 ? ANEDVD_F16 : info.shared_type;
+        const char *names[3] = {"ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp"};
+        const void **ptrs[3] = {&d.shared_gate, &d.shared_up, &d.shared_down};
+        size_t *lens[3] = {&d.shared_gate_bytes, &d.shared_up_bytes, &d.shared_down_bytes};
+        for (int j = 0; j < 3; j++) {
+            ANEDVD_TRY(find(g, blk(layer, names[j]), t));
+            if (!info.shared_as_f16) {
+                ANEDVD_TRY(tensor_bytes(g, *t, p, n));
+                *ptrs[j] = p, *lens[j] = n;
+                continue;
+            }
+            // loadLinear: readF16, then [out][in] (transposed when stored {out, in})
+            const uint64_t in = j < 2 ? H : info.shared_inter, outd = j < 2 ? info.shared_inter : H;
+            ANEDVD_TRY(read_f16(ctx, g, *t, sh16[j]));
+            if (t->dims[0] != in) {
+                std::vector<uint16_t> tr(sh16[j].size());
+                for (uint64_t o = 0; o < outd; o++)
+                    for (uint64_t i = 0; i < in; i++) tr[o * in + i] = sh16[j][i * outd + o];
+                sh16[j].swap(tr);
+            }
+            *ptrs[j] = sh16[j].data(), *lens[j] = sh16[j].size() * 2;
+        }
         // readF32 then f16 (load_gguf.zig:818-823)
         ANEDVD_TRY(find(g, blk(layer, "ffn_gate_inp_shexp"), t));
         std::vector<float> f;

@@ -649,6 +649,26 @@ int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st)
     return ANEDVD_OK;
 }
 
+// f32ToF16Slice (gguf.zig:682-692): each value rounded to the nearest f16, ties
+// to even (the hardware conversion's default rounding), overflow to infinity.
+__global__ void k_f32_to_f16(const float *__restrict__ src, uint16_t *__restrict__ dst, size_t n)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const half_t h = (half_t)src[i];
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    dst[i] = b;
+}
+
+int launch_f32_to_f16(const float *d_src, uint16_t *d_dst, size_t n, hipStream_t st)
+{
+    if (n == 0) return ANEDVD_OK;
+    hipLaunchKernelGGL(k_f32_to_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, d_src, d_dst, n);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
 int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st)
 {
     const size_t n = (size_t)m.rows * (m.cols / block_elems(m.type));

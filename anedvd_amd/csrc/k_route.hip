@@ -87,8 +87,8 @@ int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, fl
 
 // ------------------------------------------------------------------- route
 
-constexpr int kMaxExperts = 256;
-constexpr int kMaxK = 32;
+constexpr int kMaxExperts = kMaxRouteExperts;
+constexpr int kMaxK = kMaxRouteSlots;
 
 // -------------------------------------------------- one token per wavefront
 //

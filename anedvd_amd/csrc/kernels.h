@@ -38,8 +38,11 @@ __host__ __device__ inline uint64_t chunk_entry(int e, int p0, int nt)
 int launch_dequant_gguf(int type, const uint8_t *d_src, size_t n_blocks, float *d_out, hipStream_t st);
 int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st);
 int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st);
+int launch_f32_to_f16(const float *d_src, uint16_t *d_dst, size_t n, hipStream_t st);
 
 // k_route.hip
+constexpr int kMaxRouteExperts = 256;  // experts the route and dispatch kernels take (ids fit a byte)
+constexpr int kMaxRouteSlots = 32;     // slots per token
 int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits, hipStream_t st);
 // cpu.moeRoute for T rows of logits; with d_x non-null the same launch also
 // converts x [T][H] to the GEMV activation format `xq`.
@@ -89,6 +92,12 @@ int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H
                           int mt, int nchunk, const ActQ &act, int use_gelu, hipStream_t st);
 int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
                         int nchunk, float *ypart, int kk, hipStream_t st);
+
+// k_ops.hip -- cpu.moeExpertAccumF32 / moeExpertAccum on caller weight slices
+// ([inter][hidden] gate and up, [hidden][inter] down; f32, or f16 bits when f16):
+// act[inter] = act(gate . h) * (up . h), then out[hidden] += weight * down . act.
+int launch_expert_accum_ops(bool f16, const void *gate, const void *up, const void *down, const float *h, int inter,
+                            int hidden, float weight, int use_gelu, float *act, float *out, hipStream_t st);
 
 int launch_combine(const float *ypart, const int32_t *inv, const float *probs, int T, int k, int H, int KS, int P,
                    const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st);

@@ -331,6 +331,20 @@ int check_layer(const anedvd_moe_layer *L)
     return ANEDVD_OK;
 }
 
+// The most tokens one forward call takes.  The expert kernels address the
+// activations through 32-bit buffer descriptors with int offsets: x [T][H] f16, the
+// SwiGLU activations [T*kk][I] f16 (plus a 64-row tile of look-ahead past the last
+// position) and a separate shared expert's [T][Is] f16 must each stay below 2^31
+// bytes.
+size_t max_tokens(const anedvd_moe_layer *L)
+{
+    const uint64_t lim = (1ull << 31) - 1, kk = L->k + L->n_sh;
+    uint64_t t = lim / (2ull * L->H);
+    t = std::min<uint64_t>(t, lim / (2ull * L->I) / kk - 64);
+    if (L->Is && !L->n_sh) t = std::min<uint64_t>(t, lim / (2ull * L->Is) - 64);
+    return (size_t)std::min<uint64_t>(t, 1u << 20);
+}
+
 }  // namespace
 
 extern "C" {
@@ -423,9 +437,13 @@ int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *d,
     // launches (SwiGLU is separable over the intermediate width, so the pieces sum
     // to the whole).  Otherwise it keeps matrices of its own and a launch sequence
     // on the context's second stream.
+    // The pieces are extra experts and extra slots of every token: the route and
+    // dispatch take at most kMaxRouteExperts experts and kMaxRouteSlots slots, so a
+    // shared expert that would exceed either keeps its own matrices instead.
     const int st_ = d->shared_type, bl = block_elems(st_), bb = block_bytes(st_);
     const bool merge = Is > 0 && I > 0 && st_ == d->gate_type && st_ == d->up_type && st_ == d->down_type && bl &&
                        Is % I == 0 && I % bl == 0 && H % bl == 0 &&
+                       E + Is / I <= kMaxRouteExperts && (int)d->k + Is / I <= kMaxRouteSlots &&
                        d->shared_gate_bytes == (size_t)Is * H / bl * bb && d->shared_up_bytes == d->shared_gate_bytes &&
                        d->shared_down_bytes == d->shared_gate_bytes;
     const int nsh = merge ? Is / I : 0;
@@ -503,6 +521,8 @@ void anedvd_moe_layer_free(anedvd_moe_layer *L)
 
 uint64_t anedvd_moe_layer_device_bytes(const anedvd_moe_layer *L) { return L ? L->device_bytes : 0; }
 
+size_t anedvd_moe_layer_max_tokens(const anedvd_moe_layer *L) { return L ? max_tokens(L) : 0; }
+
 // ------------------------------------------------------------ op mirrors
 
 int anedvd_dequantize_range(anedvd_moe_ctx *ctx, int t, const void *src, size_t src_len, uint64_t elem_offset,
@@ -567,6 +587,38 @@ int anedvd_moe_load_expert_f32(anedvd_moe_layer *L, int which, uint32_t expert, 
     ANEDVD_TRY(ensure(ctx->io, n * sizeof(float), ctx->stream));
     ANEDVD_TRY(launch_dequant_tiles(*m, (int)expert, (float *)ctx->io.base, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(out, ctx->io.base, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_load_expert_f16(anedvd_moe_layer *L, int which, uint32_t expert, uint16_t *out, size_t n)
+{
+    ANEDVD_TRY(check_layer(L));
+    const QMat *m = which == 0 ? &L->gate : which == 1 ? &L->up : which == 2 ? &L->down : nullptr;
+    if (!m || !out) {
+        set_error("load_expert_f16: which must be 0 (gate), 1 (up) or 2 (down)");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    if (expert >= L->E) {
+        set_error("load_expert_f16: expert %u of %u", expert, L->E);
+        return ANEDVD_E_OUT_OF_RANGE;
+    }
+    if (n != (size_t)m->rows * m->cols) {
+        set_error("load_expert_f16: out holds %zu, expert has %d x %d", n, m->rows, m->cols);
+        return ANEDVD_E_DIMENSION;
+    }
+    // readExpertF16 dequantises 2048-element chunks and rounds each (gguf.zig:521-530);
+    // the chunks are whole blocks, so dequantising the expert at once and rounding
+    // every value gives the same f16 values.
+    anedvd_moe_ctx *ctx = L->ctx;
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    const size_t f32b = (n * sizeof(float) + 255) & ~(size_t)255;
+    ANEDVD_TRY(ensure(ctx->io, f32b + n * sizeof(uint16_t), ctx->stream));
+    float *d32 = (float *)ctx->io.base;
+    uint16_t *d16 = (uint16_t *)((uint8_t *)ctx->io.base + f32b);
+    ANEDVD_TRY(launch_dequant_tiles(*m, (int)expert, d32, ctx->stream));
+    ANEDVD_TRY(launch_f32_to_f16(d32, d16, n, ctx->stream));
+    ANEDVD_HIP(hipMemcpyAsync(out, d16, n * sizeof(uint16_t), hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
     return ANEDVD_OK;
 }
@@ -670,6 +722,46 @@ int anedvd_moe_dispatch(anedvd_moe_ctx *ctx, const uint32_t *idx, size_t T, size
     return ANEDVD_OK;
 }
 
+static int expert_accum_ops(anedvd_moe_ctx *ctx, bool f16, float *out, const float *h, const void *gate,
+                            const void *up, const void *down, size_t inter, size_t hidden, float weight, int use_gelu)
+{
+    if (!ctx || !out || !h || !gate || !up || !down || !inter || !hidden || inter > (1u << 24) ||
+        hidden > (1u << 24) || inter * hidden > ((size_t)1 << 31)) {
+        set_error("expert_accum: bad arguments (inter %zu, hidden %zu)", inter, hidden);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    ANEDVD_HIP(hipSetDevice(ctx->device));
+    const size_t wb = inter * hidden * (f16 ? 2 : 4);
+    ANEDVD_TRY(ensure(ctx->io, 3 * (wb + 256) + (hidden + inter + hidden) * 4 + 1024, ctx->stream));
+    Carve c{(uint8_t *)ctx->io.base};
+    uint8_t *dg = c.take<uint8_t>(wb), *du = c.take<uint8_t>(wb), *dd = c.take<uint8_t>(wb);
+    float *dh = c.take<float>(hidden), *dact = c.take<float>(inter), *dout = c.take<float>(hidden);
+    hipStream_t st = ctx->stream;
+    ANEDVD_HIP(hipMemcpyAsync(dg, gate, wb, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(du, up, wb, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(dd, down, wb, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(dh, h, hidden * 4, hipMemcpyHostToDevice, st));
+    ANEDVD_HIP(hipMemcpyAsync(dout, out, hidden * 4, hipMemcpyHostToDevice, st));
+    ANEDVD_TRY(launch_expert_accum_ops(f16, dg, du, dd, dh, (int)inter, (int)hidden, weight, use_gelu != 0, dact, dout,
+                                       st));
+    ANEDVD_HIP(hipMemcpyAsync(out, dout, hidden * 4, hipMemcpyDeviceToHost, st));
+    ANEDVD_HIP(hipStreamSynchronize(st));
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_expert_accum_f32(anedvd_moe_ctx *ctx, float *out, const float *h, const float *gate, const float *up,
+                                const float *down, size_t inter, size_t hidden, float weight, int use_gelu)
+{
+    return expert_accum_ops(ctx, false, out, h, gate, up, down, inter, hidden, weight, use_gelu);
+}
+
+int anedvd_moe_expert_accum_f16(anedvd_moe_ctx *ctx, float *out, const float *h, const uint16_t *gate,
+                                const uint16_t *up, const uint16_t *down, size_t inter, size_t hidden, float weight,
+                                int use_gelu)
+{
+    return expert_accum_ops(ctx, true, out, h, gate, up, down, inter, hidden, weight, use_gelu);
+}
+
 int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h, float weight, float *out)
 {
     ANEDVD_TRY(check_layer(L));
@@ -748,8 +840,9 @@ int anedvd_moe_layer_route(anedvd_moe_layer *L, const float *h, size_t T, float 
 static int prepare(anedvd_moe_layer *L, size_t T, bool io, Fwd &f)
 {
     ANEDVD_TRY(check_layer(L));
-    if (T > (1u << 20)) {
-        set_error("forward: %zu tokens is more than this build handles per call", T);
+    if (T > max_tokens(L)) {
+        set_error("forward: %zu tokens is more than one call takes at this shape (%zu; "
+                  "anedvd_moe_layer_max_tokens): split the call", T, max_tokens(L));
         return ANEDVD_E_INVALID_ARG;
     }
     anedvd_moe_ctx *ctx = L->ctx;

@@ -61,7 +61,8 @@ class GgufMoeCfg(C.Structure):
         ("hidden", C.c_uint32), ("n_layers", C.c_uint32), ("n_experts", C.c_uint32), ("k", C.c_uint32),
         ("inter", C.c_uint32), ("shared_inter", C.c_uint32),
         ("gate_type", C.c_int32), ("up_type", C.c_int32), ("down_type", C.c_int32), ("router_type", C.c_int32),
-        ("shared_type", C.c_int32), ("has_shared_gate_lin", C.c_int32),
+        ("shared_type", C.c_int32), ("has_shared_gate_lin", C.c_int32), ("use_gelu", C.c_int32),
+        ("shared_as_f16", C.c_int32),
     ]
 
 
@@ -85,7 +86,11 @@ SIGNATURES = {
     "anedvd_moe_layer_free": (None, [_vp]),
     "anedvd_moe_layer_device_bytes": (C.c_uint64, [_vp]),
     "anedvd_dequantize_range": (_i, [_vp, _i, _vp, _sz, C.c_uint64, _vp, _sz]),
+    "anedvd_moe_layer_max_tokens": (_sz, [_vp]),
     "anedvd_moe_load_expert_f32": (_i, [_vp, _i, C.c_uint32, _vp, _sz]),
+    "anedvd_moe_load_expert_f16": (_i, [_vp, _i, C.c_uint32, _vp, _sz]),
+    "anedvd_moe_expert_accum_f32": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _i]),
+    "anedvd_moe_expert_accum_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _i]),
     "anedvd_matmul_f16": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz]),
     "anedvd_moe_route": (_i, [_vp, _vp, _sz, _sz, _sz, _i, _vp, _vp]),
     "anedvd_moe_dispatch": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp]),
@@ -190,6 +195,31 @@ class MoeContext:
             return probs[0], idx[0]
         return probs, idx
 
+    def moe_expert_accum_f32(self, out: np.ndarray, h: np.ndarray, gate: np.ndarray, up: np.ndarray,
+                             down: np.ndarray, inter: int, hidden: int, weight: float,
+                             use_gelu: bool = False) -> np.ndarray:
+        """cpu.moeExpertAccumF32 (cpu.zig:416-452): out[hidden] += weight * expert(h),
+        f32 weight slices gate/up [inter][hidden], down [hidden][inter]."""
+        assert out.dtype == np.float32 and out.flags.c_contiguous and out.size == hidden
+        g, u, d = (_c(a, np.float32) for a in (gate, up, down))
+        assert g.size == u.size == d.size == inter * hidden
+        hh = _c(h, np.float32)
+        _check(lib().anedvd_moe_expert_accum_f32(self.h, _p(out), _p(hh), _p(g), _p(u), _p(d), inter, hidden,
+                                                 weight, int(use_gelu)))
+        return out
+
+    def moe_expert_accum_f16(self, out: np.ndarray, h: np.ndarray, gate: np.ndarray, up: np.ndarray,
+                             down: np.ndarray, inter: int, hidden: int, weight: float,
+                             use_gelu: bool = False) -> np.ndarray:
+        """cpu.moeExpertAccum (cpu.zig:1141-1185): the same with f16 weight slices."""
+        assert out.dtype == np.float32 and out.flags.c_contiguous and out.size == hidden
+        g, u, d = (_c(a, np.float16) for a in (gate, up, down))
+        assert g.size == u.size == d.size == inter * hidden
+        hh = _c(h, np.float32)
+        _check(lib().anedvd_moe_expert_accum_f16(self.h, _p(out), _p(hh), _p(g), _p(u), _p(d), inter, hidden,
+                                                 weight, int(use_gelu)))
+        return out
+
     def dispatch(self, idx: np.ndarray, n_tokens: int, k: int, n_experts: int):
         i = _c(idx, np.uint32).reshape(-1)
         offsets = np.zeros(n_experts + 1, dtype=np.int32)
@@ -257,7 +287,7 @@ class MoeLayer:
 
         d = LayerDesc()
         d.hidden, d.inter, d.n_experts, d.k = spec.hidden, spec.inter, spec.n_experts, spec.k
-        d.norm_topk_prob, d.use_gelu = int(spec.norm_topk_prob), 0
+        d.norm_topk_prob, d.use_gelu = int(spec.norm_topk_prob), int(spec.use_gelu)
         d.gate_type, d.up_type, d.down_type = spec.gate_type, spec.up_type, spec.down_type
         d.gate, d.gate_bytes = ptr(arrays["gate"], np.uint8)
         d.up, d.up_bytes = ptr(arrays["up"], np.uint8)
@@ -280,7 +310,8 @@ class MoeLayer:
                   use_gelu: bool | None = None) -> "MoeLayer":
         """Block `layer` of a GGUF file (path, or the image's bytes) loaded the way
         loadMoeLayerStreaming does (load_gguf.zig:767-826); None keeps the
-        reference GGUF loader's value of an option (false)."""
+        reference GGUF loader's value of an option (norm_topk_prob false; use_gelu
+        true for the gemma architectures, load_gguf.zig:145-158)."""
         c = gguf_moe_config(src, layer)
         img = _gguf_image(src)
         opts = GgufMoeOpts(-1 if norm_topk_prob is None else int(norm_topk_prob),
@@ -292,8 +323,10 @@ class MoeLayer:
         self.spec = W.LayerSpec(f"{c['arch']} blk.{layer}", c["hidden"], c["inter"], c["n_experts"], c["k"],
                                 bool(norm_topk_prob), c["gate_type"], c["up_type"], c["down_type"],
                                 shared_inter=c["shared_inter"],
-                                shared_type=c["shared_type"] if c["shared_type"] >= 0 else W.Q8_0,
-                                shared_gated=bool(c["has_shared_gate_lin"]))
+                                shared_type=(W.F16 if c["shared_as_f16"] else c["shared_type"])
+                                if c["shared_type"] >= 0 else W.Q8_0,
+                                shared_gated=bool(c["has_shared_gate_lin"]),
+                                use_gelu=bool(c["use_gelu"] if use_gelu is None else use_gelu))
         self.h = h
         ctx._layers.add(self)
         return self
@@ -319,6 +352,17 @@ class MoeLayer:
         out = np.zeros(n, dtype=np.float32)
         _check(lib().anedvd_moe_load_expert_f32(self.h, which, expert, _p(out), n))
         return out
+
+    def load_expert_f16(self, which: int, expert: int) -> np.ndarray:
+        """readExpertF16 / loadExpert (gguf.zig:499-531): f16 values as np.float16."""
+        s = self.spec
+        n = s.inter * s.hidden
+        out = np.zeros(n, dtype=np.uint16)
+        _check(lib().anedvd_moe_load_expert_f16(self.h, which, expert, _p(out), n))
+        return out.view(np.float16)
+
+    def max_tokens(self) -> int:
+        return int(lib().anedvd_moe_layer_max_tokens(self.h))
 
     def expert_accum(self, out: np.ndarray, expert: int, h: np.ndarray, weight: float) -> np.ndarray:
         assert out.dtype == np.float32 and out.flags.c_contiguous

@@ -265,16 +265,38 @@ def zipf_logits(spec: W.LayerSpec, n_tokens: int, seed: int = 0, alpha: float = 
     return (z + bias[None, :]).astype(np.float32)
 
 
+def dequantize_host(t: int, payload: np.ndarray) -> np.ndarray:
+    """f32 values of F16, Q8_0 or Q4_0 blocks (gguf.zig:763-776, 827-840: every
+    product d * q is exact in f32), for writing test files."""
+    b = np.ascontiguousarray(payload, dtype=np.uint8)
+    if t == W.F16:
+        return b.view(np.float16).astype(np.float32)
+    if t == W.Q8_0:
+        blk = b.reshape(-1, 34)
+        d = blk[:, :2].copy().view(np.float16).astype(np.float32)
+        return (d * blk[:, 2:].view(np.int8).astype(np.float32)).reshape(-1)
+    if t == W.Q4_0:
+        blk = b.reshape(-1, 18)
+        d = blk[:, :2].copy().view(np.float16).astype(np.float32)
+        qs = blk[:, 2:]
+        q = np.concatenate([(qs & 15).astype(np.int32) - 8, (qs >> 4).astype(np.int32) - 8], axis=1)
+        return (d * q.astype(np.float32)).reshape(-1)
+    raise ValueError(f"dequantize_host: type {t} not handled")
+
+
 def moe_gguf(spec: W.LayerSpec, n_layers: int, seed: int = 0, arch: str = "qwen3moe", router_type: int = W.F32,
-             router_transposed: bool = False, extra_metadata: dict | None = None, drop: tuple = ()) -> tuple:
+             router_transposed: bool = False, extra_metadata: dict | None = None, drop: tuple = (),
+             shared_transposed: bool = False) -> tuple:
     """A GGUF image of `n_layers` MoE blocks of `spec` in llama.cpp's tensor naming
     (the names load_gguf.zig:767-826 reads): blk.N.ffn_gate_inp.weight {H, E}
     (`router_type` F32 or F16; {E, H} when `router_transposed`),
     blk.N.ffn_{gate,up}_exps.weight {H, I, E}, blk.N.ffn_down_exps.weight {I, H, E},
     and the shared expert's blk.N.ffn_{gate,up}_shexp {H, Is}, ffn_down_shexp {Is, H}
-    and ffn_gate_inp_shexp {H} (F32).  Block N holds make_layer(spec, seed, N).
-    `drop` lists metadata keys or tensor names left out.  Returns (image bytes,
-    [per-layer arrays])."""
+    and ffn_gate_inp_shexp {H} (F32).  With `shared_transposed` the shared expert's
+    three tensors are F16 stored the other way round ({Is, H}, {H, Is}: the
+    dequantised values rounded to f16 and transposed), which loadLinear also takes.
+    Block N holds make_layer(spec, seed, N).  `drop` lists metadata keys or tensor
+    names left out.  Returns (image bytes, [per-layer arrays])."""
     from . import gguf as G
     H, I, E, Is = spec.hidden, spec.inter, spec.n_experts, spec.shared_inter
     meta = {"general.architecture": arch, "general.alignment": 32, f"{arch}.block_count": n_layers,
@@ -301,9 +323,18 @@ def moe_gguf(spec: W.LayerSpec, n_layers: int, seed: int = 0, arch: str = "qwen3
         if Is:
             lin = L.get("shared_gate_lin")
             lin = np.zeros(H, np.float32) if lin is None else lin.astype(np.float32)
-            tensors += [(f"blk.{n}.ffn_gate_shexp.weight", (H, Is), spec.shared_type, L["shared_gate"].tobytes()),
-                        (f"blk.{n}.ffn_up_shexp.weight", (H, Is), spec.shared_type, L["shared_up"].tobytes()),
-                        (f"blk.{n}.ffn_down_shexp.weight", (Is, H), spec.shared_type, L["shared_down"].tobytes()),
-                        (f"blk.{n}.ffn_gate_inp_shexp.weight", (H,), W.F32, lin.tobytes())]
+            if shared_transposed:
+                def tr(nm, rows, cols):  # [rows][cols] values -> f16 stored [cols][rows], dims {rows, cols}
+                    v = dequantize_host(spec.shared_type, L[nm]).reshape(rows, cols)
+                    return np.ascontiguousarray(v.astype(np.float16).T).tobytes()
+                tensors += [(f"blk.{n}.ffn_gate_shexp.weight", (Is, H), W.F16, tr("shared_gate", Is, H)),
+                            (f"blk.{n}.ffn_up_shexp.weight", (Is, H), W.F16, tr("shared_up", Is, H)),
+                            (f"blk.{n}.ffn_down_shexp.weight", (H, Is), W.F16, tr("shared_down", H, Is))]
+            else:
+                tensors += [(f"blk.{n}.ffn_gate_shexp.weight", (H, Is), spec.shared_type, L["shared_gate"].tobytes()),
+                            (f"blk.{n}.ffn_up_shexp.weight", (H, Is), spec.shared_type, L["shared_up"].tobytes()),
+                            (f"blk.{n}.ffn_down_shexp.weight", (Is, H), spec.shared_type,
+                             L["shared_down"].tobytes())]
+            tensors += [(f"blk.{n}.ffn_gate_inp_shexp.weight", (H,), W.F32, lin.tobytes())]
     tensors = [t for t in tensors if t[0] not in drop]
     return G.write(meta, tensors), layers

@@ -47,6 +47,7 @@ class LayerSpec:
     shared_type: int = Q8_0
     shared_gated: bool = False
     rms_normalise_input: bool = False
+    use_gelu: bool = False  # geluTanh(gate) * up (cpu.zig:78-81, 434-437) instead of SiLU
     layers: int = 1
     tokens: tuple = field(default_factory=tuple)
 

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define ANEDVD_MOE_ABI_VERSION 1
+#define ANEDVD_MOE_ABI_VERSION 2
 
 /* ggml tensor type ids as stored in GGUF (gguf.zig:30-46). */
 enum anedvd_ggml_type {
@@ -66,7 +66,7 @@ typedef struct {
     uint32_t n_experts;       /* E */
     uint32_t k;               /* experts per token */
     int32_t norm_topk_prob;   /* renormalise the top-k weights (Config.norm_topk_prob) */
-    int32_t use_gelu;         /* gelu(gate)*up instead of silu(gate)*up; must be 0 for now */
+    int32_t use_gelu;         /* geluTanh(gate)*up instead of silu(gate)*up (cpu.zig:78-81, 434-437) */
     int32_t gate_type, up_type, down_type;
     const void *gate; size_t gate_bytes;   /* [E][I][H] */
     const void *up;   size_t up_bytes;     /* [E][I][H] */
@@ -107,6 +107,12 @@ int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *de
 void anedvd_moe_layer_free(anedvd_moe_layer *layer);
 /* Device bytes held by the layer's weights. */
 uint64_t anedvd_moe_layer_device_bytes(const anedvd_moe_layer *layer);
+/* The most tokens one forward call of this layer takes (the kernels address the
+ * per-call activations with 32-bit offsets: T*H*2, T*(k + merged shared pieces)*I*2
+ * and a separate shared expert's T*Is*2 bytes stay below 2^31).  Larger calls
+ * return ANEDVD_E_INVALID_ARG; the engine's prefill chunks (Options.chunk = 128,
+ * engine.zig:45) are far below it. */
+size_t anedvd_moe_layer_max_tokens(const anedvd_moe_layer *layer);
 
 /* ----------------------------------------------------- op-level mirrors of cpu.zig */
 
@@ -119,6 +125,12 @@ int anedvd_dequantize_range(anedvd_moe_ctx *ctx, int ggml_type, const void *src,
  * from the resident layer: which 0 = gate, 1 = up, 2 = down; `out` holds
  * rows*cols f32, bit-exact. */
 int anedvd_moe_load_expert_f32(anedvd_moe_layer *layer, int which, uint32_t expert, float *out, size_t n);
+
+/* Gguf.readExpertF16 / MoeWeights.loadExpert (gguf.zig:499-531, model.zig:486-511)
+ * from the resident layer: the expert dequantised and each value rounded to the
+ * nearest f16, ties to even (f32ToF16Slice, gguf.zig:682-692); `out` holds
+ * rows*cols f16 bits, bit-exact. */
+int anedvd_moe_load_expert_f16(anedvd_moe_layer *layer, int which, uint32_t expert, uint16_t *out, size_t n);
 
 /* cpu.matmulF16 (cpu.zig:461-475) over `n_vec` input vectors:
  * out[v][o] = sum_i f32(w[o][i]) * x[v][i], in the reference's 8-lane order,
@@ -137,8 +149,25 @@ int anedvd_moe_route(anedvd_moe_ctx *ctx, const float *logits, size_t n_tokens, 
 int anedvd_moe_dispatch(anedvd_moe_ctx *ctx, const uint32_t *idx, size_t n_tokens, size_t k,
                         size_t n_experts, int32_t *offsets, int32_t *rows, int32_t *slots);
 
-/* cpu.moeExpertAccumF32 (cpu.zig:416-452) for one token and one resident expert:
- * out[H] += weight * down(silu(gate h) * up h). */
+/* cpu.moeExpertAccumF32 (cpu.zig:416-452), the op-level drop-in: one token through
+ * one expert handed over as f32 weight slices (host memory; gate and up
+ * [inter][hidden], down [hidden][inter], as loadExpertF32 returns them):
+ * out[hidden] += weight * down . (act(gate . h) * (up . h)), act = silu, or
+ * geluTanh when use_gelu.  The reference's two scratch slices are the library's. */
+int anedvd_moe_expert_accum_f32(anedvd_moe_ctx *ctx, float *out, const float *h, const float *gate,
+                                const float *up, const float *down, size_t inter, size_t hidden,
+                                float weight, int use_gelu);
+
+/* cpu.moeExpertAccum (cpu.zig:1141-1185): the same with f16 weight slices (the
+ * eager loader's MoeWeights.expertGate/Up/Down, model.zig:549-561). */
+int anedvd_moe_expert_accum_f16(anedvd_moe_ctx *ctx, float *out, const float *h, const uint16_t *gate,
+                                const uint16_t *up, const uint16_t *down, size_t inter, size_t hidden,
+                                float weight, int use_gelu);
+
+/* The same product for a resident expert of a layer (the layer's fused-dequant
+ * kernels on a one-token dispatch; the streaming path's loadExpertF32 +
+ * moeExpertAccumF32, engine.zig:743-758, without the f32 copy):
+ * out[H] += weight * down(act(gate h) * up h). */
 int anedvd_moe_expert_accum(anedvd_moe_layer *layer, uint32_t expert, const float *h, float weight,
                             float *out);
 
@@ -156,12 +185,16 @@ typedef struct {
     uint32_t n_experts, k;       /* expert_count (blk.0.ffn_gate_exps wins), expert_used_count (2 if absent) */
     uint32_t inter;              /* routed expert width, from blk.0.ffn_gate_exps.weight or the metadata */
     uint32_t shared_inter;       /* 0 = no shared expert */
-    int32_t gate_type, up_type, down_type, router_type, shared_type;
+    int32_t gate_type, up_type, down_type, router_type, shared_type;  /* shared_type: of blk.N.ffn_gate_shexp */
     int32_t has_shared_gate_lin;
+    int32_t use_gelu;            /* gelu(gate)*up: the gemma architectures (load_gguf.zig:145-158) */
+    int32_t shared_as_f16;       /* the shared expert is read as f16 [out][in] (loadLinear, load_gguf.zig:358-386):
+                                    a tensor stored {out, in}, three different types, or a type the
+                                    expert kernels do not take; else its payloads are used as stored */
 } anedvd_gguf_moe_cfg;
 
 /* Options of anedvd_moe_layer_create_gguf; NULL or -1 fields = the reference GGUF
- * loader's values (norm_topk_prob false, use_gelu false). */
+ * loader's values (norm_topk_prob false; use_gelu true for gemma* architectures). */
 typedef struct {
     int32_t norm_topk_prob;
     int32_t use_gelu;
@@ -176,7 +209,8 @@ int anedvd_gguf_moe_info(const void *gguf, size_t len, uint32_t layer, anedvd_gg
  * GGUF image (the caller maps the file; it may be unmapped on return).  The expert
  * payloads are uploaded as stored; the router and the shared gate vector are read
  * as f16 (any type, dequantised bit-exactly, rounded to nearest even); the shared
- * expert's three tensors must share one type the expert kernels take. */
+ * expert's tensors are uploaded as stored when they are {in, out} of one type the
+ * expert kernels take, else read as f16 [out][in] as loadLinear does. */
 int anedvd_moe_layer_create_gguf(anedvd_moe_ctx *ctx, const void *gguf, size_t len, uint32_t layer,
                                  const anedvd_gguf_moe_opts *opts, anedvd_moe_layer **out);
 

@@ -19,6 +19,12 @@
  *   moe_route         reference KAT (cpu.zig:1290-1336) and brute-force sort;
  *   expert_accum      reference hand-computed KAT (cpu.zig:1338-1388), f64 brute force;
  *   mlp / sigmoid     sigmoid KAT (cpu.zig:1390-1400), f64 brute force;
+ *   gelu_tanh         reference KAT (cpu.zig:1434-1449), closed forms (gelu(0) = 0,
+ *                     saturation, odd symmetry), f64 formula over a sweep;
+ *   f32_to_f16        numpy's round-to-nearest-even conversion over every f16
+ *                     value, the midpoints between them and random f32 values;
+ *   read_expert_f16   equals f32_to_f16 of read_expert_f32 (chunking cannot change
+ *                     a whole-block dequantisation);
  *   dispatch          brute-force stable sort by expert;
  *   layer forward     f64 composition, and per-token streaming == by-expert order.
  */
@@ -69,6 +75,7 @@ static inline uint32_t rd32(const uint8_t *b, size_t off)
     return (uint32_t)b[off] | ((uint32_t)b[off + 1] << 8) | ((uint32_t)b[off + 2] << 16) | ((uint32_t)b[off + 3] << 24);
 }
 static inline float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 
 /* IEEE binary16 -> binary32, exact for every input (gguf.zig:743-746). */
 float or_f16_to_f32(uint16_t h)
@@ -392,6 +399,61 @@ int or_read_expert_f32(int t, const uint8_t *payload, size_t payload_len, uint32
     uint64_t start = (uint64_t)expert * per_bytes, end = start + per_bytes;
     if (end > payload_len) return OR_ERR_OUT_OF_RANGE;
     return or_dequantize_range(t, payload + start, (size_t)per_bytes, 0, out, per_expert);
+}
+
+/* IEEE binary32 -> binary16, round to nearest, ties to even, overflow to infinity
+ * (the conversion Zig's @floatCast does for f32ToF16Slice, gguf.zig:682-692).
+ * With E the value's unbiased exponent, the f16 grid step is 2^(E-10) for a
+ * normal result and 2^-24 below 2^-14; the 24-bit significand is divided by the
+ * step (a right shift) and rounded on the bits shifted out.  A significand that
+ * rounds up to 2048 carries into the exponent by the addition. */
+uint16_t or_f32_to_f16(float f)
+{
+    const uint32_t x = f32_bits(f), sign = (x >> 16) & 0x8000u, e = (x >> 23) & 0xffu, m = x & 0x7fffffu;
+    if (e == 0xff) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u | (m >> 13) : 0u));
+    if (e == 0) return (uint16_t)sign; /* |f| < 2^-126: below half the smallest f16 subnormal */
+    const int E = (int)e - 127;
+    if (E > 15) return (uint16_t)(sign | 0x7c00u);
+    const uint32_t mant = m | 0x800000u;
+    const int shift = E < -14 ? 126 - (int)e : 13;
+    uint32_t q = 0;
+    if (shift < 32) {
+        q = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+    }
+    const uint32_t bits = E < -14 ? q : ((uint32_t)(E + 14) << 10) + q;
+    return (uint16_t)(sign | (bits > 0x7c00u ? 0x7c00u : bits));
+}
+
+void or_f32_to_f16_slice(const float *src, uint16_t *dst, size_t n)
+{
+    for (size_t i = 0; i < n; i++) dst[i] = or_f32_to_f16(src[i]);
+}
+
+/* Gguf.readExpertF16, gguf.zig:499-531: the checks of readExpertF32, then the
+ * expert dequantised 2048 elements at a time and each chunk rounded to f16. */
+int or_read_expert_f16(int t, const uint8_t *payload, size_t payload_len, uint32_t expert,
+                       uint32_t n_experts, uint16_t *out, size_t per_expert)
+{
+    size_t epb = or_block_elems(t), bpb = or_block_bytes(t);
+    if (!epb || !bpb) return OR_ERR_UNSUPPORTED_TYPE;
+    if (payload_len % bpb) return OR_ERR_INVALID_SHAPE;
+    uint64_t elems = (uint64_t)(payload_len / bpb) * epb;
+    if (elems != (uint64_t)per_expert * n_experts) return OR_ERR_DIMENSION;
+    if (per_expert % epb) return OR_ERR_INVALID_SHAPE;
+    uint64_t per_bytes = (uint64_t)(per_expert / epb) * bpb;
+    uint64_t start = (uint64_t)expert * per_bytes, end = start + per_bytes;
+    if (end > payload_len) return OR_ERR_OUT_OF_RANGE;
+    float buf[2048];
+    for (size_t done = 0; done < per_expert;) {
+        size_t m = per_expert - done < 2048 ? per_expert - done : 2048;
+        int rc = or_dequantize_range(t, payload + start, (size_t)per_bytes, done, buf, m);
+        if (rc) return rc;
+        or_f32_to_f16_slice(buf, out + done, m);
+        done += m;
+    }
+    return OR_OK;
 }
 
 /* ------------------------------------------------------------------- matmuls */

@@ -53,6 +53,14 @@ int or_dequantize_range(int ggml_type, const uint8_t *src, size_t src_len,
 int or_read_expert_f32(int ggml_type, const uint8_t *payload, size_t payload_len,
                        uint32_t expert, uint32_t n_experts, float *out, size_t per_expert);
 
+/* f32 -> f16 bits, round to nearest even (f32ToF16Slice, gguf.zig:682-692). */
+uint16_t or_f32_to_f16(float f);
+void or_f32_to_f16_slice(const float *src, uint16_t *dst, size_t n);
+/* Gguf.readExpertF16 (gguf.zig:499-531): readExpertF32 in 2048-element chunks,
+ * each rounded to f16. */
+int or_read_expert_f16(int ggml_type, const uint8_t *payload, size_t payload_len,
+                       uint32_t expert, uint32_t n_experts, uint16_t *out, size_t per_expert);
+
 /* cpu.matmulF16 (cpu.zig:461-475): 8 lane accumulators, ordered lane sum. */
 void or_matmul_f16(float *out, const uint16_t *w, const float *x, size_t out_dim, size_t in_dim);
 /* main.zig:320-326: the scalar sequential matmul refForward uses. */

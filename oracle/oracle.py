@@ -47,6 +47,10 @@ def lib():
         L.or_dequantize_range.argtypes = [C.c_int, C.c_void_p, _sz, C.c_uint64, _f32p, _sz]
         L.or_read_expert_f32.restype = C.c_int
         L.or_read_expert_f32.argtypes = [C.c_int, C.c_void_p, _sz, C.c_uint32, C.c_uint32, _f32p, _sz]
+        L.or_read_expert_f16.restype = C.c_int
+        L.or_read_expert_f16.argtypes = [C.c_int, C.c_void_p, _sz, C.c_uint32, C.c_uint32, _u16p, _sz]
+        L.or_f32_to_f16_slice.restype = None
+        L.or_f32_to_f16_slice.argtypes = [_f32p, _u16p, _sz]
         for name in ("or_matmul_f16", "or_matmul_f16_scalar"):
             getattr(L, name).restype = None
             getattr(L, name).argtypes = [_f32p, _u16p, _f32p, _sz, _sz]
@@ -109,6 +113,22 @@ def read_expert_f32(t: int, payload, expert: int, n_experts: int, per_expert: in
     return rc, out
 
 
+def read_expert_f16(t: int, payload, expert: int, n_experts: int, per_expert: int):
+    """Gguf.readExpertF16: returns (status, f16 bits as uint16)."""
+    a, p, nb = _bytes_arg(payload)
+    out = np.zeros(per_expert, dtype=np.uint16)
+    rc = lib().or_read_expert_f16(t, p, nb, expert, n_experts, out, per_expert)
+    return rc, out
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    """f32ToF16Slice: f16 bits (uint16) of each value, round to nearest even."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.zeros(x.size, dtype=np.uint16)
+    lib().or_f32_to_f16_slice(x, out, x.size)
+    return out
+
+
 def matmul_f16(w_f16: np.ndarray, x: np.ndarray, scalar: bool = False) -> np.ndarray:
     w = np.ascontiguousarray(w_f16, dtype=np.float16).view(np.uint16)
     x = np.ascontiguousarray(x, dtype=np.float32)
@@ -163,6 +183,10 @@ def sigmoid(x: float) -> float:
     return lib().or_sigmoid(x)
 
 
+def gelu_tanh(x: float) -> float:
+    return lib().or_gelu_tanh(x)
+
+
 def expf(x: float) -> float:
     return lib().or_expf(x)
 
@@ -201,7 +225,7 @@ class OracleLayer:
         keep = lambda a: (self._keep.append(a), a.ctypes.data_as(C.c_void_p))[1]
         s = _OrLayer()
         s.hidden, s.inter, s.n_experts, s.k = spec.hidden, spec.inter, spec.n_experts, spec.k
-        s.norm_topk_prob, s.use_gelu = int(spec.norm_topk_prob), 0
+        s.norm_topk_prob, s.use_gelu = int(spec.norm_topk_prob), int(spec.use_gelu)
         s.gate_type, s.up_type, s.down_type = spec.gate_type, spec.up_type, spec.down_type
         for nm in ("gate", "up", "down"):
             a = np.ascontiguousarray(arrays[nm], dtype=np.uint8)

@@ -8,6 +8,7 @@ import dataclasses
 import os
 import struct
 
+import numpy as np
 import pytest
 
 from anedvd_amd import gguf as G
@@ -150,3 +151,50 @@ def test_router_in_either_orientation_passes_the_shape_check():
     img, _ = synth.moe_gguf(TINY, 1, router_transposed=True, router_type=W.F16)
     c = moe.gguf_moe_config(img)
     assert c["router_type"] == W.F16
+
+
+def test_gemma_architecture_sets_use_gelu():
+    """load_gguf.zig:145-158: every gemma* architecture runs geluTanh(gate) * up;
+    the others keep SiLU (load_gguf.zig:1093, 1132)."""
+    for arch, want in (("gemma2", 1), ("gemma3", 1), ("qwen3moe", 0), ("mixtral", 0), ("deepseek2", 0)):
+        img, _ = synth.moe_gguf(TINY, 1, arch=arch)
+        assert moe.gguf_moe_config(img)["use_gelu"] == want, arch
+
+
+def test_shared_expert_as_stored_keeps_its_payloads():
+    img, _ = synth.moe_gguf(SHARED, 1)
+    c = moe.gguf_moe_config(img)
+    assert c["shared_type"] == W.Q8_0 and c["shared_as_f16"] == 0
+
+
+def test_transposed_shared_expert_is_read_as_f16():
+    """loadLinear (load_gguf.zig:374-384) takes a shared-expert tensor stored
+    {out, in} too and transposes it; the loader then holds the shared expert as
+    f16 [out][in], as the reference does."""
+    img, _ = synth.moe_gguf(SHARED, 1, shared_transposed=True)
+    c = moe.gguf_moe_config(img)
+    assert c["shared_inter"] == 512 and c["shared_type"] == W.F16 and c["shared_as_f16"] == 1
+
+
+def test_shared_expert_of_mixed_types_is_read_as_f16():
+    img, _ = synth.moe_gguf(SHARED, 1)
+    g = G.Gguf.from_bytes(img)
+    tensors = []
+    for t in g.order:
+        b = bytes(g.tensor_bytes(t))
+        if t.name.endswith("ffn_up_shexp.weight"):  # up as F16 of the same values
+            tensors.append((t.name, t.dims, W.F16, synth.dequantize_host(W.Q8_0, np.frombuffer(b, np.uint8))
+                            .astype(np.float16).tobytes()))
+        else:
+            tensors.append((t.name, t.dims, t.ttype, b))
+    c = moe.gguf_moe_config(G.write(dict(g.kv), tensors))
+    assert c["shared_as_f16"] == 1
+
+
+def test_shared_expert_of_wrong_size_is_dimension_mismatch():
+    img, _ = synth.moe_gguf(SHARED, 1)
+    g = G.Gguf.from_bytes(img)
+    tensors = [(t.name, (256, 256) if t.name.endswith("ffn_gate_shexp.weight") else t.dims, t.ttype,
+                bytes(g.tensor_bytes(t))[:256 * 256 // 32 * 34] if t.name.endswith("ffn_gate_shexp.weight")
+                else bytes(g.tensor_bytes(t))) for t in g.order]
+    assert status_of(G.write(dict(g.kv), tensors)) == "DimensionMismatch"

@@ -270,6 +270,48 @@ def test_sigmoid_reference_kat():
     assert 0.0 <= O.sigmoid(-1000.0) < 1e-30
 
 
+def test_gelu_tanh_reference_kat():
+    """cpu.zig:1434-1449: the six reference values within 1e-6, and gelu is not SiLU
+    at -3 (they differ by more than 0.13)."""
+    for x, want in ((0.0, 0.0), (1.0, 0.84119199), (-1.0, -0.15880796), (3.0, 2.99636241), (-3.0, -0.00363739),
+                    (0.5, 0.34571400)):
+        assert abs(O.gelu_tanh(x) - want) <= 1e-6, x
+    assert abs(O.gelu_tanh(-3.0) - (-3.0 / (1.0 + np.exp(3.0)))) > 0.13
+
+
+def test_gelu_tanh_closed_forms():
+    """What the formula 0.5 x (1 + tanh(c (x + 0.044715 x^3))) fixes: gelu(0) = 0;
+    tanh saturates, so gelu(x) = x exactly for large x and -0 for very negative x;
+    tanh is odd, so gelu(x) - gelu(-x) = x; and the f64 formula within 1e-6 over a
+    sweep (a wrong constant, sign or factor fails one of them)."""
+    assert O.gelu_tanh(0.0) == 0.0
+    for x in (10.0, 20.0, 1e3):
+        assert O.gelu_tanh(x) == x
+    for x in (-10.0, -20.0, -1e3):
+        assert O.gelu_tanh(x) == 0.0
+    xs = np.linspace(-8.0, 8.0, 4001).astype(np.float32)
+    got = np.array([O.gelu_tanh(float(x)) for x in xs], dtype=np.float64)
+    x64 = xs.astype(np.float64)
+    want = 0.5 * x64 * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x64 + 0.044715 * x64 ** 3)))
+    assert np.abs(got - want).max() <= 1e-6 * np.maximum(1.0, np.abs(want)).max()
+    odd = np.array([O.gelu_tanh(float(x)) - O.gelu_tanh(float(-x)) for x in xs[::40]])
+    assert np.abs(odd - xs[::40]).max() <= 2e-6 * np.abs(xs).max()
+
+
+def test_layer_forward_gelu_against_f64():
+    """use_gelu runs geluTanh(gate) * up in every expert (cpu.zig:434-437) and in the
+    shared expert (cpu.zig:1207): the layer against an f64 composition."""
+    import dataclasses
+    spec = dataclasses.replace(W.TINY_Q8_0, use_gelu=True)
+    L = synth.make_layer(spec, seed=3)
+    h = synth.activations(spec, 6, seed=3)
+    got = O.OracleLayer(spec, L).forward(h)
+    ref = _layer_f64(spec, L, h, gelu=True)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-6
+    silu = O.OracleLayer(dataclasses.replace(spec, use_gelu=False), L).forward(h)
+    assert np.linalg.norm(silu - ref) / np.linalg.norm(ref) > 1e-2
+
+
 @pytest.mark.parametrize("T,E,k", [(1, 8, 2), (16, 8, 2), (64, 128, 8), (37, 64, 6)])
 def test_dispatch_is_stable_sort_by_expert(T, E, k):
     rng = np.random.default_rng(T * 100 + E)
@@ -296,7 +338,45 @@ def test_read_expert_slices_whole_tensor():
         assert O.read_expert_f32(t, payload, 0, E, per + W.BLOCK[t][0])[0] == O.ERR_DIMENSION
 
 
-def _layer_f64(spec, L, h, logits=None):
+def test_f32_to_f16_round_to_nearest_even():
+    """f32ToF16Slice (gguf.zig:682-692) against numpy's IEEE conversion, bit for
+    bit: every finite f16 value, the midpoint between each pair of neighbours (the
+    ties: even wins), values just off the midpoints, the subnormal range, the
+    overflow edge (65504 stays, 65520 becomes inf) and random f32 bit patterns."""
+    allh = np.arange(0x10000, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    fin = allh[np.isfinite(allh)].astype(np.float32)
+    pos = np.unique(np.abs(fin))
+    mid = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)  # exact in f32
+    near = np.concatenate([np.nextafter(mid, np.float32(np.inf)), np.nextafter(mid, np.float32(0))])
+    rng = np.random.default_rng(0)
+    rnd = rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    rnd = rnd[np.isfinite(rnd)]
+    edge = np.array([65504.0, 65519.99, 65520.0, 1e9, -1e9, 2.0 ** -25, 2.0 ** -24, 3 * 2.0 ** -26, 2.0 ** -26,
+                     1e-30, -0.0, 0.0, np.inf, -np.inf], dtype=np.float32)
+    for x in (fin, mid, -mid, near, rnd, edge):
+        with np.errstate(over="ignore"):
+            want = x.astype(np.float16).view(np.uint16)
+        assert np.array_equal(O.f32_to_f16(x), want)
+    nan = O.f32_to_f16(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7C00) == 0x7C00 and (nan & 0x3FF) != 0
+
+
+def test_read_expert_f16_is_dequant_then_round():
+    """readExpertF16 (gguf.zig:499-531) in 2048-element chunks equals the whole
+    expert dequantised and rounded, with readExpertF32's checks."""
+    E, per = 3, 256 * 24
+    for t in (W.Q8_0, W.Q4_0, W.Q4_K, W.Q6_K, W.Q5_K):
+        payload = synth.quant_matrix(t, 13, 2, E * per, 0.3)
+        for e in range(E):
+            rc, f32 = O.read_expert_f32(t, payload, e, E, per)
+            rc16, f16 = O.read_expert_f16(t, payload, e, E, per)
+            assert rc == rc16 == O.OK
+            assert np.array_equal(f16, f32.astype(np.float16).view(np.uint16))
+        assert O.read_expert_f16(t, payload, E, E, per)[0] == O.ERR_RANGE
+        assert O.read_expert_f16(t, payload, 0, E, per + W.BLOCK[t][0])[0] == O.ERR_DIMENSION
+
+
+def _layer_f64(spec, L, h, logits=None, gelu=False):
     """f64 composition of the block (main.zig:488-520) from the oracle's routing."""
     ol = O.OracleLayer(spec, L)
     _, probs, idx = ol.route(h, h.shape[0], logits)
@@ -313,7 +393,11 @@ def _layer_f64(spec, L, h, logits=None):
             x = h[t].astype(np.float64)
             g = g_w.reshape(I, H) @ x
             u = u_w.reshape(I, H) @ x
-            out[t] += probs[t, s] * (d_w.reshape(H, I) @ (g / (1 + np.exp(-g)) * u))
+            if gelu:
+                act = 0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g + 0.044715 * g ** 3)))
+            else:
+                act = g / (1 + np.exp(-g))
+            out[t] += probs[t, s] * (d_w.reshape(H, I) @ (act * u))
     return out
 
 
