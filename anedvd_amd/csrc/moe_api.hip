@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -60,7 +61,48 @@ struct anedvd_moe_layer {
     double expert_bytes = 0, shared_bytes = 0;
 };
 
+// ------------------------------------------------- the no-allocation forward
+//
+// anedvd_moe_layer_forward_device_noalloc carves its per-call scratch (routing,
+// dispatch, f16 activations, partial sums: fwd_layout) from this file-scope device
+// array instead of the context's growable workspace.  Every GPU the library runs
+// on holds its own copy, at its own address, until the process ends.  In host code
+// `scratch` names a host-side stand-in, not device memory: host code uses only the
+// address hipGetSymbolAddress returns, looked up once per device (with that device
+// current) when a context opens it, and kept in g_scratch.  Nothing in it needs to
+// start at zero: every call writes each scratch word it later reads.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static std::mutex g_scratch_mu;
+static void *g_scratch[kMaxDevices];
+
 namespace {
+
+// Looks up this device's copy of `scratch` (the device is current).
+int scratch_setup(int device)
+{
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= kMaxDevices) {
+        set_error("no-allocation scratch: device %d is beyond the %d this build tracks", device, kMaxDevices);
+        return ANEDVD_E_NO_DEVICE;
+    }
+    if (g_scratch[device]) return ANEDVD_OK;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        set_error("hipGetSymbolAddress(scratch) on device %d failed: %s", device, hipGetErrorString(e));
+        return ANEDVD_E_HIP;
+    }
+    g_scratch[device] = p;
+    return ANEDVD_OK;
+}
+
+void *scratch_of(int device)
+{
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return device >= 0 && device < kMaxDevices ? g_scratch[device] : nullptr;
+}
 
 struct Carve {
     uint8_t *p;
@@ -372,6 +414,7 @@ int anedvd_moe_open(int device, anedvd_moe_ctx **out)
         return ANEDVD_E_NO_DEVICE;
     }
     ANEDVD_HIP(hipSetDevice(device));
+    ANEDVD_TRY(scratch_setup(device));  // this device's no-allocation scratch, once per device
     anedvd_moe_ctx *c = new anedvd_moe_ctx();
     c->device = device;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
@@ -837,7 +880,9 @@ int anedvd_moe_layer_route(anedvd_moe_layer *L, const float *h, size_t T, float 
     return ANEDVD_OK;
 }
 
-static int prepare(anedvd_moe_layer *L, size_t T, bool io, Fwd &f)
+// The checks every forward entry point makes before it touches memory; makes the
+// layer's device current.
+static int check_forward(anedvd_moe_layer *L, size_t T)
 {
     ANEDVD_TRY(check_layer(L));
     if (T > max_tokens(L)) {
@@ -845,14 +890,20 @@ static int prepare(anedvd_moe_layer *L, size_t T, bool io, Fwd &f)
                   "anedvd_moe_layer_max_tokens): split the call", T, max_tokens(L));
         return ANEDVD_E_INVALID_ARG;
     }
-    anedvd_moe_ctx *ctx = L->ctx;
-    ANEDVD_HIP(hipSetDevice(ctx->device));
+    ANEDVD_HIP(hipSetDevice(L->ctx->device));
     if (!mm_supported(L->gate.type) || !mm_supported(L->down.type) || L->gate.type != L->up.type ||
         (L->Is && !L->n_sh && (!mm_supported(L->sgate.type) || !mm_supported(L->sdown.type)))) {
         set_error("forward: no expert kernel for ggml types gate=%d up=%d down=%d", L->gate.type, L->up.type,
                   L->down.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
+    return ANEDVD_OK;
+}
+
+static int prepare(anedvd_moe_layer *L, size_t T, bool io, Fwd &f)
+{
+    ANEDVD_TRY(check_forward(L, T));
+    anedvd_moe_ctx *ctx = L->ctx;
     const int ks = (int)(L->k + L->n_sh);
     const size_t bytes = fwd_layout(L, (int)T, ks, nullptr, (uint8_t *)0, io);
     ANEDVD_TRY(ensure(ctx->ws, bytes + 4096, ctx->stream));
@@ -898,6 +949,38 @@ int anedvd_moe_layer_forward_device(anedvd_moe_layer *L, const float *d_h, size_
     Fwd f;
     ANEDVD_TRY(prepare(L, T, false, f));
     if (!T) return ANEDVD_OK;
+    return forward_device(L, d_h, (int)T, d_logits, d_out, f, L->ctx->stream, nullptr);
+}
+
+int anedvd_moe_layer_forward_device_noalloc(anedvd_moe_layer *L, const float *d_h, size_t T, const float *d_logits,
+                                            float *d_out)
+{
+    if (!d_h || !d_out) {
+        set_error("layer_forward_device_noalloc: null pointer");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    ANEDVD_TRY(check_forward(L, T));
+    if (!T) return ANEDVD_OK;
+    const int ks = (int)(L->k + L->n_sh);
+    const size_t need = fwd_layout(L, (int)T, ks, nullptr, (uint8_t *)0, false);
+    if (need > kNoAllocScratchBytes) {
+        size_t lo = 0, hi = T;  // the largest call that fits, for the message
+        while (hi - lo > 1) {
+            const size_t mid = (lo + hi) / 2;
+            (fwd_layout(L, (int)mid, ks, nullptr, (uint8_t *)0, false) <= kNoAllocScratchBytes ? lo : hi) = mid;
+        }
+        set_error("layer_forward_device_noalloc: %zu tokens need %zu bytes of scratch, more than its %zu; "
+                  "at most %zu tokens per call at this shape",
+                  T, need, kNoAllocScratchBytes, lo);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    uint8_t *base = (uint8_t *)scratch_of(L->ctx->device);
+    if (!base) {
+        set_error("layer_forward_device_noalloc: no scratch for device %d", L->ctx->device);
+        return ANEDVD_E_NO_DEVICE;
+    }
+    Fwd f;
+    fwd_layout(L, (int)T, ks, &f, base, false);
     return forward_device(L, d_h, (int)T, d_logits, d_out, f, L->ctx->stream, nullptr);
 }
 

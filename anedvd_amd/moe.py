@@ -98,6 +98,7 @@ SIGNATURES = {
     "anedvd_moe_layer_route": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
     "anedvd_moe_layer_forward": (_i, [_vp, _vp, _sz, _vp, _vp, C.POINTER(Stats)]),
     "anedvd_moe_layer_forward_device": (_i, [_vp, _vp, _sz, _vp, _vp]),
+    "anedvd_moe_layer_forward_device_noalloc": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "anedvd_moe_device_alloc": (_i, [_vp, _sz, C.POINTER(_vp)]),
     "anedvd_moe_device_free": (_i, [_vp, _vp]),
     "anedvd_moe_memcpy_h2d": (_i, [_vp, _vp, _vp, _sz]),
@@ -397,6 +398,10 @@ class MoeLayer:
 
     def forward_device(self, d_h: int, n_tokens: int, d_logits: int | None, d_out: int):
         _check(lib().anedvd_moe_layer_forward_device(self.h, d_h, n_tokens, d_logits, d_out))
+
+    def forward_device_noalloc(self, d_h: int, n_tokens: int, d_logits: int | None, d_out: int):
+        """forward_device on the library's static per-GPU scratch: no allocation."""
+        _check(lib().anedvd_moe_layer_forward_device_noalloc(self.h, d_h, n_tokens, d_logits, d_out))
 
 
 TIME_GRAPH = 1

@@ -234,6 +234,19 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *layer, const float *h, size_t n_t
 int anedvd_moe_layer_forward_device(anedvd_moe_layer *layer, const float *d_h, size_t n_tokens,
                                     const float *d_logits, float *d_out);
 
+/* anedvd_moe_layer_forward_device without any allocation.  It has no counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * per-call scratch comes from a static 64 MiB device array, one per GPU, held
+ * until the process ends, instead of the context's workspace; no hipMalloc,
+ * hipFree or allocating routine is called.  Calls whose scratch exceeds 64 MiB
+ * return ANEDVD_E_INVALID_ARG, naming the most tokens that fit (Qwen3-30B-A3B
+ * shape: 807 tokens; decode batches of 1-64 take under 6 MiB).  Every call
+ * on one GPU shares that GPU's array: calls that overlap in time on one GPU (two
+ * contexts' streams, or two threads) race and must be serialised by the caller. */
+int anedvd_moe_layer_forward_device_noalloc(anedvd_moe_layer *layer, const float *d_h, size_t n_tokens,
+                                            const float *d_logits, float *d_out);
+
 /* ------------------------------------------------- device memory and timing */
 
 int anedvd_moe_device_alloc(anedvd_moe_ctx *ctx, size_t bytes, void **d_ptr);

@@ -1,0 +1,67 @@
+"""The no-allocation forward (anedvd_moe_layer_forward_device_noalloc) computes
+what anedvd_moe_layer_forward_device computes, bit for bit, through the C ABI:
+two calls in a row on each layer, the second smaller than the first (the static
+scratch keeps the first call's contents), on the decode kernels, the grouped
+GEMM and a separately run shared expert; and a call whose scratch exceeds the
+array is refused."""
+import dataclasses
+import re
+
+import numpy as np
+import pytest
+
+from anedvd_amd import moe, synth
+from anedvd_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = moe.MoeContext(0)
+    yield c
+    c.close()
+
+
+def run(ctx, layer, spec, T, seed, noalloc):
+    h = synth.activations(spec, T, seed=seed)
+    lg = synth.uniform_logits(spec, T, seed=seed)
+    d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lg), ctx.alloc(T * spec.hidden * 4)
+    (layer.forward_device_noalloc if noalloc else layer.forward_device)(d_h, T, d_lg, d_out)
+    out = ctx.from_device(d_out, (T, spec.hidden), np.float32)
+    for p in (d_h, d_lg, d_out):
+        ctx.free(p)
+    return out
+
+
+SPECS = [
+    (W.QWEN3_30B_A3B_Q8_0, (64, 8)),
+    (W.QWEN3_30B_A3B_Q4_K_M, (512, 64)),
+    (dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="separate-shared", hidden=512, inter=512, n_experts=8, k=2,
+                         shared_inter=1024, shared_type=W.Q4_0, shared_gated=True), (300, 16)),
+]
+
+
+@pytest.mark.parametrize("spec,sizes", SPECS, ids=lambda x: x.name.split()[0] if hasattr(x, "name") else str(x))
+def test_noalloc_forward_matches_forward_device(ctx, spec, sizes):
+    layer = moe.MoeLayer(ctx, spec, synth.make_layer(spec, seed=3))
+    for i, T in enumerate(sizes):
+        want = run(ctx, layer, spec, T, 30 + i, noalloc=False)
+        got = run(ctx, layer, spec, T, 30 + i, noalloc=True)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (spec.name, T)
+    layer.free()
+
+
+def test_noalloc_refuses_calls_beyond_its_scratch(ctx):
+    spec = W.QWEN3_30B_A3B_Q8_0
+    layer = moe.MoeLayer(ctx, spec, synth.make_layer(spec, seed=3))
+    T = 4096
+    d_h = ctx.alloc(T * spec.hidden * 4)
+    with pytest.raises(moe.MoeError) as ei:
+        layer.forward_device_noalloc(d_h, T, None, d_h)
+    assert ei.value.name == "InvalidArgument"
+    most = int(re.search(r"at most (\d+) tokens", str(ei.value)).group(1))
+    print(f"\nno-allocation forward: at most {most} tokens per call at the Qwen3-30B-A3B shape")
+    assert 64 <= most < T
+    ctx.free(d_h)
+    layer.free()
