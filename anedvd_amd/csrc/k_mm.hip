@@ -776,7 +776,7 @@ constexpr int kMaxKS = 16;      // K partials the combine reads per position
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart, const int32_t *__restrict__ inv,
                                                  const float *__restrict__ probs, int T, int k, int H, int KS, int P,
                                                  const float *__restrict__ shared, const float *__restrict__ shared_scale,
-                                                 int sKS, float *__restrict__ out)
+                                                 int sKS, const float *resid, float *out)
 {
     __shared__ float4 part[kCombLanes + 1][kCombCols];  // slot-lane sums, then the shared term
     const int c = threadIdx.x % kCombCols, l = threadIdx.x / kCombCols;
@@ -826,6 +826,10 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart
                 const float4 v = part[i][c];
                 r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
             }
+            if (resid) {  // x += proj (main.zig:519): the residual plus the whole block output
+                const float4 x = *(const float4 *)(resid + (size_t)t * H + h);
+                r = make_float4(x.x + r.x, x.y + r.y, x.z + r.z, x.w + r.w);
+            }
             *(float4 *)(out + (size_t)t * H + h) = r;
         }
         __syncthreads();
@@ -839,7 +843,7 @@ __global__ __launch_bounds__(256) void k_combine_rows(const float *__restrict__ 
                                                       const float *__restrict__ probs, int T, int k, int H, int KS,
                                                       int P, const float *__restrict__ shared,
                                                       const float *__restrict__ shared_scale, int sKS,
-                                                      float *__restrict__ out)
+                                                      const float *resid, float *out)
 {
     const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int H4 = H / 4;
@@ -881,6 +885,10 @@ __global__ __launch_bounds__(256) void k_combine_rows(const float *__restrict__ 
             y.x += z.x; y.y += z.y; y.z += z.z; y.w += z.w;
         }
         acc.x += sc * y.x; acc.y += sc * y.y; acc.z += sc * y.z; acc.w += sc * y.w;
+    }
+    if (resid) {
+        const float4 x = *(const float4 *)(resid + (size_t)t * H + h);
+        acc = make_float4(x.x + acc.x, x.y + acc.y, x.z + acc.z, x.w + acc.w);
     }
     *(float4 *)(out + (size_t)t * H + h) = acc;
 }
@@ -1050,7 +1058,8 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
 }
 
 int launch_combine(const float *ypart, const int32_t *inv, const float *probs, int T, int k, int H, int KS, int P,
-                   const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st)
+                   const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st,
+                   const float *resid)
 {
     if (T <= 0) return ANEDVD_OK;
     if (KS > kMaxKS || sKS > kMaxKS) {
@@ -1060,11 +1069,11 @@ int launch_combine(const float *ypart, const int32_t *inv, const float *probs, i
     const size_t threads = (size_t)T * (H / 4);
     if (threads >= 65536) {  // enough (token, column) threads to fill the GPU: slots in order per thread
         hipLaunchKernelGGL(k_combine_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, ypart, inv, probs,
-                           T, k, H, KS, P, shared, shared_scale, sKS, out);
+                           T, k, H, KS, P, shared, shared_scale, sKS, resid, out);
     } else {  // decode: spread the slots over lanes so each thread waits on one slot's loads
         const dim3 grid((unsigned)((H / 4 + kCombCols - 1) / kCombCols), (unsigned)std::min(T, 65535));
         hipLaunchKernelGGL(k_combine, grid, dim3(kCombLanes * kCombCols), 0, st, ypart, inv, probs, T, k, H, KS, P,
-                           shared, shared_scale, sKS, out);
+                           shared, shared_scale, sKS, resid, out);
     }
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;

@@ -99,7 +99,9 @@ int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const D
 int launch_expert_accum_ops(bool f16, const void *gate, const void *up, const void *down, const float *h, int inter,
                             int hidden, float weight, int use_gelu, float *act, float *out, hipStream_t st);
 
+// out = sum over slots of p * y (+ s * shared) [+ resid: the engine's x += proj].
 int launch_combine(const float *ypart, const int32_t *inv, const float *probs, int T, int k, int H, int KS, int P,
-                   const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st);
+                   const float *shared, const float *shared_scale, int sKS, float *out, hipStream_t st,
+                   const float *resid = nullptr);
 
 }  // namespace anedvd

@@ -309,8 +309,10 @@ __global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__res
     if (threadIdx.x == 0) scale[t] = shared_sigmoid(g);
 }
 
+// One forward call on stream st.  With `resid` the output is resid + the block's
+// output (the engine's x += proj, main.zig:519), as a stack of layers chains it.
 int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_logits, float *d_out, const Fwd &f,
-                   hipStream_t st, hipEvent_t *ev)
+                   hipStream_t st, hipEvent_t *ev, const float *resid = nullptr)
 {
     const int H = L->H, I = L->I, E = L->E, k = L->k, kk = k + (int)L->n_sh, P = T * kk;
     auto mark = [&](int i) {
@@ -359,7 +361,7 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
     mark(4);
     ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, T, kk, H, f.plan.ks_dn, P, separate ? f.sh_ypart : nullptr,
                               (separate && L->sgate_lin) ? f.sh_scale : nullptr, separate ? f.splan.ks_dn : 0, d_out,
-                              st));
+                              st, resid));
     mark(5);
     return ANEDVD_OK;
 }
@@ -1042,9 +1044,46 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
             set_error("time_forward: layers must share a context and a shape");
             return ANEDVD_E_INVALID_ARG;
         }
+    const bool chain = (flags & ANEDVD_TIME_CHAIN) != 0;
+    if (chain && (flags & (ANEDVD_TIME_GRAPH | ANEDVD_TIME_EXPERT_SOLO))) {
+        set_error("time_forward: a chained stack is timed with directly launched calls and stage events only");
+        return ANEDVD_E_INVALID_ARG;
+    }
     hipStream_t st = ctx->stream;
     Fwd f;
     ANEDVD_TRY(prepare(layers[0], T, false, f));
+    // Call i: layer i mod n.  Chained, the layers form a stack: each pass over it
+    // starts from d_h, layer j reads the previous layer's x (two ping-pong buffers)
+    // and writes x + its block output, layer j routes logits row block j of
+    // d_logits, and the last layer writes d_out.
+    const size_t H = layers[0]->H, E = layers[0]->E;
+    float *pp[2] = {nullptr, nullptr};
+    struct PpFree {
+        float **p;
+        ~PpFree()
+        {
+            for (int i = 0; i < 2; i++)
+                if (p[i]) (void)hipFree(p[i]);
+        }
+    } pp_free{pp};
+    if (chain && n_layers > 1)
+        for (int i = 0; i < 2; i++) ANEDVD_HIP(hipMalloc(&pp[i], T * H * sizeof(float)));
+    struct Call {
+        anedvd_moe_layer *L;
+        const float *in, *logits, *resid;
+        float *out;
+    };
+    auto call_of = [&](int i) -> Call {
+        const size_t j = (size_t)i % n_layers;
+        if (!chain) return Call{layers[j], d_h, d_logits, nullptr, d_out};
+        const float *in = j == 0 ? d_h : pp[(j - 1) % 2];
+        float *out = j + 1 == n_layers ? d_out : pp[j % 2];
+        return Call{layers[j], in, d_logits ? d_logits + j * T * E : nullptr, in, out};
+    };
+    auto run_call = [&](int i, hipEvent_t *ev) -> int {
+        const Call c = call_of(i);
+        return forward_device(c.L, c.in, (int)T, c.logits, c.out, f, st, ev, c.resid);
+    };
     // With ANEDVD_TIME_GRAPH each layer's forward is captured once into a HIP graph
     // and the timed loop replays the graphs (one submission per call).
     std::vector<hipGraphExec_t> execs;
@@ -1055,7 +1094,7 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
     if (flags & ANEDVD_TIME_GRAPH) {
         for (size_t i = 0; i < n_layers; i++) {
             ANEDVD_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-            const int rc = forward_device(layers[i], d_h, (int)T, d_logits, d_out, f, st, nullptr);
+            const int rc = run_call((int)i, nullptr);
             hipGraph_t g = nullptr;
             const hipError_t e = hipStreamEndCapture(st, &g);
             if (rc != ANEDVD_OK || e != hipSuccess) {
@@ -1084,7 +1123,7 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
             }
             return ANEDVD_OK;
         }
-        return forward_device(layers[(size_t)i % n_layers], d_h, (int)T, d_logits, d_out, f, st, nullptr);
+        return run_call(i, nullptr);
     };
     int rc = ANEDVD_OK;
     for (int i = 0; i < warmup && rc == ANEDVD_OK; i++) rc = step(i);
@@ -1110,8 +1149,7 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
     if (kernel_ms) {
         std::vector<hipEvent_t> ev((size_t)iters * 6);
         for (auto &e : ev) ANEDVD_HIP(hipEventCreate(&e));
-        for (int i = 0; i < iters; i++)
-            ANEDVD_TRY(forward_device(layers[i % n_layers], d_h, (int)T, d_logits, d_out, f, st, &ev[(size_t)i * 6]));
+        for (int i = 0; i < iters; i++) ANEDVD_TRY(run_call(i, &ev[(size_t)i * 6]));
         ANEDVD_HIP(hipStreamSynchronize(st));
         double acc[6] = {0, 0, 0, 0, 0, 0};
         for (int i = 0; i < iters; i++) {
@@ -1138,9 +1176,11 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
         ANEDVD_HIP(hipEventCreate(&a));
         ANEDVD_HIP(hipEventCreate(&b));
         int src = ANEDVD_OK;
-        for (int s = 0; s < 2 && src == ANEDVD_OK; s++) {
+        for (int s = 0; s < 3 && src == ANEDVD_OK; s++) {
             auto launch = [&](int i) -> int {
                 const anedvd_moe_layer *L = layers[(size_t)i % n_layers];
+                if (s == 2)  // the router GEMV alone: T tokens of d_h against the layer's [E][H] f16 router
+                    return launch_router(L->router, d_h, (int)T, (int)L->E, H, f.logits, st);
                 return s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act,
                                                      L->gelu, st)
                               : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart,
@@ -1155,7 +1195,7 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
                 set_error("time_forward: expert timing failed");
                 src = ANEDVD_E_HIP;
             }
-            kernel_ms[1 + s] = x / iters;
+            kernel_ms[s == 2 ? 0 : 1 + s] = x / iters;
         }
         (void)hipEventDestroy(a);
         (void)hipEventDestroy(b);

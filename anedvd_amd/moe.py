@@ -408,16 +408,22 @@ TIME_GRAPH = 1
 TIME_EXPERT_SOLO = 2
 
 
+TIME_CHAIN = 4
+
+
 def time_forward(layers: list, d_h: int, n_tokens: int, d_logits: int | None, d_out: int,
-                 warmup: int, iters: int, stages: bool = False, graph: bool = False, solo: bool = False):
+                 warmup: int, iters: int, stages: bool = False, graph: bool = False, solo: bool = False,
+                 chain: bool = False):
     """Runs the timed loop inside the library (HIP events on the context's stream),
     replaying per-layer HIP graphs when `graph`.  Returns (total_ms, per-stage mean
     ms or None); with `solo` the gate/up and down entries are single-launch means
-    from back-to-back launches of that stage alone."""
+    from back-to-back launches of that stage alone, and entry 0 the router GEMV's.
+    With `chain` the layers are a stack (x += proj from one layer to the next,
+    d_logits [n_layers][T][E])."""
     arr = (C.c_void_p * len(layers))(*[l.h.value for l in layers])
     ms = C.c_float()
     km = (C.c_float * 6)()
-    flags = (TIME_GRAPH if graph else 0) | (TIME_EXPERT_SOLO if solo else 0)
+    flags = (TIME_GRAPH if graph else 0) | (TIME_EXPERT_SOLO if solo else 0) | (TIME_CHAIN if chain else 0)
     _check(lib().anedvd_moe_time_forward(arr, len(layers), d_h, n_tokens, d_logits, d_out, warmup, iters,
                                          flags, C.byref(ms), km if (stages or solo) else None))
     return ms.value, (list(km) if (stages or solo) else None)

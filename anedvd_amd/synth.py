@@ -180,10 +180,38 @@ _GEN = {W.F16: f16, W.Q8_0: q8_0, W.Q8_1: q8_1, W.Q4_0: q4_0, W.Q4_1: q4_1, W.Q5
         W.Q3_K: q3_k, W.Q4_K: q4_k, W.Q5_K: q5_k, W.Q6_K: q6_k}
 
 
+_CHUNK_BLOCKS = 1 << 20
+
+
+def _workers() -> int:
+    import os
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
 def quant_matrix(t: int, seed: int, stream: int, n_elems: int, sigma: float, elem_offset: int = 0) -> np.ndarray:
+    """GGUF blocks of type t for elements [elem_offset, elem_offset + n_elems) of a
+    stream.  Every block is a pure function of its index, so large tensors are
+    generated in chunks on a thread pool (numpy's element-wise work runs outside
+    the GIL) with the same bytes as one call."""
     epb, bpb = W.BLOCK[t]
     assert n_elems % epb == 0 and elem_offset % epb == 0
-    return _GEN[t](seed, stream, n_elems // epb, sigma, elem_offset // epb).reshape(-1)
+    nb, b0 = n_elems // epb, elem_offset // epb
+    if nb <= _CHUNK_BLOCKS:
+        return _GEN[t](seed, stream, nb, sigma, b0).reshape(-1)
+    from concurrent.futures import ThreadPoolExecutor
+    out = np.empty(nb * bpb, dtype=np.uint8)
+
+    def part(c0):
+        n = min(_CHUNK_BLOCKS, nb - c0)
+        out[c0 * bpb:(c0 + n) * bpb] = _GEN[t](seed, stream, n, sigma, b0 + c0).reshape(-1)
+
+    with ThreadPoolExecutor(_workers()) as ex:
+        list(ex.map(part, range(0, nb, _CHUNK_BLOCKS)))
+    return out
 
 
 # ------------------------------------------------------------------- layers

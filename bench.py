@@ -1,26 +1,33 @@
-"""Throughput of the MI355X MoE FFN layer on its headline workload.
+"""Throughput of the MI355X MoE FFN layer on its headline workload, with every
+benchmarked workload beside it.
 
-Workload: one Qwen3-30B-A3B-shaped MoE layer (hidden 2048, 128 experts of SwiGLU
+Headline: one Qwen3-30B-A3B-shaped MoE layer (hidden 2048, 128 experts of SwiGLU
 2048->768->2048, top-8 softmax with renormalisation), Q8_0 experts, at decode
-batch 64 with i.i.d. U(0,1) router logits (the router GEMV is not part of this
-workload).  A step is one layer forward over the batch (route, dispatch, fused
-dequant + gate/up, fused dequant + down, combine) with the inputs already
-resident in HBM, its kernels launched directly on the library's stream (the
-time with one HIP graph per call is reported beside it).  Steps rotate over
-`--copies` device copies of the layer so the 256 MB Infinity Cache cannot serve
-the weights between steps.
+batch 64 with i.i.d. U(0,1) router logits (the router GEMV is timed on its own).
+A step is one layer forward over the batch (route, dispatch, fused dequant +
+gate/up, fused dequant + down, combine) with the inputs already resident in HBM,
+its kernels launched directly on the library's stream (the time with one HIP
+graph per call is reported beside it).  Steps rotate over `--copies` device
+copies of the layer so the 256 MB Infinity Cache cannot serve the weights.
 
-Prints ONE JSON line (rank 0, N=1) with the throughput, the roofline of the
-dominant kernel (the fused dequant + gate/up GEMV: its mean launch time over
-back-to-back launches, HIP events on the library's stream), and the CPU
-restatement of the reference path timed on the host cores on a bounded sample of
-the same batch.
+Beside it (`configs`): the Qwen3 Q4_K_M 512-token prefill with Zipf routing,
+Mixtral-8x7B Q4_0 at 1 and 2048 tokens, and the DeepSeek-V2-Lite 26-layer stack
+(26 distinct layers chained x += proj, at decode batch 32 and a 1024-token
+prefill).  Every workload's output is checked against the oracle on sampled
+tokens of the same run, and the oracle (the CPU restatement of the reference
+path, AVX2 build) is timed on one pinned host core in two modes: streaming (the
+engine's expert reads, per token or per 128-token prefill chunk) and resident
+f32 experts.
+
+Prints ONE JSON line (rank 0, N=1).
 """
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -33,6 +40,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 METRIC = "MoE-layer tok/s + % HBM roofline (decode), % MFMA peak (prefill), 30B-A3B shape"
+CPU_RUNS = 5                   # the CPU baseline reports the median of this many runs
 
 
 def log(msg: str):
@@ -60,109 +68,233 @@ def read_traffic(name: str):
     return None
 
 
-def cpu_baseline(spec, L, h, logits, budget_s: float):
-    """The oracle's streaming forward (Engine.forward's per-token decode path:
-    route, dequantise each selected expert, SwiGLU GEMVs) on 1 core, over as
-    many tokens of the batch as fit in about `budget_s` seconds."""
+# ------------------------------------------------------------------ CPU baseline
+
+def host_cpu() -> dict:
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "cores_allowed": len(os.sched_getaffinity(0))}
+
+
+@contextlib.contextmanager
+def pinned_core():
+    """Pins the calling thread to one core (the last one it may use) while timing."""
+    old = os.sched_getaffinity(0)
+    core = max(old)
+    os.sched_setaffinity(0, {core})
+    try:
+        yield core
+    finally:
+        os.sched_setaffinity(0, old)
+
+
+def cpu_median(fn) -> tuple:
+    fn()  # warm-up
+    ts = []
+    for _ in range(CPU_RUNS):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts
+
+
+def cpu_baseline(spec, L, h, lg, mode_a: tuple, n_b: int) -> dict:
+    """The oracle timed on one pinned core, median of CPU_RUNS runs after a warm-up.
+    Mode A is the engine's streaming path: ("stream", n) runs the per-token decode
+    loop (engine.zig:705-779: route, read each selected expert's three projections
+    from the GGUF bytes to f32, moeExpertAccumF32) over n tokens; ("chunk", n) runs
+    the batched prefill (engine.zig:1158-1268: each routed expert read once for the
+    chunk, then every token it serves) on one n-token chunk.  Mode B holds the
+    experts the sample touches as resident f32 (dequantised before timing) and runs
+    the decode loop over n_b tokens: the expert products alone."""
     from oracle import oracle as O
     ol = O.OracleLayer(spec, L)
-    t0 = time.perf_counter()
-    ref1 = ol.forward(h[:1], logits[:1], streaming=True)
-    per_tok = time.perf_counter() - t0
-    n = int(max(1, min(h.shape[0], budget_s / max(per_tok, 1e-6))))
-    t0 = time.perf_counter()
-    ref = ol.forward(h[:n], logits[:n], streaming=True)
-    dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/moe_oracle.c streaming decode (per token: route, dequantise 8 Q8_0 experts to f32, "
-                      f"SwiGLU GEMVs), first {n} tokens of the batch, {dt:.1f} s, gcc -O2, 1 thread"}, ref, n
+    kind, n_a = mode_a
+    ha, la = h[:n_a], (None if lg is None else lg[:n_a])
+    hb, lb = h[:n_b], (None if lg is None else lg[:n_b])
+    _, _, ia = ol.route(ha, n_a, la)
+    _, _, ib = ol.route(hb, n_b, lb)
+    touched_a = len(np.unique(ia))
+    exp_b = spec.expert_bytes()
+    out = {}
+    with pinned_core() as core:
+        ta, _ = cpu_median(lambda: ol.forward(ha, la, streaming=(kind == "stream"), fast=True))
+        R = ol.resident(np.unique(ib), fast=True)
+        tb, _ = cpu_median(lambda: R.forward(hb, lb))
+        R.free()
+    # bytes the CPU path reads: streaming, every (token, slot) reads its expert; a
+    # prefill chunk reads each touched expert once; resident, f32 weights per slot
+    bytes_a = (n_a * spec.k if kind == "stream" else touched_a) * exp_b + n_a * spec.shared_bytes()
+    bytes_b = n_b * spec.k * 3 * spec.inter * spec.hidden * 4
+    out["mode_a"] = {"tokens_per_s": round(n_a / ta, 3), "GBps": round(bytes_a / ta / 1e9, 3),
+                     "median_s": round(ta, 4), "runs": CPU_RUNS,
+                     "sample": (f"per-token streaming decode of {n_a} tokens" if kind == "stream" else
+                                f"batched prefill of one {n_a}-token chunk ({touched_a} experts read once)")}
+    out["mode_b"] = {"tokens_per_s": round(n_b / tb, 3), "GBps": round(bytes_b / tb / 1e9, 3),
+                     "median_s": round(tb, 4), "runs": CPU_RUNS,
+                     "sample": f"decode loop over {n_b} tokens on resident f32 experts ({len(np.unique(ib))} held)"}
+    out.update({"cores": 1, "core": core, "kind": "port",
+                "build": "oracle/moe_oracle.c, gcc -O3 -mavx2 -mno-fma -ffp-contract=off (8-lane loops vectorised, "
+                         "results bit-identical to the portable build)"})
+    return out
 
+
+# ------------------------------------------------------------------ workloads
 
 CONFIGS = {
-    # name: (spec attribute, tokens, routing, device copies rotated, layers timed as a stack)
-    "qwen3-q4km-512": ("QWEN3_30B_A3B_Q4_K_M", 512, "zipf", 2, 1),
-    "mixtral-q4_0-2048": ("MIXTRAL_8X7B_Q4_0", 2048, "normal", 3, 1),
-    "mixtral-q4_0-1": ("MIXTRAL_8X7B_Q4_0", 1, "normal", 3, 1),
-    "deepseek-v2-lite-32-x26": ("DEEPSEEK_V2_LITE_Q8_0", 32, "uniform", 26, 26),
-    "deepseek-v2-lite-1024-x26": ("DEEPSEEK_V2_LITE_Q8_0", 1024, "uniform", 26, 26),
+    # spec: workloads attribute; T tokens; routing of the logits; copies of the layer
+    # rotated (stack: distinct chained layers); parity: tokens sampled against the
+    # oracle; cpu_a: mode A of the CPU baseline; cpu_b: tokens of mode B
+    "qwen3-q4km-512": dict(spec="QWEN3_30B_A3B_Q4_K_M", T=512, routing="zipf", copies=2, parity=32,
+                           cpu_a=("chunk", 32), cpu_b=32),
+    "mixtral-q4_0-2048": dict(spec="MIXTRAL_8X7B_Q4_0", T=2048, routing="normal", copies=3, parity=16,
+                              cpu_a=("chunk", 4), cpu_b=4),
+    "mixtral-q4_0-1": dict(spec="MIXTRAL_8X7B_Q4_0", T=1, routing="normal", copies=3, parity=1,
+                           cpu_a=("stream", 1), cpu_b=1),
+    "deepseek-v2-lite-32-x26": dict(spec="DEEPSEEK_V2_LITE_Q8_0", T=32, routing="uniform", stack=26, parity=6,
+                                    cpu_a=("stream", 8), cpu_b=16),
+    "deepseek-v2-lite-1024-x26": dict(spec="DEEPSEEK_V2_LITE_Q8_0", T=1024, routing="uniform", stack=26, parity=6,
+                                      cpu_a=("chunk", 32), cpu_b=16),
 }
-_LAYERS = {}  # spec name -> resident layer copies, shared by the configs of one spec
+_LAYERS = {}  # (spec name, kind) -> resident layers and their host arrays
 
 
-def resident_layers(ctx, spec, copies: int) -> list:
-    """`copies` device copies of one synthetic layer of `spec` (seed 0): each copy
-    is a distinct HBM allocation, so rotating through them defeats the Infinity
-    Cache as a stack of distinct layers would."""
+def logits_for(spec, routing: str, T: int, seed: int):
+    from anedvd_amd import synth
+    if routing == "zipf":
+        lg = synth.zipf_logits(spec, T, seed=seed)
+    elif routing == "uniform":
+        lg = synth.uniform_logits(spec, T, seed=seed)
+    else:
+        lg = synth.activations(spec, T, seed=seed + 1)[:, :spec.n_experts]
+    return np.ascontiguousarray(lg, dtype=np.float32)
+
+
+def resident_copies(ctx, spec, copies: int):
+    """`copies` device copies of one synthetic layer of `spec` (seed 0): distinct
+    HBM allocations, so rotating through them defeats the Infinity Cache."""
     from anedvd_amd import moe, synth
-    have = _LAYERS.setdefault(spec.name, [])
-    if len(have) < copies:
-        L = synth.make_layer(spec, seed=0)
-        while len(have) < copies:
-            have.append(moe.MoeLayer(ctx, spec, L))
-    return have[:copies]
+    key = (spec.name, "copies")
+    if key not in _LAYERS:
+        _LAYERS[key] = (synth.make_layer(spec, seed=0), [])
+    L, have = _LAYERS[key]
+    while len(have) < copies:
+        have.append(moe.MoeLayer(ctx, spec, L))
+    return L, have[:copies]
+
+
+def resident_stack(ctx, spec, n: int):
+    """n distinct layers of `spec` (layer seeds 0..n-1), resident."""
+    from anedvd_amd import moe, synth
+    key = (spec.name, "stack")
+    if key not in _LAYERS:
+        t0 = time.perf_counter()
+        Ls, layers = [], []
+        for i in range(n):
+            Ls.append(synth.make_layer(spec, seed=0, layer=i))
+            layers.append(moe.MoeLayer(ctx, spec, Ls[-1]))
+        _LAYERS[key] = (Ls, layers)
+        log(f"[bench] {n} distinct {spec.name} layers generated and resident in {time.perf_counter() - t0:.1f} s")
+    return _LAYERS[key]
 
 
 def free_layers():
-    for ls in _LAYERS.values():
+    for _, ls in _LAYERS.values():
         for l in ls:
             l.free()
     _LAYERS.clear()
 
 
-def run_config(name: str, ctx, warmup: int, steps: int) -> dict:
+def parity_of(got: np.ndarray, want: np.ndarray, n: int) -> dict:
+    from anedvd_amd import moe
+    return {"tokens_checked": n, "rel_l2": moe.rel_l2(got, want),
+            "max_abs": float(np.abs(got.astype(np.float64) - want).max())}
+
+
+def sample_rows(T: int, n: int) -> np.ndarray:
+    return np.unique(np.linspace(0, T - 1, n).round().astype(np.int64)) if n < T else np.arange(T)
+
+
+def run_config(name: str, ctx, warmup: int, steps: int, with_parity: bool) -> dict:
     """One workload beside the headline: a layer call (route + dispatch + expert
     products + shared expert + combine, router logits given), rotated over device
-    copies of the layer.  For a stack, call j runs layer j mod n of n distinct
-    resident layers and the stack time is n times the mean call.  Reports tokens/s,
-    the layer's algorithmic HBM bytes/s and useful MFMA-path FLOP/s against the peaks."""
+    copies of the layer, or a chained stack of distinct layers.  Reports tokens/s,
+    the algorithmic HBM bytes/s and useful MFMA-path FLOP/s against the peaks, and
+    the oracle's agreement on sampled tokens of the same inputs."""
     from anedvd_amd import moe, synth
     from anedvd_amd import workloads as W
-    attr, T, routing, copies, stack = CONFIGS[name]
-    spec = getattr(W, attr)
+    from oracle import oracle as O
+    c = CONFIGS[name]
+    spec, T, stack = getattr(W, c["spec"]), c["T"], c.get("stack", 0)
     t0 = time.perf_counter()
-    layers = resident_layers(ctx, spec, copies)
     h = synth.activations(spec, T, seed=1)
-    if routing == "zipf":
-        lg = synth.zipf_logits(spec, T, seed=1)
-    elif routing == "uniform":
-        lg = synth.uniform_logits(spec, T, seed=1)
+    rows = sample_rows(T, c["parity"])
+    r = {"name": name, "workload": spec.name, "tokens": T, "routing": c["routing"]}
+    if stack:
+        Ls, layers = resident_stack(ctx, spec, stack)
+        lgs = np.stack([logits_for(spec, c["routing"], T, seed=1 + i) for i in range(stack)])
+        _, st = layers[0].forward(h, lgs[0], stats=True)
+        d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lgs), ctx.alloc(T * spec.hidden * 4)
+        passes = max(2, steps // stack)
+        ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, stack, stack * passes, chain=True)
+        _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 0, stack, stages=True, chain=True)
+        got = ctx.from_device(d_out, (T, spec.hidden), np.float32)  # one whole pass from d_h
+        for p in (d_h, d_lg, d_out):
+            ctx.free(p)
+        n_calls = stack * passes
+        if with_parity:
+            x = h[rows].copy()
+            for i in range(stack):
+                x = x + O.OracleLayer(spec, Ls[i]).forward(x, lgs[i][rows], fast=True)
+            r["parity"] = parity_of(got[rows], x, len(rows))
+        r.update({"stack_layers": stack, "layers": f"{stack} distinct layers, chained x += proj",
+                  "stack_ms": round(ms / passes, 4), "stack_tokens_per_s": round(T / (ms / passes / 1e3), 1)})
+        L = Ls[0]
+        lg = lgs[0]
+        solo = None
     else:
-        lg = synth.activations(spec, T, seed=2)[:, :spec.n_experts]
-    lg = np.ascontiguousarray(lg, dtype=np.float32)
-    _, st = layers[0].forward(h, lg, stats=True)
-    d_h, d_lg = ctx.to_device(h), ctx.to_device(lg)
-    d_out = ctx.alloc(T * spec.hidden * 4)
-    steps = max(steps, 2 * copies) // copies * copies
-    warmup = max(warmup, copies)
-    ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, warmup, steps)
-    _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, steps, stages=True)
-    _, solo = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, steps, solo=True)
-    for p in (d_h, d_lg, d_out):
-        ctx.free(p)
-    t = ms / 1e3 / steps
+        L, layers = resident_copies(ctx, spec, c["copies"])
+        lg = logits_for(spec, c["routing"], T, seed=1)
+        out_host, st = layers[0].forward(h, lg, stats=True)
+        d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lg), ctx.alloc(T * spec.hidden * 4)
+        n_calls = max(steps, 2 * c["copies"]) // c["copies"] * c["copies"]
+        ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, max(warmup, c["copies"]), n_calls)
+        _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, n_calls, stages=True)
+        _, solo = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, n_calls, solo=True)
+        for p in (d_h, d_lg, d_out):
+            ctx.free(p)
+        if with_parity:
+            want = O.OracleLayer(spec, L).forward(h[rows], lg[rows], fast=True)
+            r["parity"] = parity_of(out_host[rows], want, len(rows))
+        r["layer_copies_rotated"] = c["copies"]
+    t = ms / 1e3 / n_calls  # one layer call
     flops = spec.call_flops(T, with_router=False)
     lbytes = spec.call_bytes(st["touched_experts"], T, with_router=False)
-    r = {"name": name, "workload": spec.name, "tokens": T, "routing": routing, "layer_copies_rotated": copies,
-         "touched_experts": st["touched_experts"], "max_group": st["max_group"],
-         "path": "grouped GEMM" if st["path"] else "decode GEMV",
-         "ms_per_call": round(ms / steps, 4), "tokens_per_s": round(T / t, 1),
-         "TFLOPs": round(flops / t / 1e12, 2), "mfma_frac": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-         "layer_GBps": round(lbytes / t / 1e9, 1), "hbm_frac": round(lbytes / t / 1e9 / HBM_PEAK_GBS, 4),
-         "stage_ms": dict(zip(["route_dispatch", "gate_up", "down", "shared", "combine", "total"],
-                              [round(x, 4) for x in stages])),
-         "solo_launch_ms": {"gate_up": round(solo[1], 4), "down": round(solo[2], 4)}}
-    gu_flops = 2 * 2 * T * spec.k * spec.hidden * spec.inter  # the routed gate and up products
-    r["gate_up_mfma_frac"] = round(gu_flops / (solo[1] / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
-    if stack > 1:
-        r["stack_layers"] = stack
-        r["stack_ms"] = round(ms / steps * stack, 4)
-        r["stack_tokens_per_s"] = round(T / (t * stack), 1)
+    r.update({"touched_experts": st["touched_experts"], "max_group": st["max_group"],
+              "path": "grouped GEMM" if st["path"] else "decode GEMV",
+              "ms_per_call": round(ms / n_calls, 4), "tokens_per_s": round(T / t, 1),
+              "TFLOPs": round(flops / t / 1e12, 2), "mfma_frac": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+              "layer_GBps": round(lbytes / t / 1e9, 1), "hbm_frac": round(lbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+              "stage_ms": dict(zip(["route_dispatch", "gate_up", "down", "shared", "combine", "total"],
+                                   [round(x, 4) for x in stages]))})
+    if solo is not None:
+        r["solo_launch_ms"] = {"gate_up": round(solo[1], 4), "down": round(solo[2], 4)}
+        gu_flops = 2 * 2 * T * spec.k * spec.hidden * spec.inter  # the routed gate and up products
+        r["gate_up_mfma_frac"] = round(gu_flops / (solo[1] / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+    r["_cpu"] = (spec, L, h, lg, c["cpu_a"], c["cpu_b"])
     log(f"[bench] {name}: {r['ms_per_call'] * 1e3:.1f} us/call ({r['path']}), {r['tokens_per_s']:.0f} tok/s, "
         f"{r['TFLOPs']} TFLOP/s ({100 * r['mfma_frac']:.1f}% of fp16 MFMA peak), {r['layer_GBps']} GB/s "
         f"({100 * r['hbm_frac']:.1f}% of HBM), touched {r['touched_experts']}, max group {r['max_group']}"
-        + (f", {stack}-layer stack {r['stack_ms']:.3f} ms" if stack > 1 else "")
-        + f", event stages {r['stage_ms']}, solo launches {r['solo_launch_ms']} "
-        f"(setup {time.perf_counter() - t0:.1f} s)")
+        + (f", {stack}-layer stack {r['stack_ms']:.3f} ms" if stack else "")
+        + (f", parity rel-L2 {r['parity']['rel_l2']:.2e} on {r['parity']['tokens_checked']} tokens"
+           if "parity" in r else "")
+        + f", event stages {r['stage_ms']} (setup {time.perf_counter() - t0:.1f} s)")
     return r
 
 
@@ -174,7 +306,8 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--copies", type=int, default=8, help="device copies of the layer rotated per step")
     ap.add_argument("--sweep", default="1,8,32", help="extra decode batches reported beside the headline ('' = none)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
+    ap.add_argument("--cpu", type=int, default=1, help="time the CPU baseline (0 = skip)")
+    ap.add_argument("--parity", type=int, default=1, help="check every workload against the oracle (0 = skip)")
     ap.add_argument("--configs", default=",".join(CONFIGS),
                     help="further workloads reported beside the headline ('' = none): " + ", ".join(CONFIGS))
     ap.add_argument("--configs-only", action="store_true", help="run only the --configs workloads (profiling)")
@@ -202,9 +335,12 @@ def main():
         log(f"[bench] calibration: 3 device copies of {args.calibrate_copy} MiB")
         del src, dst
 
+    names = [x for x in args.configs.split(",") if x.strip()]
     if args.configs_only:
         ctx = moe.MoeContext(0)
-        out = [run_config(name, ctx, args.warmup, args.steps) for name in args.configs.split(",") if name.strip()]
+        out = [run_config(name, ctx, args.warmup, args.steps, bool(args.parity)) for name in names]
+        for r in out:
+            r.pop("_cpu")
         print(json.dumps({"configs": out}), flush=True)
         free_layers()
         ctx.close()
@@ -235,16 +371,19 @@ def main():
         touched = st["touched_experts"]
         layer_s = ms / 1e3 / steps
         lbytes = spec.call_bytes(touched, T, with_router=False)
+        rb = spec.n_experts * spec.hidden * 2 + T * spec.hidden * 4 + T * spec.n_experts * 4
         r = {"batch": T, "touched_experts": touched, "ms_per_step": ms / steps, "graph_ms_per_step": ms_graph / steps,
              "tokens_per_s": T / layer_s, "layer_GBps": lbytes / layer_s / 1e9,
              "layer_hbm_frac": lbytes / layer_s / 1e9 / HBM_PEAK_GBS,
              "stage_ms": dict(zip(["route_dispatch", "gate_up", "down", "shared", "combine", "total"],
                                   [round(x, 5) for x in stages])),
-             "solo_launch_ms": {"gate_up": round(solo[1], 5), "down": round(solo[2], 5)}}
+             "solo_launch_ms": {"gate_up": round(solo[1], 5), "down": round(solo[2], 5)},
+             "router_gemv": {"us": round(solo[0] * 1e3, 3), "bytes": rb,
+                             "GBps": round(rb / (solo[0] / 1e3) / 1e9, 1)}}
         log(f"[bench] B={T}: {ms / steps * 1e3:.1f} us/step ({ms_graph / steps * 1e3:.1f} as graphs), "
             f"{r['tokens_per_s']:.0f} tok/s, "
             f"{r['layer_GBps']:.0f} GB/s ({100 * r['layer_hbm_frac']:.1f}% of HBM), touched {touched}, "
-            f"event stages {r['stage_ms']}, solo launches {r['solo_launch_ms']}")
+            f"event stages {r['stage_ms']}, solo launches {r['solo_launch_ms']}, router GEMV {r['router_gemv']}")
         return r, h, lg, out_host
 
     sweep = []
@@ -261,19 +400,39 @@ def main():
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": read_traffic("pmc_k_mm_gateup_q8_0_decode_b64.md"),
                 "bytes_per_launch": gu_bytes, "avg_launch_ms": gu_ms}
+    for l in layers:
+        l.free()
 
-    configs = []
-    for name in [x for x in args.configs.split(",") if x.strip()]:
-        configs.append(run_config(name, ctx, args.warmup, max(10, args.steps // 4)))
+    configs = [run_config(name, ctx, args.warmup, max(10, args.steps // 4), bool(args.parity)) for name in names]
     free_layers()
 
-    cpu = None
     parity = None
-    if args.cpu_seconds > 0:
-        cpu, ref, n = cpu_baseline(spec, L, h, lg, args.cpu_seconds)
-        parity = {"tokens_checked": n, "rel_l2": moe.rel_l2(out_gpu[:n], ref),
-                  "max_abs": float(np.abs(out_gpu[:n].astype(np.float64) - ref).max())}
-        log(f"[bench] cpu baseline {cpu['value']} tok/s; GPU vs oracle on {n} tokens: rel-L2 {parity['rel_l2']:.2e}")
+    if args.parity:
+        from oracle import oracle as O
+        rows = sample_rows(B, 16)
+        want = O.OracleLayer(spec, L).forward(h[rows], lg[rows], fast=True)
+        parity = parity_of(out_gpu[rows], want, len(rows))
+        log(f"[bench] headline vs oracle on {len(rows)} tokens: rel-L2 {parity['rel_l2']:.2e}, "
+            f"max-abs {parity['max_abs']:.2e}")
+
+    cpu = None
+    if args.cpu:
+        hw = host_cpu()
+        base = cpu_baseline(spec, L, h, lg, ("stream", 16), 32)
+        a = base["mode_a"]
+        cpu = {"value": a["tokens_per_s"], "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"oracle streaming decode (per token: route, read the 8 selected Q8_0 experts to f32, "
+                         f"SwiGLU GEMVs) over the first 16 tokens of the batch, median of {CPU_RUNS} runs on one "
+                         f"pinned core of {hw['cpu_model']} ({hw['nproc']} logical CPUs)",
+               "GBps": a["GBps"], "mode_b": base["mode_b"], "build": base["build"], **hw}
+        log(f"[bench] cpu baseline: streaming {a['tokens_per_s']} tok/s ({a['GBps']} GB/s), resident f32 "
+            f"{base['mode_b']['tokens_per_s']} tok/s on {hw['cpu_model']}")
+        for r in configs:
+            r["cpu_baseline"] = cpu_baseline(*r["_cpu"])
+            log(f"[bench] cpu baseline {r['name']}: mode A {r['cpu_baseline']['mode_a']['tokens_per_s']} tok/s, "
+                f"mode B {r['cpu_baseline']['mode_b']['tokens_per_s']} tok/s")
+    for r in configs:
+        r.pop("_cpu")
 
     line = {
         "metric": METRIC, "value": round(head["tokens_per_s"], 1), "unit": "tokens/s", "n_gpus": 1,
@@ -287,14 +446,12 @@ def main():
         "graph_ms_per_step": round(head["graph_ms_per_step"], 5),
         "layer_GBps": round(head["layer_GBps"], 1), "layer_hbm_frac": round(head["layer_hbm_frac"], 4),
         "touched_experts": head["touched_experts"], "stage_ms": head["stage_ms"],
-        "solo_launch_ms": head["solo_launch_ms"],
+        "solo_launch_ms": head["solo_launch_ms"], "router_gemv": head["router_gemv"],
         "roofline": roofline, "cpu_baseline": cpu, "parity_vs_oracle": parity,
         "sweep": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()} for r in sweep],
         "configs": configs,
     }
     print(json.dumps(line), flush=True)
-    for l in layers:
-        l.free()
     ctx.close()
 
 

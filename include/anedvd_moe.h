@@ -266,9 +266,17 @@ int anedvd_moe_synchronize(anedvd_moe_ctx *ctx);
  * combine, and the whole call.  With ANEDVD_TIME_EXPERT_SOLO as well,
  * kernel_ms[1] and kernel_ms[2] are instead the mean milliseconds of one routed
  * gate/up (resp. down) launch, timed over `iters` back-to-back launches of that
- * stage alone (same layer rotation, the last call's dispatch and activations). */
+ * stage alone (same layer rotation, the last call's dispatch and activations),
+ * and kernel_ms[0] that of one router GEMV launch (cpu.matmulF16 of the T rows of
+ * d_h against the layer's [E][H] f16 router, engine.zig:715).
+ * ANEDVD_TIME_CHAIN: the layers are a stack, as the engine runs a model's MoE
+ * blocks: each pass over it starts from d_h, layer j takes the previous layer's
+ * x and writes x + its block output (x += proj, main.zig:519), routing row block
+ * j of d_logits ([n_layers][T][E], when given); the last layer writes d_out.
+ * Not with ANEDVD_TIME_GRAPH or ANEDVD_TIME_EXPERT_SOLO. */
 #define ANEDVD_TIME_GRAPH 1
 #define ANEDVD_TIME_EXPERT_SOLO 2
+#define ANEDVD_TIME_CHAIN 4
 int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, const float *d_h,
                             size_t n_tokens, const float *d_logits, float *d_out, int warmup,
                             int iters, int flags, float *ms, float *kernel_ms);

@@ -731,6 +731,84 @@ done:
     return rc;
 }
 
+/* Mode B of the CPU baseline: the experts dequantised to f32 once and held (as the
+ * eager loader holds its experts resident, model.zig:414-470), so the per-token
+ * loop below times the expert products alone.  need[e] != 0 marks the experts to
+ * hold; the others stay NULL. */
+struct or_resident {
+    const or_layer *L;
+    float **wg, **wu, **wd;
+};
+
+or_resident *or_resident_create(const or_layer *L, const uint8_t *need)
+{
+    const size_t E = L->n_experts, n = (size_t)L->inter * L->hidden;
+    or_resident *R = calloc(1, sizeof *R);
+    if (!R) return NULL;
+    R->L = L;
+    R->wg = calloc(E, sizeof(float *));
+    R->wu = calloc(E, sizeof(float *));
+    R->wd = calloc(E, sizeof(float *));
+    if (!R->wg || !R->wu || !R->wd) { or_resident_free(R); return NULL; }
+    for (size_t e = 0; e < E; e++) {
+        if (!need[e]) continue;
+        R->wg[e] = malloc(n * sizeof(float));
+        R->wu[e] = malloc(n * sizeof(float));
+        R->wd[e] = malloc(n * sizeof(float));
+        if (!R->wg[e] || !R->wu[e] || !R->wd[e] ||
+            or_read_expert_f32(L->gate_type, L->gate, L->gate_len, (uint32_t)e, (uint32_t)E, R->wg[e], n) ||
+            or_read_expert_f32(L->up_type, L->up, L->up_len, (uint32_t)e, (uint32_t)E, R->wu[e], n) ||
+            or_read_expert_f32(L->down_type, L->down, L->down_len, (uint32_t)e, (uint32_t)E, R->wd[e], n)) {
+            or_resident_free(R);
+            return NULL;
+        }
+    }
+    return R;
+}
+
+void or_resident_free(or_resident *R)
+{
+    if (!R) return;
+    for (size_t e = 0; R->wg && e < R->L->n_experts; e++) {
+        free(R->wg[e]);
+        free(R->wu[e]);
+        free(R->wd[e]);
+    }
+    free(R->wg); free(R->wu); free(R->wd);
+    free(R);
+}
+
+/* The decode loop of engine.zig:705-779 over resident experts: per token, route,
+ * then moeExpertAccumF32 per slot, then the shared expert.  OR_ERR_OUT_OF_RANGE if a
+ * token routes to an expert that is not held. */
+int or_layer_forward_resident(const or_resident *R, const float *h, size_t T, const float *logits_in, float *out)
+{
+    const or_layer *L = R->L;
+    const size_t H = L->hidden, I = L->inter, E = L->n_experts, k = L->k;
+    int rc = OR_OK;
+    float *lg = malloc(E * sizeof(float)), *probs = malloc(k * sizeof(float));
+    uint32_t *idx = malloc(k * sizeof(uint32_t));
+    float *hs = malloc(I * sizeof(float)), *is = malloc(I * sizeof(float));
+    float *sh_out = L->shared_inter ? malloc(H * sizeof(float)) : NULL;
+    float *sh_scr = L->shared_inter ? malloc(L->shared_inter * sizeof(float)) : NULL;
+    for (size_t t = 0; t < T && rc == OR_OK; t++) {
+        const float *ht = h + t * H;
+        if (logits_in) memcpy(lg, logits_in + t * E, E * sizeof(float));
+        else or_matmul_f16(lg, L->router, ht, E, H);
+        or_moe_route(lg, E, k, L->norm_topk_prob, probs, idx);
+        float *proj = out + t * H;
+        for (size_t o = 0; o < H; o++) proj[o] = 0.0f;
+        for (size_t s = 0; s < k; s++) {
+            const uint32_t e = idx[s];
+            if (!R->wg[e]) { rc = OR_ERR_OUT_OF_RANGE; break; }
+            or_moe_expert_accum_f32(proj, hs, is, ht, R->wg[e], R->wu[e], R->wd[e], I, H, probs[s], L->use_gelu);
+        }
+        if (rc == OR_OK && L->shared_inter) shared_add(L, ht, proj, sh_out, sh_scr);
+    }
+    free(lg); free(probs); free(idx); free(hs); free(is); free(sh_out); free(sh_scr);
+    return rc;
+}
+
 /* The streaming decode loop exactly as the engine runs it (engine.zig:705-779):
  * per token, per slot, dequantise the three projections from the payload and
  * accumulate.  Slow on purpose; it is the CPU baseline. */

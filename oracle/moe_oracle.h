@@ -127,6 +127,15 @@ int or_layer_forward(const or_layer *L, const float *h, size_t n_tokens, const f
 int or_layer_forward_streaming(const or_layer *L, const float *h, size_t n_tokens,
                                const float *logits_in, float *out);
 
+/* Resident f32 experts (the CPU baseline's mode B): need[e] != 0 dequantises
+ * expert e's three projections once; or_layer_forward_resident then runs the
+ * decode loop of engine.zig:705-779 on them (bit-identical to the streaming loop). */
+typedef struct or_resident or_resident;
+or_resident *or_resident_create(const or_layer *L, const uint8_t *need);
+void or_resident_free(or_resident *R);
+int or_layer_forward_resident(const or_resident *R, const float *h, size_t n_tokens,
+                              const float *logits_in, float *out);
+
 #ifdef __cplusplus
 }
 #endif

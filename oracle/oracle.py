@@ -28,7 +28,25 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", HERE], check=True)
 
 
+AVX2_PATH = os.path.join(HERE, "liboracle_moe_avx2.so")
 _lib = None
+_lib_fast = None
+
+
+def has_avx2() -> bool:
+    try:
+        return any(line.startswith("flags") and " avx2" in line for line in open("/proc/cpuinfo"))
+    except OSError:
+        return False
+
+
+def lib_fast():
+    """The AVX2 build of the same source (bit-identical results), for timing the
+    CPU baseline; the portable build where the host lacks AVX2."""
+    global _lib_fast
+    if _lib_fast is None:
+        _lib_fast = _load(AVX2_PATH) if has_avx2() and os.path.exists(AVX2_PATH) else lib()
+    return _lib_fast
 
 
 def lib():
@@ -36,7 +54,13 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = C.CDLL(LIB_PATH)
+        _lib = _load(LIB_PATH)
+    return _lib
+
+
+def _load(path):
+    if True:
+        L = C.CDLL(path)
         L.or_block_elems.restype = _sz
         L.or_block_elems.argtypes = [C.c_int]
         L.or_block_bytes.restype = _sz
@@ -78,8 +102,13 @@ def lib():
         L.or_layer_forward.argtypes = [C.c_void_p, _f32p, _sz, C.c_void_p, _f32p]
         L.or_layer_forward_streaming.restype = C.c_int
         L.or_layer_forward_streaming.argtypes = [C.c_void_p, _f32p, _sz, C.c_void_p, _f32p]
-        _lib = L
-    return _lib
+        L.or_resident_create.restype = C.c_void_p
+        L.or_resident_create.argtypes = [C.c_void_p, _u8p]
+        L.or_resident_free.restype = None
+        L.or_resident_free.argtypes = [C.c_void_p]
+        L.or_layer_forward_resident.restype = C.c_int
+        L.or_layer_forward_resident.argtypes = [C.c_void_p, _f32p, _sz, C.c_void_p, _f32p]
+    return L
 
 
 def _bytes_arg(src):
@@ -256,13 +285,54 @@ class OracleLayer:
                              logits.ctypes.data_as(C.c_void_p), probs.reshape(-1), idx.reshape(-1))
         return logits, probs, idx
 
-    def forward(self, h: np.ndarray, logits_in: np.ndarray | None = None, streaming: bool = False) -> np.ndarray:
+    def forward(self, h: np.ndarray, logits_in: np.ndarray | None = None, streaming: bool = False,
+                fast: bool = False) -> np.ndarray:
+        """The block for T tokens.  streaming: the engine's per-token decode loop
+        (expert reads per token and slot); else experts dequantised once per call
+        (the engine's batched prefill, engine.zig:1204-1264).  fast: the AVX2 build."""
         h = np.ascontiguousarray(h, np.float32)
         T = h.shape[0]
         lp = None if logits_in is None else np.ascontiguousarray(logits_in, np.float32)
         out = np.zeros((T, self.spec.hidden), dtype=np.float32)
-        fn = lib().or_layer_forward_streaming if streaming else lib().or_layer_forward
+        L = lib_fast() if fast else lib()
+        fn = L.or_layer_forward_streaming if streaming else L.or_layer_forward
         rc = fn(self.ptr, h.reshape(-1), T, None if lp is None else lp.ctypes.data_as(C.c_void_p), out.reshape(-1))
         if rc != OK:
             raise RuntimeError(f"oracle layer forward failed: {rc}")
         return out
+
+    def resident(self, need, fast: bool = False) -> "Resident":
+        """Mode B: experts with need[e] dequantised to f32 once and held."""
+        return Resident(self, need, fast)
+
+
+class Resident:
+    """Resident f32 experts of an OracleLayer (or_resident_create)."""
+
+    def __init__(self, layer: OracleLayer, need, fast: bool):
+        self.layer = layer
+        self.L = lib_fast() if fast else lib()
+        mask = np.zeros(layer.spec.n_experts, np.uint8)
+        mask[np.asarray(need, dtype=np.int64)] = 1
+        self.h = self.L.or_resident_create(layer.ptr, mask)
+        if not self.h:
+            raise RuntimeError("or_resident_create failed")
+
+    def forward(self, h: np.ndarray, logits_in: np.ndarray | None = None) -> np.ndarray:
+        h = np.ascontiguousarray(h, np.float32)
+        T = h.shape[0]
+        lp = None if logits_in is None else np.ascontiguousarray(logits_in, np.float32)
+        out = np.zeros((T, self.layer.spec.hidden), dtype=np.float32)
+        rc = self.L.or_layer_forward_resident(self.h, h.reshape(-1), T,
+                                              None if lp is None else lp.ctypes.data_as(C.c_void_p), out.reshape(-1))
+        if rc != OK:
+            raise RuntimeError(f"oracle resident forward failed: {rc}")
+        return out
+
+    def free(self):
+        if self.h:
+            self.L.or_resident_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()

@@ -117,6 +117,33 @@ def test_deepseek_v2_lite_with_merged_shared_expert(ctx, T, n_sample):
     layer.free()
 
 
+@pytest.mark.parametrize("T", [20, 300])
+def test_chained_stack_matches_layer_by_layer(ctx, T):
+    """The timed stack (ANEDVD_TIME_CHAIN: layer j takes the previous layer's x and
+    writes x + its block output, x += proj as main.zig:519 adds it) equals running
+    the distinct layers one after another from the host and adding the residual,
+    bit for bit; and a second pass from the same input gives the same result."""
+    spec = dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="stack", hidden=512, inter=512, n_experts=8, k=2,
+                               shared_inter=1024, shared_gated=True)
+    n = 3
+    Ls = [synth.make_layer(spec, seed=0, layer=i) for i in range(n)]
+    layers = [moe.MoeLayer(ctx, spec, L) for L in Ls]
+    h = synth.activations(spec, T, seed=2)
+    lgs = np.stack([synth.uniform_logits(spec, T, seed=10 + i) for i in range(n)])
+    x = h.copy()
+    for i in range(n):
+        x = x + layers[i].forward(x, lgs[i])
+    d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lgs), ctx.alloc(T * spec.hidden * 4)
+    for passes in (1, 2):
+        moe.time_forward(layers, d_h, T, d_lg, d_out, 0, n * passes, chain=True)
+        got = ctx.from_device(d_out, (T, spec.hidden), np.float32)
+        assert np.array_equal(bits(got), bits(x)), passes
+    for p in (d_h, d_lg, d_out):
+        ctx.free(p)
+    for layer in layers:
+        layer.free()
+
+
 # ------------------------------------------------------------------ invariants
 
 INVARIANT_SPECS = [

@@ -413,6 +413,30 @@ def test_layer_forward_streaming_equals_expert_major_and_f64():
     assert np.linalg.norm(a - ref) / np.linalg.norm(ref) < 1e-6
 
 
+def test_fast_build_and_resident_mode_are_bit_identical():
+    """The CPU baseline's builds and modes compute the same bits: the AVX2 build of
+    the oracle (vectorised 8-lane loops, no FMA, no reassociation) equals the
+    portable build, and the resident-f32 decode loop equals the streaming one."""
+    import dataclasses
+    spec = dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, hidden=512, inter=512, n_experts=16, k=4,
+                               shared_inter=1024, shared_gated=True)
+    L = synth.make_layer(spec, seed=4)
+    h = synth.activations(spec, 12, seed=4)
+    ol = O.OracleLayer(spec, L)
+    ref = ol.forward(h, streaming=True)
+    for fast in (False, True):
+        assert np.array_equal(ol.forward(h, streaming=True, fast=fast).view(np.uint32), ref.view(np.uint32))
+        assert np.array_equal(ol.forward(h, fast=fast).view(np.uint32), ref.view(np.uint32))
+        R = ol.resident(range(spec.n_experts), fast=fast)
+        assert np.array_equal(R.forward(h).view(np.uint32), ref.view(np.uint32))
+        R.free()
+    _, _, idx = ol.route(h, 12)
+    R = ol.resident([int(idx[0, 0])])
+    with pytest.raises(RuntimeError):  # a token routed to an expert that is not held
+        R.forward(h)
+    R.free()
+
+
 def test_layer_forward_shared_expert_gate():
     """With shared_gate_lin = 0 the shared expert joins at half weight
     (engine.zig:2100-2105); with no gate it joins at weight 1.0 (engine.zig:687-691)."""
