@@ -196,12 +196,16 @@ __device__ inline float shared_sigmoid(float g)
     return ex / (1.0f + ex);
 }
 
+// 2^p with p = 15 - e for maxabs = m 2^e, m in [0.5, 1), clamped to [-100, 100]: the
+// largest magnitude lands in [2^14, 2^15).  For a normal maxabs with biased exponent
+// field E, e = E - 126; a subnormal one (E = 0) clamps to 2^100 as its true exponent
+// would.  Read off the bits: no frexp, no ldexp.
 __device__ inline float pow2_scale(float maxabs)
 {
     if (!(maxabs > 0.0f) || !(maxabs < __builtin_inff())) return 1.0f;
-    int e;
-    frexpf(maxabs, &e);  // maxabs = m * 2^e, m in [0.5, 1)
-    return ldexpf(1.0f, max(-100, min(15 - e, 100)));
+    const int E = (__float_as_int(maxabs) >> 23) & 0xFF;
+    const int p = max(-100, min(141 - E, 100));
+    return __int_as_float((p + 127) << 23);
 }
 
 template <int CTRL>

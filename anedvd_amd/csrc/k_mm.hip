@@ -38,6 +38,17 @@ constexpr int kWaves = 4;
 #ifndef ANEDVD_WG_TARGET
 #define ANEDVD_WG_TARGET 1024
 #endif
+// Mean group size (tokens per expert) from which the planner takes the grouped
+// GEMM (k_pf.hip) instead of the decode kernels.
+#ifndef ANEDVD_STAGED_MIN
+#define ANEDVD_STAGED_MIN 32
+#endif
+// Mean group size from which the grouped GEMM takes 128-token workgroups (types
+// with such a kernel only).
+#ifndef ANEDVD_PF_WIDE_MIN
+#define ANEDVD_PF_WIDE_MIN 64
+#endif
+constexpr int kCUs = 256;  // MI355X compute units
 #ifdef ANEDVD_MM_WPE
 #define MM_ATTR __attribute__((amdgpu_waves_per_eu(ANEDVD_MM_WPE)))
 #else
@@ -919,16 +930,45 @@ static int choose_ks(int units, int spu, long wg_per_ks, int waves_per_k, int mi
 MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u)
 {
     MmPlan p{};
-    // The grouped GEMM (64-token chunks) once the groups average 32 tokens and its
-    // gate/up grid has a workgroup per CU at least; the chunks then give the grid
-    // its parallelism and K is not split.  (A single shared expert at 32 tokens
-    // would be 22 workgroups: it measured 105 us against the decode kernels' split K.)
+    // The grouped GEMM (64-token chunks of a group, activations staged in LDS and
+    // shared by four wavefronts) once the groups average 32 tokens and its gate/up
+    // grid has a workgroup per CU at least; the chunks then give the grid its
+    // parallelism and K is not split.  Below that, the decode kernels: 16-token
+    // tiles, activations straight from L2, K split over workgroups.  (A single
+    // shared expert at 32 tokens on the grouped GEMM would be 22 workgroups: it
+    // measured 105 us against the decode kernels' split K.  Kernels that read the
+    // activations from L2 per wavefront with folded scales and 32- or 64-token
+    // chunks measured 233 against 192 us on the Qwen3 512-token prefill and 512
+    // against 377 us on the DeepSeek 1024-token one: four wavefronts fetching the
+    // same activations from L2 cost more than staging them once in LDS.)
+    const long mean = P / std::max(max_u, 1);
     const long pf_wgs = (long)((P + 63) / 64) * (I / 128);
-    p.mt = (P >= 32 * max_u && grouped_supported(H, I) && pf_wgs >= 256) ? 4 : 1;
+    if (mean >= ANEDVD_STAGED_MIN && grouped_supported(H, I) && pf_wgs >= 256) {
+        p.kind = kMmStaged;
+        // 128-token workgroups once the groups average 64 tokens: each dequantised
+        // step then feeds eight token tiles instead of four.  (Mixtral 2048 tokens:
+        // gate/up 1.31 -> 1.20 ms; DeepSeek-V2-Lite 1024: gate/up 220 -> 210 us,
+        // down 130 -> 111 us.)
+        const long wide_wgs = (long)((P + 127) / 128) * (I / 128);
+        const bool wide = mean >= ANEDVD_PF_WIDE_MIN && wide_wgs >= 256;
+        p.mt_gu = wide && grouped_wide(gate_type) ? 8 : 4;
+        p.mt_dn = wide && grouped_wide(down_type) ? 8 : 4;
+        // A long down K (>= 128 steps) splits in two when that shortens the grid's
+        // rounds of resident workgroups (two per CU) by 10 %: a partial last round
+        // is then half as long, for one more plane for the combine to add.
+        // (Mixtral 2048 tokens: down 858 -> 700 us, combine 27 -> 45 us.)
+        const long dn_wgs = (long)(P / (16 * p.mt_dn) + max_u) * (H / 256);
+        const long r1 = (dn_wgs + 2 * kCUs - 1) / (2 * kCUs), r2 = (2 * dn_wgs + 2 * kCUs - 1) / (2 * kCUs);
+        p.ks_dn = I / kStep >= 128 && 10 * r2 <= 18 * r1 && grouped_down_ks_ok(down_type, I, 2) ? 2 : 1;
+        p.mt = std::max(p.mt_gu, p.mt_dn);
+    } else {
+        p.kind = kMmDecode;
+        p.mt = 1;
+    }
     p.chunk = 16 * p.mt;
     p.nchunk = P / p.chunk + max_u;
-    if (p.mt > 1) {
-        p.ks_gu = p.ks_dn = 1;
+    if (p.kind != kMmDecode) {
+        p.ks_gu = 1;
         return p;
     }
     p.ks_gu = choose_ks(H / kStep / steps_per_unit(gate_type), steps_per_unit(gate_type), (long)max_u * (I / kRowBlock),
@@ -976,7 +1016,8 @@ static int launch_down_d(const MmArgs &a, int, hipStream_t st)
 int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
                          const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st)
 {
-    if (plan.mt > 1) return launch_grouped_gateup(gate, up, x, H, I, d, P, plan.mt, plan.nchunk, act, use_gelu, st);
+    if (plan.kind == kMmStaged)
+        return launch_grouped_gateup(gate, up, x, H, I, d, P, plan.mt_gu, plan.nchunk, act, use_gelu, st);
     if (gate.type != up.type) {
         set_error("expert gate/up: gate type %d and up type %d differ", gate.type, up.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
@@ -1026,7 +1067,8 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
         set_error("down: the dispatch's rows and slots and the output are needed (kk %d)", kk);
         return ANEDVD_E_INVALID_ARG;
     }
-    if (plan.mt > 1) return launch_grouped_down(down, act, H, I, d, P, plan.mt, plan.nchunk, ypart, kk, st);
+    if (plan.kind == kMmStaged)
+        return launch_grouped_down(down, act, H, I, d, P, plan.mt_dn, plan.nchunk, plan.ks_dn, ypart, kk, st);
     MmArgs a{};
     a.w0 = down;
     a.x = act;

@@ -29,55 +29,118 @@ __device__ inline void exp_table_ready(uint64_t warm) { asm volatile("" ::"v"(wa
 
 // ------------------------------------------------------------------ router
 
+// cpu.matmulF16's order fixes, for each (token, expert), eight sequential chains:
+// chain l adds x[8j+l] * f32(w[8j+l]) for j = 0, 1, ... (multiply and add rounded
+// separately); the eight chain sums are then added l = 0..7 in order, then the
+// scalar tail i >= H8 = H & ~7.  The chains cannot be split, so the kernel gives
+// every chain its own lane and makes each lane's operands one contiguous stream:
+// the router is stored lane-major, wt[(8 e + l) J + j] = w[e][8 j + l] with
+// J = H / 8 (router_layout), read 8 j's per 16-byte load; the token's x is staged
+// in LDS the same way, xs[l J + j] = x[8 j + l].  Each lane runs TT tokens' chains
+// at once (independent adds interleave), and the eight lanes of an expert sit in
+// one DPP row for the ordered sum.
+//
 // Block: 256 threads = 32 experts x 8 lanes.  Grid: (ceil(E/32), ceil(T/TT)).
-// Thread (e, l) accumulates x[t][8j+l] * f32(w[e][8j+l]) for j ascending, for TT
-// tokens at once; the 8 lane sums of an expert are then added lane 0..7 in order.
-template <int TT>
-__global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ w, const float *__restrict__ x,
-                                                int T, int E, int H, float *__restrict__ logits)
+__global__ void k_router_layout(const uint16_t *__restrict__ w, int E, int H, uint16_t *__restrict__ wt)
 {
-    extern __shared__ float xs[];  // [TT][H]
+    const int J = H >> 3;
+    const size_t n = (size_t)E * 8 * J;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const size_t e = i / (8 * (size_t)J), r = i % (8 * (size_t)J);
+    const int l = (int)(r / J), j = (int)(r % J);
+    wt[i] = w[e * H + 8 * (size_t)j + l];
+}
+
+template <int TT>
+__global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ wt, const uint16_t *__restrict__ w,
+                                                const float *__restrict__ x, int T, int E, int H,
+                                                float *__restrict__ logits)
+{
+    extern __shared__ float xs[];  // [TT][8][J]
+    const int J = H >> 3, H8 = J * 8;
     const int t0 = blockIdx.y * TT;
     const int nt = min(TT, T - t0);
-    for (int i = threadIdx.x; i < nt * H; i += blockDim.x) xs[i] = x[(size_t)t0 * H + i];
+    for (int t = 0; t < nt; t++)
+        for (int i = threadIdx.x; i < H8; i += blockDim.x) xs[(t * 8 + (i & 7)) * J + (i >> 3)] = x[(size_t)(t0 + t) * H + i];
     __syncthreads();
 
     const int l = threadIdx.x & 7;
     const int e = blockIdx.x * 32 + (threadIdx.x >> 3);
     const bool live = e < E;
-    const uint16_t *row = w + (size_t)(live ? e : 0) * H;
+    const uint16_t *wr = wt + ((size_t)(live ? e : 0) * 8 + l) * J;
     float acc[TT];
 #pragma unroll
     for (int t = 0; t < TT; t++) acc[t] = 0.0f;
-    const int H8 = H & ~7;
-    for (int i = l; i < H8; i += 8) {
-        const float wv = f16_bits_to_f32(row[i]);
+    int j = 0;
+    if ((J & 7) == 0) {
+        // 8 j's per 16-byte load, the next block's load issued before this one's adds
+        const uint4 *w16 = (const uint4 *)wr;
+        uint4 cur = w16[0];
+        for (; j < J; j += 8) {
+            const uint4 nxt = w16[min(j + 8, J - 8) >> 3];
+            const uint32_t ww[4] = {cur.x, cur.y, cur.z, cur.w};
 #pragma unroll
-        for (int t = 0; t < TT; t++)
-            if (t < nt) acc[t] = __fadd_rn(acc[t], __fmul_rn(xs[t * H + i], wv));
+            for (int q = 0; q < 8; q++) {
+                const float wv = f16_bits_to_f32((uint16_t)(ww[q >> 1] >> (16 * (q & 1))));
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+                    acc[t] = __fadd_rn(acc[t], __fmul_rn(xs[(t * 8 + l) * J + j + q], wv));
+            }
+            cur = nxt;
+        }
+    } else {
+        for (; j < J; j++) {
+            const float wv = f16_bits_to_f32(wr[j]);
+#pragma unroll
+            for (int t = 0; t < TT; t++) acc[t] = __fadd_rn(acc[t], __fmul_rn(xs[(t * 8 + l) * J + j], wv));
+        }
     }
     // Ordered lane sum: lane 0 + lane 1 + ... + lane 7, then the scalar tail.
+    const uint16_t *row = w + (size_t)(live ? e : 0) * H;
 #pragma unroll
     for (int t = 0; t < TT; t++) {
         float sum = __shfl(acc[t], (threadIdx.x & ~7), 64);
-        for (int j = 1; j < 8; j++) sum = __fadd_rn(sum, __shfl(acc[t], (threadIdx.x & ~7) + j, 64));
-        for (int i = H8; i < H; i++) sum = __fadd_rn(sum, __fmul_rn(f16_bits_to_f32(row[i]), xs[t * H + i]));
-        if (live && l == 0 && t < nt) logits[(size_t)(t0 + t) * E + e] = sum;
+        for (int q = 1; q < 8; q++) sum = __fadd_rn(sum, __shfl(acc[t], (threadIdx.x & ~7) + q, 64));
+        if (live && l == 0 && t < nt) {
+            for (int i = H8; i < H; i++)
+                sum = __fadd_rn(sum, __fmul_rn(f16_bits_to_f32(row[i]), x[(size_t)(t0 + t) * H + i]));
+            logits[(size_t)(t0 + t) * E + e] = sum;
+        }
     }
 }
 
-int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits, hipStream_t st)
+int launch_router_layout(const uint16_t *d_w, int E, int H, uint16_t *d_wt, hipStream_t st)
+{
+    const size_t n = (size_t)E * (H & ~7);
+    if (!n) return ANEDVD_OK;
+    hipLaunchKernelGGL(k_router_layout, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, d_w, E, H, d_wt);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
+int launch_router(const uint16_t *d_wt, const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits,
+                  hipStream_t st)
 {
     if (T <= 0) return ANEDVD_OK;
-    // Tokens per block sized so the staged activations fit in 64 KiB of LDS.
+    // Tokens per block: enough blocks to spread over the CUs, the staged
+    // activations within 64 KiB of LDS.
     const dim3 block(256);
-    if ((size_t)8 * H * 4 <= 65536) {
-        const dim3 grid((E + 31) / 32, (T + 7) / 8);
-        hipLaunchKernelGGL(k_router<8>, grid, block, (size_t)8 * H * 4, st, d_w, d_x, T, E, H, d_logits);
-    } else if ((size_t)2 * H * 4 <= 65536) {
-        const dim3 grid((E + 31) / 32, (T + 1) / 2);
-        hipLaunchKernelGGL(k_router<2>, grid, block, (size_t)2 * H * 4, st, d_w, d_x, T, E, H, d_logits);
-    } else {
+    const int eb = (E + 31) / 32;
+    auto go = [&](auto tt) -> int {
+        constexpr int TT = decltype(tt)::value;
+        const size_t lds = (size_t)TT * (H & ~7) * 4;
+        if (lds > 65536) return -1;
+        hipLaunchKernelGGL(k_router<TT>, dim3(eb, (T + TT - 1) / TT), block, lds, st, d_wt, d_w, d_x, T, E, H,
+                           d_logits);
+        return 0;
+    };
+    const long blocks1 = (long)eb * T;
+    int rc = -1;
+    if (blocks1 >= 1024) rc = go(std::integral_constant<int, 4>{});
+    if (rc && blocks1 >= 512) rc = go(std::integral_constant<int, 2>{});
+    if (rc) rc = go(std::integral_constant<int, 1>{});
+    if (rc) {
         set_error("router: hidden size %d too large for the staged router", H);
         return ANEDVD_E_INVALID_ARG;
     }

@@ -43,7 +43,12 @@ int launch_f32_to_f16(const float *d_src, uint16_t *d_dst, size_t n, hipStream_t
 // k_route.hip
 constexpr int kMaxRouteExperts = 256;  // experts the route and dispatch kernels take (ids fit a byte)
 constexpr int kMaxRouteSlots = 32;     // slots per token
-int launch_router(const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits, hipStream_t st);
+// cpu.matmulF16 of T rows of x against the [E][H] f16 router: d_wt is the router
+// in the kernel's lane-major layout (launch_router_layout, E * (H & ~7) halves),
+// d_w the [E][H] matrix itself (read only for a tail of H % 8 columns).
+int launch_router_layout(const uint16_t *d_w, int E, int H, uint16_t *d_wt, hipStream_t st);
+int launch_router(const uint16_t *d_wt, const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits,
+                  hipStream_t st);
 // cpu.moeRoute for T rows of logits; with d_x non-null the same launch also
 // converts x [T][H] to the GEMV activation format `xq`.
 // Shared-expert pieces merged into the routed experts: n pieces, experts E..E+n-1,
@@ -66,10 +71,17 @@ int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int no
 int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st);
 
 // k_mm.hip -- expert products on MFMA
+enum MmKind {
+    kMmDecode = 0,   // k_mm_gateup / k_mm_down: 16-token tiles, per-block f32 scales, K split
+    kMmStaged = 1    // k_pf_gateup / k_pf_down: 64-token chunks, activations staged in LDS
+};
 struct MmPlan {
+    int kind;     // MmKind
     int ks_gu;    // K split of gate/up (workgroups per 64-row block)
     int ks_dn;    // K split of down
-    int mt;       // 16-token tiles per workgroup: 1 (decode kernels) or 4 (grouped GEMM, k_pf.hip)
+    int mt;       // 16-token tiles per chunk: 1 (decode), 4 or 8 (grouped GEMM)
+    int mt_gu;    // grouped GEMM: 16-token tiles per gate/up workgroup (4 or 8, at most mt)
+    int mt_dn;    // grouped GEMM: 16-token tiles per down workgroup (4 or 8, at most mt)
     int chunk;    // tokens per work-list chunk (16 mt), the dispatch's `chunk`
     int nchunk;   // bound on the work list's length: P / chunk + max_u
 };
@@ -88,10 +100,14 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
                        const MmPlan &plan, float *ypart, int kk, hipStream_t st);
 // k_pf.hip -- the grouped GEMM for prefill-sized groups (chunks of 16 mt tokens)
 bool grouped_supported(int H, int I);
+bool grouped_wide(int type);  // the type has a 128-token-chunk grouped kernel
+// A workgroup takes 16 mt tokens of a work-list chunk of d.chunk tokens.
 int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
                           int mt, int nchunk, const ActQ &act, int use_gelu, hipStream_t st);
+// With ks > 1 the K axis is split over ks workgroups, each writing plane ks of ypart.
 int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
-                        int nchunk, float *ypart, int kk, hipStream_t st);
+                        int nchunk, int ks, float *ypart, int kk, hipStream_t st);
+bool grouped_down_ks_ok(int type, int I, int ks);  // I/64 steps split into ks whole scale-unit blocks
 
 // k_ops.hip -- cpu.moeExpertAccumF32 / moeExpertAccum on caller weight slices
 // ([inter][hidden] gate and up, [hidden][inter] down; f32, or f16 bits when f16):

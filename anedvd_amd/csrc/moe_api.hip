@@ -52,7 +52,8 @@ struct anedvd_moe_layer {
     uint32_t H = 0, I = 0, E = 0, k = 0;
     int norm = 0, gelu = 0;
     QMat gate{}, up{}, down{};
-    uint16_t *router = nullptr;
+    uint16_t *router = nullptr;    // [E][H] f16
+    uint16_t *router_t = nullptr;  // the router kernel's lane-major copy (launch_router_layout)
     uint32_t Is = 0;
     uint32_t n_sh = 0;  // shared expert merged as n_sh expert-width pieces after the E routed experts
     QMat sgate{}, sup{}, sdown{};  // the shared expert when it is not merged
@@ -321,7 +322,7 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
     mark(0);
     const float *logits = d_logits;
     if (!logits) {
-        ANEDVD_TRY(launch_router(L->router, d_h, T, E, H, f.logits, st));
+        ANEDVD_TRY(launch_router(L->router_t, L->router, d_h, T, E, H, f.logits, st));
         logits = f.logits;
     }
     SharedSlots sh;
@@ -509,12 +510,20 @@ int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *d,
         rc = make_qmat(L->down, d->down_type, H, I, E, d->down, d->down_bytes, ctx->stream, L->device_bytes, "down",
                        sdn, nsh);
     if (!rc) {
-        const size_t rb = (size_t)E * H * 2;
-        if (hipMalloc(&L->router, rb) != hipSuccess || hipMemcpy(L->router, d->router, rb, hipMemcpyHostToDevice) != hipSuccess) {
+        // the router as given ([E][H], for a tail of H % 8 columns) and in the router
+        // kernel's lane-major layout
+        const size_t rb = (size_t)E * H * 2, rtb = (size_t)E * (H & ~7) * 2;
+        if (hipMalloc(&L->router, rb) != hipSuccess || hipMalloc(&L->router_t, rtb) != hipSuccess ||
+            hipMemcpy(L->router, d->router, rb, hipMemcpyHostToDevice) != hipSuccess) {
             set_error("router upload failed");
             rc = ANEDVD_E_HIP;
         }
-        L->device_bytes += rb;
+        if (!rc) rc = launch_router_layout(L->router, E, H, L->router_t, ctx->stream);
+        if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) {
+            set_error("router layout failed");
+            rc = ANEDVD_E_HIP;
+        }
+        L->device_bytes += rb + rtb;
     }
     if (!rc && d->shared_inter) {
         L->Is = d->shared_inter;
@@ -560,6 +569,7 @@ void anedvd_moe_layer_free(anedvd_moe_layer *L)
     free_qmat(L->sup);
     free_qmat(L->sdown);
     if (L->router) (void)hipFree(L->router);
+    if (L->router_t) (void)hipFree(L->router_t);
     if (L->sgate_lin) (void)hipFree(L->sgate_lin);
     delete L;
 }
@@ -678,14 +688,16 @@ int anedvd_matmul_f16(anedvd_moe_ctx *ctx, float *out, const uint16_t *w, const 
     if (!n_vec) return ANEDVD_OK;
     ANEDVD_HIP(hipSetDevice(ctx->device));
     const size_t wb = out_dim * in_dim * 2, xb = n_vec * in_dim * 4, ob = n_vec * out_dim * 4;
-    ANEDVD_TRY(ensure(ctx->io, wb + xb + ob + 1024, ctx->stream));
+    ANEDVD_TRY(ensure(ctx->io, 2 * wb + xb + ob + 1024, ctx->stream));
     Carve c{(uint8_t *)ctx->io.base};
     uint16_t *dw = c.take<uint16_t>(out_dim * in_dim);
+    uint16_t *dwt = c.take<uint16_t>(out_dim * in_dim);
     float *dx = c.take<float>(n_vec * in_dim);
     float *dout = c.take<float>(n_vec * out_dim);
     ANEDVD_HIP(hipMemcpyAsync(dw, w, wb, hipMemcpyHostToDevice, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_TRY(launch_router(dw, dx, (int)n_vec, (int)out_dim, (int)in_dim, dout, ctx->stream));
+    ANEDVD_TRY(launch_router_layout(dw, (int)out_dim, (int)in_dim, dwt, ctx->stream));
+    ANEDVD_TRY(launch_router(dwt, dw, dx, (int)n_vec, (int)out_dim, (int)in_dim, dout, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(out, dout, ob, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
     return ANEDVD_OK;
@@ -873,7 +885,7 @@ int anedvd_moe_layer_route(anedvd_moe_layer *L, const float *h, size_t T, float 
     float *dp = c.take<float>(T * k);
     uint32_t *di = c.take<uint32_t>(T * k);
     ANEDVD_HIP(hipMemcpyAsync(dh, h, T * H * 4, hipMemcpyHostToDevice, ctx->stream));
-    ANEDVD_TRY(launch_router(L->router, dh, (int)T, (int)E, (int)H, dl, ctx->stream));
+    ANEDVD_TRY(launch_router(L->router_t, L->router, dh, (int)T, (int)E, (int)H, dl, ctx->stream));
     ANEDVD_TRY(launch_route(dl, (int)T, (int)E, (int)k, L->norm, dp, di, nullptr, 0, ActQ{}, ctx->stream));
     if (logits) ANEDVD_HIP(hipMemcpyAsync(logits, dl, T * E * 4, hipMemcpyDeviceToHost, ctx->stream));
     ANEDVD_HIP(hipMemcpyAsync(probs, dp, T * k * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -937,7 +949,9 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *L, const float *h, size_t T, cons
         stats->touched_experts = (uint32_t)touched;
         stats->max_group = (uint32_t)meta[1];
         stats->weight_bytes = (uint64_t)(touched * L->expert_bytes + L->shared_bytes + (logits ? 0.0 : 2.0 * L->E * L->H));
-        stats->path = f.plan.mt > 1 ? 1 : 0;
+        stats->path = f.plan.kind == kMmStaged ? 1 : 0;
+        stats->chunk = (uint32_t)f.plan.chunk;
+        stats->down_ks = (uint32_t)f.plan.ks_dn;
     }
     return ANEDVD_OK;
 }
@@ -1180,7 +1194,7 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
             auto launch = [&](int i) -> int {
                 const anedvd_moe_layer *L = layers[(size_t)i % n_layers];
                 if (s == 2)  // the router GEMV alone: T tokens of d_h against the layer's [E][H] f16 router
-                    return launch_router(L->router, d_h, (int)T, (int)L->E, H, f.logits, st);
+                    return launch_router(L->router_t, L->router, d_h, (int)T, (int)L->E, H, f.logits, st);
                 return s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act,
                                                      L->gelu, st)
                               : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart,

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define ANEDVD_MOE_ABI_VERSION 2
+#define ANEDVD_MOE_ABI_VERSION 3
 
 /* ggml tensor type ids as stored in GGUF (gguf.zig:30-46). */
 enum anedvd_ggml_type {
@@ -86,7 +86,9 @@ typedef struct {
     uint32_t touched_experts;      /* experts with >= 1 routed token in this call */
     uint64_t weight_bytes;         /* expert + shared + router bytes the call had to read */
     uint32_t max_group;            /* largest tokens-per-expert group */
-    uint32_t path;                 /* 0 = decode GEMV, 1 = prefill grouped GEMM */
+    uint32_t path;                 /* expert kernels: 0 = decode (16-token tiles), 1 = grouped GEMM */
+    uint32_t chunk;                /* tokens per expert-kernel work item: 16, 64 or 128 */
+    uint32_t down_ks;              /* K shares of the down product (partial planes the combine adds) */
 } anedvd_moe_stats;
 
 /* ------------------------------------------------------------------ lifetime */

@@ -167,7 +167,7 @@ def test_prefill_agrees_with_per_token_decode(ctx, spec):
     T = 600
     h = synth.activations(spec, T, seed=21)
     whole, st = layer.forward(h, stats=True)
-    assert st["path"] == 1
+    assert st["path"] >= 1
     _, p_all, i_all = layer.route(h)
     pieces = []
     for t0 in range(0, T, 16):
