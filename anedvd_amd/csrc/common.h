@@ -208,6 +208,9 @@ __device__ inline float pow2_scale(float maxabs)
     return __int_as_float((p + 127) << 23);
 }
 
+// 1 / s for a power of two s = 2^p, |p| <= 126: 2^-p, exact, from the exponent bits.
+__device__ inline float pow2_recip(float s) { return __int_as_float(0x7F000000 - __float_as_int(s)); }
+
 template <int CTRL>
 __device__ inline float dpp_f32(float v)
 {

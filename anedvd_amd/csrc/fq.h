@@ -49,9 +49,25 @@ __device__ inline uint32_t h2_bits(h2 h)
 }
 
 
+// Where a wavefront's four 16-row tiles come from: tile tt is tile idx(tt) of row
+// block rb of planes src(tt).  One matrix's whole 64-row block (Tiles1), or two
+// tiles each of two matrices of the same shape (Tiles2: gate and up, tiles t0 and
+// t0 + 1).  tt is a compile-time index in every use, so the choice folds away.
+struct Tiles1 {
+    Planes p;
+    __device__ const Planes &src(int) const { return p; }
+    __device__ int idx(int tt) const { return tt; }
+};
+struct Tiles2 {
+    Planes g, u;
+    int t0;
+    __device__ const Planes &src(int tt) const { return tt < 2 ? g : u; }
+    __device__ int idx(int tt) const { return t0 + (tt & 1); }
+};
+
 // ------------------------------------------------------------------ decoders
 //
-// A decoder loads one step of a wavefront's four row tiles (a 64-row block): load();
+// A decoder loads one step of a wavefront's four row tiles: load();
 // takes what stays valid for a whole scale unit on the unit's first step: begin();
 // and yields the f16 B operand of (tile tt, block j) at step `ss` of the unit:
 // bop().  Lane l = 16 g + n holds row n of the tile and the 8 columns 32 j + 8 g + i.
@@ -66,14 +82,16 @@ struct FF16 {
         u32x4 q[kPfTiles][2];
     };
     struct State {};
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    template <class TS>
+    __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
-        const int qo = lane_plane_off(p, rb, s, 32);
+        const int qo = lane_plane_off(ts.src(0), rb, s, 32);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++)
 #pragma unroll
             for (int j = 0; j < 2; j++)
-                r.q[tt][j] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 32 * lane, qo + 2048 * tt + 16 * j, kNT);
+                r.q[tt][j] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).q, 32 * lane, qo + 2048 * ts.idx(tt) + 16 * j,
+                                                                   kNT);
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
     __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int) { return as_h8(r.q[tt][j]); }
@@ -89,13 +107,14 @@ struct FQ8_0 {
         uint32_t s[kPfTiles];
     };
     struct State {};
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    template <class TS>
+    __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
-        const int qo = lane_plane_off(p, rb, s, 16), so = row_plane_off(p, rb, s, 4);
+        const int qo = lane_plane_off(ts.src(0), rb, s, 16), so = row_plane_off(ts.src(0), rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.q, 16 * lane, qo + 1024 * tt, kNT);
-            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * tt, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).q, 16 * lane, qo + 1024 * ts.idx(tt), kNT);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ts.idx(tt), kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -116,13 +135,14 @@ struct FQ4_0 {
         uint32_t s[kPfTiles];
     };
     struct State {};
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    template <class TS>
+    __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
-        const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, 4);
+        const int qo = lane_plane_off(ts.src(0), rb, s, 8), so = row_plane_off(ts.src(0), rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
-            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * tt, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kNT);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ts.idx(tt), kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -149,22 +169,25 @@ struct FQLegacy {
         u32x2 s[kPfTiles];  // (d0 | m0 << 16, d1 | m1 << 16) with a min, else (d0 | d1 << 16, -)
     };
     struct State {};
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    template <class TS>
+    __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
+        const Planes &p = ts.src(0);
         const int qo = lane_plane_off(p, rb, s, 8), so = row_plane_off(p, rb, s, kHasMin ? 8 : 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
+            const int ti = ts.idx(tt);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ti, kNT);
             if constexpr (kHasMin)
-                r.s[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.s, 8 * (lane & 15), so + 128 * tt, kNT);
+                r.s[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).s, 8 * (lane & 15), so + 128 * ti, kNT);
             else
-                r.s[tt].x = __builtin_amdgcn_raw_buffer_load_b32(p.s, 4 * (lane & 15), so + 64 * tt, kNT);
+                r.s[tt].x = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ti, kNT);
         }
         if constexpr (kFive) {
             const int ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, ho + 128 * tt, kNT);
+                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, ho + 128 * ts.idx(tt), kNT);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -206,16 +229,19 @@ struct FQ4_K {
     struct State {
         uint32_t dm[kPfTiles][8];  // f16 d1 | f16 (-m1) << 16 per (tile, sub-block)
     };
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    template <class TS>
+    __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
+        const Planes &p = ts.src(0);
         const int qo = lane_plane_off(p, rb, s, 8);
 #pragma unroll
-        for (int tt = 0; tt < kPfTiles; tt++) r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
+        for (int tt = 0; tt < kPfTiles; tt++)
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kNT);
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * tt, kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ts.idx(tt), kNT);
         }
     }
     // The 6-bit scales and mins of getScaleMinK4 (gguf.zig:948-958) for all eight
@@ -270,19 +296,21 @@ struct FQ5_K {
         u32x4 sc[kPfTiles];  // d, dmin, scales: loaded on a unit's first step
     };
     using State = FQ4_K::State;
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    template <class TS>
+    __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
+        const Planes &p = ts.src(0);
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
-            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, ho + 128 * tt, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kNT);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, ho + 128 * ts.idx(tt), kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * tt, kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ts.idx(tt), kNT);
         }
     }
     __device__ static inline void begin(const Raw &r, State &st, int ss, int lane)
@@ -322,24 +350,29 @@ struct FQ23K {
     struct State {
         half_t dl[kPfTiles][8], ml[kPfTiles][8];  // [tt][2 ss + j] of the lane's sub-block 4 ss + 2 j + g / 2
     };
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    template <class TS>
+    __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
+        const Planes &p = ts.src(0);
         const int qo = lane_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.q, 4 * lane, qo + 256 * tt, kNT);
+            const int ti = ts.idx(tt);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).q, 4 * lane, qo + 256 * ti, kNT);
             if constexpr (kThree)
-                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.h, 2 * lane, lane_plane_off(p, rb, s, 2) + 128 * tt, kNT);
+                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, lane_plane_off(p, rb, s, 2) + 128 * ti,
+                                                               kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, kThree ? 2 : 4);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++) {
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * tt, kNT);
+                const int ti = ts.idx(tt);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ti, kNT);
                 if constexpr (kThree)
-                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15), dof + 32 * tt, kNT);
+                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).d, 2 * (lane & 15), dof + 32 * ti, kNT);
                 else
-                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.d, 4 * (lane & 15), dof + 64 * tt, kNT);
+                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).d, 4 * (lane & 15), dof + 64 * ti, kNT);
             }
         }
     }
@@ -397,20 +430,23 @@ struct FQ6_K {
     struct State {
         uint32_t dsc[kPfTiles][4];  // f16 pairs; [tt][k / 2] half k % 2 (k = 2 ss + j): d * sc of the lane's sub-block 2 k + g / 2
     };
-    __device__ static inline void load(Raw &r, const Planes &p, int rb, int s, int lane)
+    template <class TS>
+    __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
+        const Planes &p = ts.src(0);
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(p.q, 8 * lane, qo + 512 * tt, kNT);
-            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(p.h, 4 * lane, ho + 256 * tt, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kNT);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).h, 4 * lane, ho + 256 * ts.idx(tt), kNT);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, 2);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++) {
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(p.s, 16 * (lane & 15), so + 256 * tt, kNT);
-                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(p.d, 2 * (lane & 15), dof + 32 * tt, kNT);
+                const int ti = ts.idx(tt);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ti, kNT);
+                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).d, 2 * (lane & 15), dof + 32 * ti, kNT);
             }
         }
     }

@@ -13,6 +13,8 @@
 //   - activations carry one power of two per row (x as converted; the SwiGLU
 //     activations are rescaled to their row's largest descale while staged), so
 //     nothing is rescaled inside the K loop.
+#include <type_traits>
+
 #include "common.h"
 #include "fq.h"
 #include "kernels.h"
@@ -128,15 +130,15 @@ __device__ inline void stage_store(const S &st, int b, half_t *dst)
 // compile-time indices.  Weight loads past the last step go out of range (zero, no
 // memory traffic).  s0 is a multiple of four (a scale unit starts there); the
 // staging offsets already point at step s0.
-template <class F, int MT, int MTL, class S>
-__device__ inline void pf_loop(const Planes &W, int rb, int s0, int steps, int lane, S &stage, half_t *abuf,
+template <class F, int MT, int MTL, class TS, class S>
+__device__ inline void pf_loop(const TS &W, int rb, int s0, int steps, int lane, S &stage, half_t *abuf,
                                int srow, f32x4 (*acc)[MT])
 {
     constexpr int U = 4;
     constexpr int BUF = 16 * MT * kAStride;
     static_assert(U % F::kSpu == 0, "a scale unit must fit an unrolled block");
     const int n = lane & 15, g = lane >> 4;
-    const int so = (W.nrb - rb) * W.steps;
+    const int so = (W.src(0).nrb - rb) * W.src(0).steps;
     auto ws = [&](int x) { return x < steps ? s0 + x : so; };
     constexpr int D = F::kDepth, DA = F::kStageDepth;
     constexpr int R = D == 1 ? 2 : 4;    // ring of weight slots; divides the unrolled block
@@ -240,8 +242,8 @@ __device__ inline void pf_loop(const Planes &W, int rb, int s0, int steps, int l
 // pf_loop for the chunk's live 16-token tiles (uniform over the workgroup): one
 // instantiation per count, so a step holds no branch and the compiler may
 // interleave the dequantisation with the MFMAs.
-template <class F, int MT, int L = MT, class S>
-__device__ inline void pf_loop_live(const Planes &W, int rb, int s0, int steps, int lane, S &stage, half_t *abuf,
+template <class F, int MT, int L = MT, class TS, class S>
+__device__ inline void pf_loop_live(const TS &W, int rb, int s0, int steps, int lane, S &stage, half_t *abuf,
                                     int srow, int mt_live, f32x4 (*acc)[MT])
 {
     if constexpr (L > 1) {
@@ -282,43 +284,42 @@ __device__ inline bool pf_chunk(const Dispatch &d, int w, int sub, int &e, int &
     return true;
 }
 
-// LDS of one workgroup: the two staged activation tiles during the K loop, then
-// (gate/up) the gate and up results of 64 tokens x 64 rows at a time.
+// LDS of one workgroup: the two staged activation tiles of the K loop.
 template <int MT>
 struct PfLds {
-    static constexpr int kA = 2 * 16 * MT * kAStride * 2;        // bytes
-    static constexpr int kEpi = 2 * 64 * (kRowBlock + 1) * 4;    // bytes
-    static constexpr int kBytes = kA > kEpi ? kA : kEpi;
+    static constexpr int kA = 2 * 16 * MT * kAStride * 2;  // bytes
 };
 
 // ------------------------------------------------------------ gate / up
 
-// Grid nchunk * I/128 workgroups of 256 threads, chunks fastest.  Wave w: matrix
-// w & 1 (gate, up) of row block 2 x + (w >> 1), x the workgroup's row-block pair.
-// After the K loop the gate and up results of one row block at a time go through
-// LDS (64 tokens x 64 rows each, as many passes as 64-token groups); each
-// wavefront then applies SiLU(g) * u to 16 of the tokens and writes them in the
-// activation format (one 64-column group per token).
+// Grid nchunk * sub * I/128 workgroups of 256 threads, chunks fastest.  Wave w:
+// tiles t0 = 2 (w & 1) and t0 + 1 of both gate and up of row block 2 x + (w >> 1),
+// x the workgroup's row-block pair, so SiLU(g) * u forms in registers.  A token's
+// 64-column activation group (one row block) is split over the wavefront pair
+// (w, w ^ 1): each takes its 32 columns' largest magnitude (in-lane over two tiles,
+// DPP over the 16 lanes of a row), the pair meets in LDS, and each writes its 32
+// columns scaled by the group's power of two.
 template <class F, int MT>
 __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
 {
     constexpr int R = MT / 4;
     __shared__ float dvs[16 * MT];
-    __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kBytes];
+    __shared__ float gmax[4][16 * MT];  // per wavefront: its 32 columns' largest |act| per token
+    __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
     int e, p0, nt;
     const int nw = a.nchunk * a.sub;
     if (!pf_chunk<MT>(a.d, (int)(blockIdx.x % nw), a.sub, e, p0, nt)) return;  // uniform over the workgroup
     const int rbg = (int)(blockIdx.x / nw);
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const int mat = wv & 1, half = wv >> 1, rb = 2 * rbg + half;
-    const Planes W = planes(mat ? a.w1 : a.w0, e);
+    const int t0 = 2 * (wv & 1), rb = 2 * rbg + (wv >> 1);
+    const Tiles2 W{planes(a.w0, e), planes(a.w1, e), t0};
     half_t *abuf = (half_t *)smem;
     const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
     StageX<R, F::kStageDepth == 1 ? 2 : 4> stage;
     stage.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
 #pragma unroll
     for (int h = 0; h < R; h++) stage.off[h] = a.d.rows[p0 + min(r + 64 * h, nt - 1)] * a.H * 2 + 32 * q;
-    f32x4 acc[kPfTiles][MT];
+    f32x4 acc[kPfTiles][MT];  // [0, 1]: gate tiles t0, t0 + 1; [2, 3]: up
 #pragma unroll
     for (int tt = 0; tt < kPfTiles; tt++)
 #pragma unroll
@@ -330,44 +331,58 @@ __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
 
     if ((int)threadIdx.x < 16 * MT) dvs[threadIdx.x] = tdv;
     __syncthreads();
-    float dv[MT][4];
+    // act = SiLU(g dv) * (u dv) over the gate accumulators (token tiles past the
+    // chunk's live ones hold zeros, and stay zero); the activation choice is
+    // uniform, taken once outside the unrolled loops
+    auto act_pass = [&](auto gelu) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * mt + 4 * g + i;
+                const float dv = dvs[m];
+                float mx = 0.0f;
+#pragma unroll
+                for (int tp = 0; tp < 2; tp++) {
+                    const float v = gate_act(acc[tp][mt][i] * dv, decltype(gelu)::value) * (acc[2 + tp][mt][i] * dv);
+                    acc[tp][mt][i] = v;
+                    mx = fmaxf(mx, fabsf(v));
+                }
+                mx = row_max_f32(mx);
+                if (n == 0) gmax[wv][m] = mx;
+            }
+    };
+    if (a.use_gelu) act_pass(std::true_type{});
+    else act_pass(std::false_type{});
+    __syncthreads();
+    // Lane n even stores the f16 pair of columns (n, n + 1), adjacent in the
+    // activation format, through a buffer descriptor: the token row's offset is
+    // scalar, the lane's row and column offset fixed.
+    const bool even = (n & 1) == 0;
+    const rsrc_t aq = make_rsrc(a.act.q, (size_t)a.P * a.I * 2);
+    const rsrc_t ads = make_rsrc(a.act.ds, (size_t)(a.I / kStep) * a.act.ld * 4);
+    const int lrow = 4 * g * a.I * 2;
+    const int col[2] = {2 * (kStep * rb + mma_pos(16 * t0 + n)), 2 * (kStep * rb + mma_pos(16 * (t0 + 1) + n))};
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) dv[mt][i] = dvs[16 * mt + 4 * g + i];
-    // results * the tokens' descales -> LDS [mat][token][row]: one row block and 64
-    // tokens per pass
-    float *res = (float *)smem;
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * mt + 4 * g + i;
+            const float sc = pow2_scale(fmaxf(gmax[wv][m], gmax[wv ^ 1][m]));
+            const int srow = (p0 + 16 * mt + i) * a.I * 2;  // uniform
 #pragma unroll
-    for (int hb = 0; hb < 2; hb++) {
-#pragma unroll
-        for (int h = 0; h < R; h++) {
-            if (half == hb) {
-#pragma unroll
-                for (int mq = 0; mq < 4; mq++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int m = 16 * mq + 4 * g + i;
-#pragma unroll
-                        for (int tt = 0; tt < kPfTiles; tt++)
-                            res[(mat * 64 + m) * (kRowBlock + 1) + 16 * tt + n] = acc[tt][4 * h + mq][i] * dv[4 * h + mq][i];
-                    }
-            }
-            __syncthreads();
-            const int rbo = 2 * rbg + hb;
-            for (int m = 16 * wv; m < 16 * wv + 16; m++) {  // uniform per wavefront
-                const float gv = res[m * (kRowBlock + 1) + lane], uv = res[(64 + m) * (kRowBlock + 1) + lane];
-                const float v = gate_act(gv, a.use_gelu) * uv;
-                const float sc = pow2_scale(wave_max(fabsf(v)));
-                if (64 * h + m < nt) {
-                    const size_t pos = (size_t)p0 + 64 * h + m;
-                    a.act.q[pos * a.I + (size_t)kStep * rbo + mma_pos(lane)] = (half_t)(v * sc);
-                    if (lane == 0) a.act.ds[(size_t)rbo * a.act.ld + pos] = 1.0f / sc;
+            for (int tp = 0; tp < 2; tp++) {
+                const float v = acc[tp][mt][i] * sc;
+                const float vn = dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]: lane n ^ 1's value
+                if (m < nt && even) {
+                    const h2 pr = {(half_t)v, (half_t)vn};
+                    __builtin_amdgcn_raw_buffer_store_b32(h2_bits(pr), aq, lrow + col[tp], srow, 0);
                 }
             }
-            __syncthreads();
+            if (m < nt && t0 == 0 && n == 0)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pow2_recip(sc)), ads, 16 * g,
+                                                      (rb * a.act.ld + p0 + 16 * mt + i) * 4, 0);
         }
-    }
 }
 
 // ---------------------------------------------------------------- down
@@ -393,7 +408,7 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int rb = 4 * rbg + wv;
     const int ksteps = a.I / kStep / a.ks, s0 = kq * ksteps;  // this workgroup's K share
-    const Planes W = planes(a.w0, e);
+    const Tiles1 W{planes(a.w0, e)};
     const int G = a.I / kStep, ld = a.x.ld;
     {
         // the row references: thread (part, m) takes every NP-th group of position m,
