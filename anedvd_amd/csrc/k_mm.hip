@@ -961,6 +961,7 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u)
         const long r1 = (dn_wgs + 2 * kCUs - 1) / (2 * kCUs), r2 = (2 * dn_wgs + 2 * kCUs - 1) / (2 * kCUs);
         p.ks_dn = I / kStep >= 128 && 10 * r2 <= 18 * r1 && grouped_down_ks_ok(down_type, I, 2) ? 2 : 1;
         p.mt = std::max(p.mt_gu, p.mt_dn);
+        p.contig = P >= 2 * 16 * p.mt * (long)max_u;  // experts average two chunks or more
     } else {
         p.kind = kMmDecode;
         p.mt = 1;
@@ -1017,7 +1018,7 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
                          const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st)
 {
     if (plan.kind == kMmStaged)
-        return launch_grouped_gateup(gate, up, x, H, I, d, P, plan.mt_gu, plan.nchunk, act, use_gelu, st);
+        return launch_grouped_gateup(gate, up, x, H, I, d, P, plan.mt_gu, plan.nchunk, plan.contig, act, use_gelu, st);
     if (gate.type != up.type) {
         set_error("expert gate/up: gate type %d and up type %d differ", gate.type, up.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
@@ -1068,7 +1069,8 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
         return ANEDVD_E_INVALID_ARG;
     }
     if (plan.kind == kMmStaged)
-        return launch_grouped_down(down, act, H, I, d, P, plan.mt_dn, plan.nchunk, plan.ks_dn, ypart, kk, st);
+        return launch_grouped_down(down, act, H, I, d, P, plan.mt_dn, plan.nchunk, plan.contig, plan.ks_dn, ypart, kk,
+                                   st);
     MmArgs a{};
     a.w0 = down;
     a.x = act;

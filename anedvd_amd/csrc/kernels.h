@@ -82,6 +82,7 @@ struct MmPlan {
     int mt;       // 16-token tiles per chunk: 1 (decode), 4 or 8 (grouped GEMM)
     int mt_gu;    // grouped GEMM: 16-token tiles per gate/up workgroup (4 or 8, at most mt)
     int mt_dn;    // grouped GEMM: 16-token tiles per down workgroup (4 or 8, at most mt)
+    int contig;   // grouped GEMM: XCD-contiguous workgroup order
     int chunk;    // tokens per work-list chunk (16 mt), the dispatch's `chunk`
     int nchunk;   // bound on the work list's length: P / chunk + max_u
 };
@@ -102,11 +103,12 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
 bool grouped_supported(int H, int I);
 bool grouped_wide(int type);  // the type has a 128-token-chunk grouped kernel
 // A workgroup takes 16 mt tokens of a work-list chunk of d.chunk tokens.
+// contig: XCD-contiguous workgroup order (experts averaging two or more chunks).
 int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
-                          int mt, int nchunk, const ActQ &act, int use_gelu, hipStream_t st);
+                          int mt, int nchunk, int contig, const ActQ &act, int use_gelu, hipStream_t st);
 // With ks > 1 the K axis is split over ks workgroups, each writing plane ks of ypart.
 int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
-                        int nchunk, int ks, float *ypart, int kk, hipStream_t st);
+                        int nchunk, int contig, int ks, float *ypart, int kk, hipStream_t st);
 bool grouped_down_ks_ok(int type, int I, int ks);  // I/64 steps split into ks whole scale-unit blocks
 
 // k_ops.hip -- cpu.moeExpertAccumF32 / moeExpertAccum on caller weight slices
