@@ -78,6 +78,7 @@ struct FF16 {
     static constexpr bool kHoistA = false;  // 32 VGPRs of values per ring slot already
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
+    static constexpr int kMinLoads = 8;                    // load instructions of every load() call
     struct Raw {
         u32x4 q[kPfTiles][2];
     };
@@ -102,6 +103,7 @@ struct FQ8_0 {
     static constexpr bool kHoistA = false;  // at 176 VGPRs two waves per SIMD instead of three
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
+    static constexpr int kMinLoads = 8;
     struct Raw {
         u32x4 q[kPfTiles];
         uint32_t s[kPfTiles];
@@ -130,6 +132,7 @@ struct FQ4_0 {
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
+    static constexpr int kMinLoads = 8;
     struct Raw {
         u32x2 q[kPfTiles];
         uint32_t s[kPfTiles];
@@ -163,6 +166,7 @@ struct FQLegacy {
     static constexpr bool kHoistA = !kFive;  // the 5-bit formats: three waves per SIMD without it
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
+    static constexpr int kMinLoads = kFive ? 12 : 8;
     struct Raw {
         u32x2 q[kPfTiles];
         uint32_t h[kFive ? kPfTiles : 1];
@@ -222,6 +226,7 @@ struct FQ4_K {
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
+    static constexpr int kMinLoads = 4;                    // the scales come on a unit's first step only
     struct Raw {
         u32x2 q[kPfTiles];
         u32x4 sc[kPfTiles];  // d, dmin, scales: loaded on a unit's first step
@@ -290,6 +295,7 @@ struct FQ5_K {
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
+    static constexpr int kMinLoads = 8;
     struct Raw {
         u32x2 q[kPfTiles];
         uint32_t h[kPfTiles];
@@ -341,6 +347,7 @@ struct FQ23K {
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
+    static constexpr int kMinLoads = kThree ? 8 : 4;
     struct Raw {
         uint32_t q[kPfTiles];
         uint32_t h[kThree ? kPfTiles : 1];
@@ -421,6 +428,7 @@ struct FQ6_K {
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
     static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
+    static constexpr int kMinLoads = 8;
     struct Raw {
         u32x2 q[kPfTiles];
         uint32_t h[kPfTiles];

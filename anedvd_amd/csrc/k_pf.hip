@@ -255,6 +255,176 @@ __device__ inline void pf_loop_live(const TS &W, int rb, int s0, int steps, int 
     pf_loop<F, MT, L>(W, rb, s0, steps, lane, stage, abuf, srow, acc);
 }
 
+// ------------------------------------------------------------ direct-to-LDS staging
+
+// The gate/up activations (x rows gathered through the dispatch, one power of two
+// per row, so they need no rescaling) go from memory straight to LDS with
+// buffer_load_dwordx4 ... lds: no register ring, so a step's activations are
+// requested kXDepth steps ahead.  Four ring slots, one per unrolled step, each its
+// own LDS array; a slot holds 16 MT token rows of 128 bytes (the step's 64
+// columns), row r's 16-byte piece p at physical piece p ^ x_sw(r), so the MFMA
+// operand reads of 8 or 16 consecutive rows hit distinct banks.  The hardware
+// writes lane l of such a load at byte 16 l of its 1 KiB destination: a
+// wavefront's load fills 8 rows, lane l the physical piece l % 8 of row l / 8.
+#ifndef ANEDVD_PF_DMA
+#define ANEDVD_PF_DMA 1
+#endif
+constexpr int kXDepth = 3;
+
+__device__ inline int x_sw(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int MT>
+struct DmaX {
+    static constexpr int kInst = MT / 2;  // loads per wavefront per step: 16 MT rows x 128 B / 4 wavefronts / 1 KiB
+    rsrc_t q;
+    int off[kInst];  // load i: the lane's token row base + its logical piece (bytes)
+    int dst;         // this wavefront's first destination byte in a slot
+};
+
+template <int MT>
+__device__ inline void x_issue(const DmaX<MT> &x, half_t *slot, int s)
+{
+#if __HIP_DEVICE_COMPILE__  // the compiler's host pass has no LDS-pointer builtins
+#pragma unroll
+    for (int i = 0; i < DmaX<MT>::kInst; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(x.q, (lds_void *)((char *)slot + x.dst + 1024 * i), 16, x.off[i],
+                                                 s * 2 * kStep, 0, 0);
+#endif
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt at their maxima: no wait).
+template <int N>
+__device__ inline void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Waits until the activation loads of the next step are done, given what this
+// wavefront issued after them: two weight load() calls of at least F::kMinLoads
+// instructions each, and c activation steps of kInst loads.  (VMEM loads complete
+// in order; counting fewer than were issued only waits longer.)
+template <class F, int MT>
+__device__ inline void x_wait(int c)
+{
+    constexpr int kI = DmaX<MT>::kInst, kW = F::kMinLoads;
+    if (c == 2) wait_vm<2 * kW + 2 * kI>();
+    else if (c == 1) wait_vm<2 * kW + kI>();
+    else wait_vm<2 * kW>();
+}
+
+// The workgroup barrier of the direct-to-LDS loop.  __syncthreads() would wait
+// for every load into LDS in flight (its release fence covers them); the loop's
+// own vmcnt wait has covered the next step's, and no other LDS write precedes the
+// barrier.  The acquire fence after it keeps the next step's LDS reads below it.
+__device__ inline void x_barrier()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Weight steps in flight ahead in the direct-to-LDS loop.  The compiler's own
+// waits for a weight load do not count the activation loads issued after it (it
+// treats them as no vector-memory result), so they also wait for whatever of
+// those is older than the loads it does count: with the weights two steps ahead
+// and issued before each step's activation loads, that is the next step's
+// activations, which the barrier needs anyway.
+#ifndef ANEDVD_PF_DMA_WD
+#define ANEDVD_PF_DMA_WD 2
+#endif
+
+// pf_loop with the activations in the direct-to-LDS ring.  Per step s the
+// wavefront issues the weight loads of step s + D, then the activation loads of
+// step s + 3; before the barrier that ends step s it waits for step s + 1's
+// activation loads, issued two steps earlier: younger than them are the weight
+// loads issued at steps s - 1 and s and the activation loads of steps s + 2 and
+// s + 3 that exist.  The slot step s + 4 will fill is the one step s reads, free
+// after that barrier.
+template <class F, int MT, int MTL, class TS>
+__device__ inline void pf_loop_dma(const TS &W, int rb, int steps, int lane, const DmaX<MT> &x, half_t *xs0,
+                                   half_t *xs1, half_t *xs2, half_t *xs3, f32x4 (*acc)[MT])
+{
+    constexpr int U = 4, DA = kXDepth;
+    static_assert(U % F::kSpu == 0, "a scale unit must fit an unrolled block");
+    // (F16's 128-byte weight slots stay one step ahead: two more of them would not fit)
+    constexpr int DW = sizeof(typename F::Raw) <= 80 ? ANEDVD_PF_DMA_WD : 1;
+    constexpr int D = F::kDepth > DW ? F::kDepth : DW;
+    constexpr int R = D == 1 ? 2 : 4;
+    static_assert(D >= 1 && D <= 3, "at most three steps ahead");
+    const int n = lane & 15, g = lane >> 4;
+    const int so = (W.src(0).nrb - rb) * W.src(0).steps;
+    auto ws = [&](int v) { return v < steps ? v : so; };
+    auto slot = [&](int b) { return b == 0 ? xs0 : b == 1 ? xs1 : b == 2 ? xs2 : xs3; };  // b a constant
+    typename F::Raw w[R];
+    typename F::State st;
+#pragma unroll
+    for (int v = -DA; v < 0; v++) {  // the steady state's order: weights of v + D, activations of v + DA
+        if (v + D >= 0) F::load(w[(v + D) % R], W, rb, ws(v + D), lane);
+        if (v + DA < steps) x_issue(x, slot((v + DA) & 3), v + DA);
+    }
+    // step 0's activations: younger than them are the weight loads of the
+    // virtual steps -2 and -1 that exist (min(D, 2) calls) and the activation
+    // loads of steps 1 and 2 (not counted: only stricter)
+    wait_vm<(D >= 2 ? 2 : 1) * F::kMinLoads>();
+    x_barrier();
+    // the lane's operand offsets in a slot (halves): row n of a token tile, piece 2 g + j
+    const int ao0 = n * 64 + (((2 * g) ^ x_sw(n)) << 3), ao1 = n * 64 + (((2 * g + 1) ^ x_sw(n)) << 3);
+    for (int s0 = 0; s0 < steps; s0 += U) {
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            const int s = s0 + k;
+            if (s >= steps) break;  // uniform
+            F::load(w[(k + D) % R], W, rb, ws(s + D), lane);
+            if (s + DA < steps) x_issue(x, slot((k + DA) & 3), s + DA);
+            __builtin_amdgcn_sched_barrier(0);
+            const int ss = k % F::kSpu;
+            const half_t *a = slot(k);
+            F::begin(w[k % R], st, ss, lane);
+            half8 av[2][MT];
+            if constexpr (F::kHoistA) {
+#pragma unroll
+                for (int mt = 0; mt < MTL; mt++) {
+                    av[0][mt] = *(const half8 *)(a + mt * 16 * 64 + ao0);
+                    av[1][mt] = *(const half8 *)(a + mt * 16 * 64 + ao1);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                half8 b[kPfTiles];
+#pragma unroll
+                for (int tt = 0; tt < kPfTiles; tt++) b[tt] = F::bop(w[k % R], st, ss, tt, j, lane);
+#pragma unroll
+                for (int mt = 0; mt < MTL; mt++) {
+                    if constexpr (!F::kHoistA) av[j][mt] = *(const half8 *)(a + mt * 16 * 64 + (j ? ao1 : ao0));
+#pragma unroll
+                    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av[j][mt], b[tt], acc[tt][mt]);
+                }
+            }
+            if (s + 1 < steps) {
+                x_wait<F, MT>((s + 2 < steps) + (s + 3 < steps));
+                x_barrier();
+            }
+        }
+    }
+}
+
+template <class F, int MT, int L = MT, class TS>
+__device__ inline void pf_loop_dma_live(const TS &W, int rb, int steps, int lane, const DmaX<MT> &x, half_t *xs0,
+                                        half_t *xs1, half_t *xs2, half_t *xs3, int mt_live, f32x4 (*acc)[MT])
+{
+    if constexpr (L > 1) {
+        if (mt_live < L) {
+            pf_loop_dma_live<F, MT, L - 1>(W, rb, steps, lane, x, xs0, xs1, xs2, xs3, mt_live, acc);
+            return;
+        }
+    }
+    pf_loop_dma<F, MT, L>(W, rb, steps, lane, x, xs0, xs1, xs2, xs3, acc);
+}
+
 struct PfArgs {
     QMat w0, w1;  // gate, up (or down in w0)
     ActQ x;       // gate/up input (tokens) or down input (positions)
@@ -327,10 +497,11 @@ struct PfLds {
 template <class F, int MT>
 __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
 {
-    constexpr int R = MT / 4;
     __shared__ float dvs[16 * MT];
     __shared__ float gmax[4][16 * MT];  // per wavefront: its 32 columns' largest |act| per token
+#if !ANEDVD_PF_DMA
     __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
+#endif
     int e, p0, nt, w, rbg;
     const int nw = a.nchunk * a.sub;
     pf_item((int)blockIdx.x, pf_nw8(nw), a.contig, w, rbg);
@@ -338,12 +509,6 @@ __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int t0 = 2 * (wv & 1), rb = 2 * rbg + (wv >> 1);
     const Tiles2 W{planes(a.w0, e), planes(a.w1, e), t0};
-    half_t *abuf = (half_t *)smem;
-    const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
-    StageX<R, F::kStageDepth == 1 ? 2 : 4> stage;
-    stage.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
-#pragma unroll
-    for (int h = 0; h < R; h++) stage.off[h] = a.d.rows[p0 + min(r + 64 * h, nt - 1)] * a.H * 2 + 32 * q;
     f32x4 acc[kPfTiles][MT];  // [0, 1]: gate tiles t0, t0 + 1; [2, 3]: up
 #pragma unroll
     for (int tt = 0; tt < kPfTiles; tt++)
@@ -351,8 +516,29 @@ __global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
         for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     // token m's descale for the epilogue, loaded by thread m before the K loop
     const float tdv = (int)threadIdx.x < 16 * MT ? a.x.ds[a.d.rows[p0 + min((int)threadIdx.x, nt - 1)]] : 0.0f;
-    pf_loop_live<F, MT>(W, rb, 0, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q,
-                        __builtin_amdgcn_readfirstlane((nt + 15) / 16), acc);
+    const int mt_live = __builtin_amdgcn_readfirstlane((nt + 15) / 16);
+#if ANEDVD_PF_DMA
+    __shared__ __attribute__((aligned(1024))) half_t xs0[16 * MT * 64], xs1[16 * MT * 64], xs2[16 * MT * 64],
+        xs3[16 * MT * 64];
+    DmaX<MT> xd;
+    xd.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
+    xd.dst = wv * DmaX<MT>::kInst * 1024;
+#pragma unroll
+    for (int i = 0; i < DmaX<MT>::kInst; i++) {
+        const int row = 8 * (wv * DmaX<MT>::kInst + i) + (lane >> 3);
+        xd.off[i] = a.d.rows[p0 + min(row, nt - 1)] * a.H * 2 + 16 * ((lane & 7) ^ x_sw(row));
+    }
+    pf_loop_dma_live<F, MT>(W, rb, a.H / kStep, lane, xd, xs0, xs1, xs2, xs3, mt_live, acc);
+#else
+    constexpr int R = MT / 4;
+    half_t *abuf = (half_t *)smem;
+    const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
+    StageX<R, F::kStageDepth == 1 ? 2 : 4> stage;
+    stage.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
+#pragma unroll
+    for (int h = 0; h < R; h++) stage.off[h] = a.d.rows[p0 + min(r + 64 * h, nt - 1)] * a.H * 2 + 32 * q;
+    pf_loop_live<F, MT>(W, rb, 0, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q, mt_live, acc);
+#endif
 
     if ((int)threadIdx.x < 16 * MT) dvs[threadIdx.x] = tdv;
     __syncthreads();
