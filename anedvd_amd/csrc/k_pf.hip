@@ -494,8 +494,16 @@ struct PfLds {
 // (w, w ^ 1): each takes its 32 columns' largest magnitude (in-lane over two tiles,
 // DPP over the 16 lanes of a row), the pair meets in LDS, and each writes its 32
 // columns scaled by the group's power of two.
+// Three wavefronts per SIMD where the decoder fits them without spilling (Q4_K at
+// 64-token workgroups: 170 -> 168 VGPRs), else the compiler's choice.
 template <class F, int MT>
-__global__ __launch_bounds__(256) void k_pf_gateup(PfArgs a)
+constexpr int pf_gu_waves()
+{
+    return std::is_same<F, FQ4_K>::value && MT == 4 ? 3 : 1;
+}
+
+template <class F, int MT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves<F, MT>()))) void k_pf_gateup(PfArgs a)
 {
     __shared__ float dvs[16 * MT];
     __shared__ float gmax[4][16 * MT];  // per wavefront: its 32 columns' largest |act| per token
