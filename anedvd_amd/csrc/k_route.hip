@@ -36,9 +36,10 @@ __device__ inline void exp_table_ready(uint64_t warm) { asm volatile("" ::"v"(wa
 // every chain its own lane and makes each lane's operands one contiguous stream:
 // the router is stored lane-major, wt[(8 e + l) J + j] = w[e][8 j + l] with
 // J = H / 8 (router_layout), read 8 j's per 16-byte load; the token's x is staged
-// in LDS the same way, xs[l J + j] = x[8 j + l].  Each lane runs TT tokens' chains
-// at once (independent adds interleave), and the eight lanes of an expert sit in
-// one DPP row for the ordered sum.
+// in LDS the same way, xs[l JP + j] = x[8 j + l], the row stride JP (>= J, four
+// times an odd number) putting the eight chains' 16-byte reads on distinct banks.
+// Each lane runs TT tokens' chains at once (independent adds interleave), and the
+// eight lanes of an expert sit in one DPP row for the ordered sum.
 //
 // Block: 256 threads = 32 experts x 8 lanes.  Grid: (ceil(E/32), ceil(T/TT)).
 __global__ void k_router_layout(const uint16_t *__restrict__ w, int E, int H, uint16_t *__restrict__ wt)
@@ -52,17 +53,19 @@ __global__ void k_router_layout(const uint16_t *__restrict__ w, int E, int H, ui
     wt[i] = w[e * H + 8 * (size_t)j + l];
 }
 
+__host__ __device__ inline int router_stride(int J) { return ((J + 3) / 4 | 1) * 4; }
+
 template <int TT>
 __global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ wt, const uint16_t *__restrict__ w,
                                                 const float *__restrict__ x, int T, int E, int H,
                                                 float *__restrict__ logits)
 {
-    extern __shared__ float xs[];  // [TT][8][J]
-    const int J = H >> 3, H8 = J * 8;
+    extern __shared__ float xs[];  // [TT][8][JP]
+    const int J = H >> 3, H8 = J * 8, JP = router_stride(J);
     const int t0 = blockIdx.y * TT;
     const int nt = min(TT, T - t0);
     for (int t = 0; t < nt; t++)
-        for (int i = threadIdx.x; i < H8; i += blockDim.x) xs[(t * 8 + (i & 7)) * J + (i >> 3)] = x[(size_t)(t0 + t) * H + i];
+        for (int i = threadIdx.x; i < H8; i += blockDim.x) xs[(t * 8 + (i & 7)) * JP + (i >> 3)] = x[(size_t)(t0 + t) * H + i];
     __syncthreads();
 
     const int l = threadIdx.x & 7;
@@ -80,12 +83,19 @@ __global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ wt,
         for (; j < J; j += 8) {
             const uint4 nxt = w16[min(j + 8, J - 8) >> 3];
             const uint32_t ww[4] = {cur.x, cur.y, cur.z, cur.w};
+            float xv[TT][8];
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                const float4 a = *(const float4 *)&xs[(t * 8 + l) * JP + j];
+                const float4 b = *(const float4 *)&xs[(t * 8 + l) * JP + j + 4];
+                xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+                xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+            }
 #pragma unroll
             for (int q = 0; q < 8; q++) {
                 const float wv = f16_bits_to_f32((uint16_t)(ww[q >> 1] >> (16 * (q & 1))));
 #pragma unroll
-                for (int t = 0; t < TT; t++)
-                    acc[t] = __fadd_rn(acc[t], __fmul_rn(xs[(t * 8 + l) * J + j + q], wv));
+                for (int t = 0; t < TT; t++) acc[t] = __fadd_rn(acc[t], __fmul_rn(xv[t][q], wv));
             }
             cur = nxt;
         }
@@ -93,7 +103,7 @@ __global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ wt,
         for (; j < J; j++) {
             const float wv = f16_bits_to_f32(wr[j]);
 #pragma unroll
-            for (int t = 0; t < TT; t++) acc[t] = __fadd_rn(acc[t], __fmul_rn(xs[(t * 8 + l) * J + j], wv));
+            for (int t = 0; t < TT; t++) acc[t] = __fadd_rn(acc[t], __fmul_rn(xs[(t * 8 + l) * JP + j], wv));
         }
     }
     // Ordered lane sum: lane 0 + lane 1 + ... + lane 7, then the scalar tail.
@@ -129,7 +139,7 @@ int launch_router(const uint16_t *d_wt, const uint16_t *d_w, const float *d_x, i
     const int eb = (E + 31) / 32;
     auto go = [&](auto tt) -> int {
         constexpr int TT = decltype(tt)::value;
-        const size_t lds = (size_t)TT * (H & ~7) * 4;
+        const size_t lds = (size_t)TT * 8 * router_stride(H >> 3) * 4;
         if (lds > 65536) return -1;
         hipLaunchKernelGGL(k_router<TT>, dim3(eb, (T + TT - 1) / TT), block, lds, st, d_wt, d_w, d_x, T, E, H,
                            d_logits);
