@@ -275,24 +275,70 @@ __device__ inline int x_sw(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// A stager issues one step's loads into a ring slot (issue: kIssue vector-memory
+// instructions) and, once they are done, fixes up the bytes its own wavefront's
+// loads wrote before the barrier that publishes the slot (fix).
+
+// gate/up: x rows (one power of two per row) need no fix.
 template <int MT>
 struct DmaX {
     static constexpr int kInst = MT / 2;  // loads per wavefront per step: 16 MT rows x 128 B / 4 wavefronts / 1 KiB
+    static constexpr int kIssue = kInst;
+    static constexpr int kRawCap = 80;  // weight slots up to this size go two steps ahead
     rsrc_t q;
     int off[kInst];  // load i: the lane's token row base + its logical piece (bytes)
     int dst;         // this wavefront's first destination byte in a slot
-};
-
-template <int MT>
-__device__ inline void x_issue(const DmaX<MT> &x, half_t *slot, int s)
-{
+    __device__ inline void issue(half_t *slot, int s, int)
+    {
 #if __HIP_DEVICE_COMPILE__  // the compiler's host pass has no LDS-pointer builtins
 #pragma unroll
-    for (int i = 0; i < DmaX<MT>::kInst; i++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(x.q, (lds_void *)((char *)slot + x.dst + 1024 * i), 16, x.off[i],
-                                                 s * 2 * kStep, 0, 0);
+        for (int i = 0; i < kInst; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(q, (lds_void *)((char *)slot + dst + 1024 * i), 16, off[i],
+                                                     s * 2 * kStep, 0, 0);
 #endif
-}
+    }
+    __device__ inline void fix(half_t *, int) {}
+};
+
+// down: the SwiGLU activations carry a power of two per (position, 64-column
+// group) -- one per step.  With the pieces, each wavefront loads its rows'
+// descales for the step into its own 64 floats of LDS (lane j the row of piece
+// load j / 8, lane j / 8 % ... as the pieces' lanes l / 8), and fix() rescales its
+// own 16-byte pieces in place to the row's reference: a power of two <= 1, exact,
+// as the register staging did.
+template <int MT>
+struct DmaAct {
+    static constexpr int kInst = MT / 2;
+    static constexpr int kIssue = kInst + 1;  // the pieces, then the descales
+    static constexpr int kRawCap = MT == 8 ? 72 : 80;  // Q8_0 and Q5_1 at 128 tokens: one step (two waves per SIMD)
+    rsrc_t q, ds;
+    int off[kInst];     // load i: the lane's position's piece (bytes)
+    int doff;           // the descale of row 8 (w kInst + j / 8) + j % 8, j = min(lane, 8 kInst - 1) (bytes)
+    int dst, ld4, wv;
+    float *dgs;         // LDS [4 slots][4 wavefronts][64]: the loaded descales
+    const float *rinv;  // LDS [16 MT]: 1 / each row's reference
+    __device__ inline void issue(half_t *slot, int s, int b)
+    {
+#if __HIP_DEVICE_COMPILE__
+#pragma unroll
+        for (int i = 0; i < kInst; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(q, (lds_void *)((char *)slot + dst + 1024 * i), 16, off[i],
+                                                     s * 2 * kStep, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ds, (lds_void *)(dgs + (b * 4 + wv) * 64), 4, doff, s * ld4, 0, 0);
+#endif
+    }
+    __device__ inline void fix(half_t *slot, int b)
+    {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < kInst; i++) {
+            const int j = 8 * i + (lane >> 3);
+            const half_t f = (half_t)(dgs[(b * 4 + wv) * 64 + j] * rinv[8 * wv * kInst + j]);
+            half8 *p = (half8 *)((char *)slot + dst + 1024 * i + 16 * lane);
+            *p = *p * f;
+        }
+    }
+};
 
 // s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt at their maxima: no wait).
 template <int N>
@@ -302,14 +348,17 @@ __device__ inline void wait_vm()
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// s_waitcnt lgkmcnt(0) alone.
+__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+
 // Waits until the activation loads of the next step are done, given what this
 // wavefront issued after them: two weight load() calls of at least F::kMinLoads
-// instructions each, and c activation steps of kInst loads.  (VMEM loads complete
-// in order; counting fewer than were issued only waits longer.)
-template <class F, int MT>
+// instructions each, and c activation steps of X::kIssue loads.  (VMEM loads
+// complete in order; counting fewer than were issued only waits longer.)
+template <class F, class X>
 __device__ inline void x_wait(int c)
 {
-    constexpr int kI = DmaX<MT>::kInst, kW = F::kMinLoads;
+    constexpr int kI = X::kIssue, kW = F::kMinLoads;
     if (c == 2) wait_vm<2 * kW + 2 * kI>();
     else if (c == 1) wait_vm<2 * kW + kI>();
     else wait_vm<2 * kW>();
@@ -317,11 +366,13 @@ __device__ inline void x_wait(int c)
 
 // The workgroup barrier of the direct-to-LDS loop.  __syncthreads() would wait
 // for every load into LDS in flight (its release fence covers them); the loop's
-// own vmcnt wait has covered the next step's, and no other LDS write precedes the
-// barrier.  The acquire fence after it keeps the next step's LDS reads below it.
+// own vmcnt wait has covered the next step's, and the stager's fix-up writes are
+// waited for here.  The acquire fence after it keeps the next step's LDS reads
+// below it.
 __device__ inline void x_barrier()
 {
     __builtin_amdgcn_sched_barrier(0);
+    wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     __builtin_amdgcn_sched_barrier(0);
@@ -337,39 +388,41 @@ __device__ inline void x_barrier()
 #define ANEDVD_PF_DMA_WD 2
 #endif
 
-// pf_loop with the activations in the direct-to-LDS ring.  Per step s the
+// pf_loop with the activations in the direct-to-LDS ring (steps [s0w, s0w + steps)
+// of the weights; the stager's offsets already point at step s0w).  Per step s the
 // wavefront issues the weight loads of step s + D, then the activation loads of
 // step s + 3; before the barrier that ends step s it waits for step s + 1's
 // activation loads, issued two steps earlier: younger than them are the weight
 // loads issued at steps s - 1 and s and the activation loads of steps s + 2 and
 // s + 3 that exist.  The slot step s + 4 will fill is the one step s reads, free
 // after that barrier.
-template <class F, int MT, int MTL, class TS>
-__device__ inline void pf_loop_dma(const TS &W, int rb, int steps, int lane, const DmaX<MT> &x, half_t *xs0,
+template <class F, int MT, int MTL, class TS, class X>
+__device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int lane, X &x, half_t *xs0,
                                    half_t *xs1, half_t *xs2, half_t *xs3, f32x4 (*acc)[MT])
 {
     constexpr int U = 4, DA = kXDepth;
     static_assert(U % F::kSpu == 0, "a scale unit must fit an unrolled block");
-    // (F16's 128-byte weight slots stay one step ahead: two more of them would not fit)
-    constexpr int DW = sizeof(typename F::Raw) <= 80 ? ANEDVD_PF_DMA_WD : 1;
+    // (larger weight slots stay one step ahead: two more of them would not fit)
+    constexpr int DW = sizeof(typename F::Raw) <= X::kRawCap ? ANEDVD_PF_DMA_WD : 1;
     constexpr int D = F::kDepth > DW ? F::kDepth : DW;
     constexpr int R = D == 1 ? 2 : 4;
     static_assert(D >= 1 && D <= 3, "at most three steps ahead");
     const int n = lane & 15, g = lane >> 4;
     const int so = (W.src(0).nrb - rb) * W.src(0).steps;
-    auto ws = [&](int v) { return v < steps ? v : so; };
+    auto ws = [&](int v) { return v < steps ? s0w + v : so; };  // weights of step v of this K share
     auto slot = [&](int b) { return b == 0 ? xs0 : b == 1 ? xs1 : b == 2 ? xs2 : xs3; };  // b a constant
     typename F::Raw w[R];
     typename F::State st;
 #pragma unroll
     for (int v = -DA; v < 0; v++) {  // the steady state's order: weights of v + D, activations of v + DA
         if (v + D >= 0) F::load(w[(v + D) % R], W, rb, ws(v + D), lane);
-        if (v + DA < steps) x_issue(x, slot((v + DA) & 3), v + DA);
+        if (v + DA < steps) x.issue(slot((v + DA) & 3), v + DA, (v + DA) & 3);
     }
     // step 0's activations: younger than them are the weight loads of the
     // virtual steps -2 and -1 that exist (min(D, 2) calls) and the activation
     // loads of steps 1 and 2 (not counted: only stricter)
     wait_vm<(D >= 2 ? 2 : 1) * F::kMinLoads>();
+    x.fix(slot(0), 0);
     x_barrier();
     // the lane's operand offsets in a slot (halves): row n of a token tile, piece 2 g + j
     const int ao0 = n * 64 + (((2 * g) ^ x_sw(n)) << 3), ao1 = n * 64 + (((2 * g + 1) ^ x_sw(n)) << 3);
@@ -379,7 +432,7 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int steps, int lane, con
             const int s = s0 + k;
             if (s >= steps) break;  // uniform
             F::load(w[(k + D) % R], W, rb, ws(s + D), lane);
-            if (s + DA < steps) x_issue(x, slot((k + DA) & 3), s + DA);
+            if (s + DA < steps) x.issue(slot((k + DA) & 3), s + DA, (k + DA) & 3);
             __builtin_amdgcn_sched_barrier(0);
             const int ss = k % F::kSpu;
             const half_t *a = slot(k);
@@ -405,24 +458,25 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int steps, int lane, con
                 }
             }
             if (s + 1 < steps) {
-                x_wait<F, MT>((s + 2 < steps) + (s + 3 < steps));
+                x_wait<F, X>((s + 2 < steps) + (s + 3 < steps));
+                x.fix(slot((k + 1) & 3), (k + 1) & 3);
                 x_barrier();
             }
         }
     }
 }
 
-template <class F, int MT, int L = MT, class TS>
-__device__ inline void pf_loop_dma_live(const TS &W, int rb, int steps, int lane, const DmaX<MT> &x, half_t *xs0,
+template <class F, int MT, int L = MT, class TS, class X>
+__device__ inline void pf_loop_dma_live(const TS &W, int rb, int s0w, int steps, int lane, X &x, half_t *xs0,
                                         half_t *xs1, half_t *xs2, half_t *xs3, int mt_live, f32x4 (*acc)[MT])
 {
     if constexpr (L > 1) {
         if (mt_live < L) {
-            pf_loop_dma_live<F, MT, L - 1>(W, rb, steps, lane, x, xs0, xs1, xs2, xs3, mt_live, acc);
+            pf_loop_dma_live<F, MT, L - 1>(W, rb, s0w, steps, lane, x, xs0, xs1, xs2, xs3, mt_live, acc);
             return;
         }
     }
-    pf_loop_dma<F, MT, L>(W, rb, steps, lane, x, xs0, xs1, xs2, xs3, acc);
+    pf_loop_dma<F, MT, L>(W, rb, s0w, steps, lane, x, xs0, xs1, xs2, xs3, acc);
 }
 
 struct PfArgs {
@@ -536,7 +590,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
         const int row = 8 * (wv * DmaX<MT>::kInst + i) + (lane >> 3);
         xd.off[i] = a.d.rows[p0 + min(row, nt - 1)] * a.H * 2 + 16 * ((lane & 7) ^ x_sw(row));
     }
-    pf_loop_dma_live<F, MT>(W, rb, a.H / kStep, lane, xd, xs0, xs1, xs2, xs3, mt_live, acc);
+    pf_loop_dma_live<F, MT>(W, rb, 0, a.H / kStep, lane, xd, xs0, xs1, xs2, xs3, mt_live, acc);
 #else
     constexpr int R = MT / 4;
     half_t *abuf = (half_t *)smem;
@@ -615,8 +669,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
 template <class F, int MT>
 __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
 {
-    constexpr int R = MT / 4;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
     __shared__ float ref[16 * MT];
     __shared__ int orow[16 * MT];  // output rows of the chunk's positions, (token, slot) order
     __shared__ float ref4[256 / (16 * MT)][16 * MT];
@@ -656,6 +708,40 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
         }
         __syncthreads();
     }
+    f32x4 acc[kPfTiles][MT];
+#pragma unroll
+    for (int tt = 0; tt < kPfTiles; tt++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    const int mt_live = __builtin_amdgcn_readfirstlane((nt + 15) / 16);
+#if ANEDVD_PF_DMA
+    __shared__ __attribute__((aligned(1024))) half_t ys0[16 * MT * 64], ys1[16 * MT * 64], ys2[16 * MT * 64],
+        ys3[16 * MT * 64];
+    __shared__ float dgs[4 * 4 * 64], rinv[16 * MT];
+    if ((int)threadIdx.x < 16 * MT) rinv[threadIdx.x] = 1.0f / ref[threadIdx.x];
+    __syncthreads();
+    constexpr int kI = DmaAct<MT>::kInst;
+    DmaAct<MT> xd;
+    xd.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
+    xd.ds = make_rsrc(a.x.ds, (size_t)G * ld * 4);
+    xd.ld4 = ld * 4;
+    xd.wv = wv;
+    xd.dst = wv * kI * 1024;
+    xd.dgs = dgs;
+    xd.rinv = rinv;
+#pragma unroll
+    for (int i = 0; i < kI; i++) {
+        const int row = 8 * (wv * kI + i) + (lane >> 3);
+        xd.off[i] = min(p0 + row, a.P - 1) * a.I * 2 + 16 * ((lane & 7) ^ x_sw(row)) + s0 * 2 * kStep;
+    }
+    {
+        const int j = min(lane, 8 * kI - 1), row = 8 * (wv * kI + j / 8) + j % 8;
+        xd.doff = min(p0 + row, a.P - 1) * 4 + s0 * xd.ld4;
+    }
+    pf_loop_dma_live<F, MT>(W, rb, s0, ksteps, lane, xd, ys0, ys1, ys2, ys3, mt_live, acc);
+#else
+    constexpr int R = MT / 4;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
     const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
     StageAct<R, F::kStageDepth == 1 ? 2 : 4> stage;
     stage.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
@@ -668,13 +754,8 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
         stage.doff[h] = pos * 4 + s0 * stage.ld4;
         stage.inv_ref[h] = 1.0f / ref[r + 64 * h];
     }
-    f32x4 acc[kPfTiles][MT];
-#pragma unroll
-    for (int tt = 0; tt < kPfTiles; tt++)
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    pf_loop_live<F, MT>(W, rb, s0, ksteps, lane, stage, (half_t *)smem, r * kAStride + 16 * q,
-                        __builtin_amdgcn_readfirstlane((nt + 15) / 16), acc);
+    pf_loop_live<F, MT>(W, rb, s0, ksteps, lane, stage, (half_t *)smem, r * kAStride + 16 * q, mt_live, acc);
+#endif
     float *ypk = a.ypart + (size_t)kq * a.P * a.H;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
