@@ -1,7 +1,7 @@
-// fq.h -- the folded-scale decoders of the expert kernels that dequantise a whole
-// step once to f16 and reuse it for several 16-token tiles (k_pf.hip, and the
-// grouped variants of k_mm.hip): the block and sub-block scales go into the f16
-// weights, so the MFMA accumulates the whole K with no per-block rescale.
+// fq.h -- the folded-scale decoders of the grouped GEMM (k_pf.hip), which
+// dequantises a whole step once to f16 and reuses it for several 16-token tiles:
+// the block and sub-block scales go into the f16 weights, so the MFMA accumulates
+// the whole K with no per-block rescale.
 #pragma once
 
 #include "common.h"
@@ -9,20 +9,13 @@
 
 namespace anedvd {
 
-// Weight and activation steps loaded ahead of the one being multiplied: the
-// super-block formats (small register footprint per step, memory-bound prefill
-// shapes) go deeper than Q8_0 / Q4_0, whose kernels keep three wavefronts per SIMD.
+// Weight steps loaded ahead of the one being multiplied, at least (the grouped
+// loop may go deeper): the super-block formats two, the 32-element formats one.
 #ifndef ANEDVD_PF_DEPTH_K
 #define ANEDVD_PF_DEPTH_K 2
 #endif
 #ifndef ANEDVD_PF_DEPTH_L
 #define ANEDVD_PF_DEPTH_L 1
-#endif
-#ifndef ANEDVD_PF_STAGE_K
-#define ANEDVD_PF_STAGE_K 2
-#endif
-#ifndef ANEDVD_PF_STAGE_L
-#define ANEDVD_PF_STAGE_L 1
 #endif
 constexpr int kPfTiles = 4;   // 16-row tiles per wavefront: each staged A read feeds four MFMAs
 
@@ -77,7 +70,6 @@ struct FF16 {
     static constexpr int kSpu = 1;
     static constexpr bool kHoistA = false;  // 32 VGPRs of values per ring slot already
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
-    static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     static constexpr int kMinLoads = 8;                    // load instructions of every load() call
     struct Raw {
         u32x4 q[kPfTiles][2];
@@ -102,7 +94,6 @@ struct FQ8_0 {
     static constexpr int kSpu = 1;
     static constexpr bool kHoistA = false;  // at 176 VGPRs two waves per SIMD instead of three
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
-    static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     static constexpr int kMinLoads = 8;
     struct Raw {
         u32x4 q[kPfTiles];
@@ -131,7 +122,6 @@ struct FQ4_0 {
     static constexpr int kSpu = 1;
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
-    static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     static constexpr int kMinLoads = 8;
     struct Raw {
         u32x2 q[kPfTiles];
@@ -165,7 +155,6 @@ struct FQLegacy {
     static constexpr int kSpu = 1;
     static constexpr bool kHoistA = !kFive;  // the 5-bit formats: three waves per SIMD without it
     static constexpr int kDepth = ANEDVD_PF_DEPTH_L;       // steps of weights in flight ahead
-    static constexpr int kStageDepth = ANEDVD_PF_STAGE_L;  // steps of activations in flight ahead
     static constexpr int kMinLoads = kFive ? 12 : 8;
     struct Raw {
         u32x2 q[kPfTiles];
@@ -225,7 +214,6 @@ struct FQ4_K {
     static constexpr int kSpu = 4;
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
-    static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     static constexpr int kMinLoads = 4;                    // the scales come on a unit's first step only
     struct Raw {
         u32x2 q[kPfTiles];
@@ -294,7 +282,6 @@ struct FQ5_K {
     static constexpr int kSpu = 4;
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
-    static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     static constexpr int kMinLoads = 8;
     struct Raw {
         u32x2 q[kPfTiles];
@@ -346,7 +333,6 @@ struct FQ23K {
     static constexpr int kSpu = 4;
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
-    static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     static constexpr int kMinLoads = kThree ? 8 : 4;
     struct Raw {
         uint32_t q[kPfTiles];
@@ -427,7 +413,6 @@ struct FQ6_K {
     static constexpr int kSpu = 4;
     static constexpr bool kHoistA = true;   // activation fragments read at the step's start
     static constexpr int kDepth = ANEDVD_PF_DEPTH_K;       // steps of weights in flight ahead
-    static constexpr int kStageDepth = ANEDVD_PF_STAGE_K;  // steps of activations in flight ahead
     static constexpr int kMinLoads = 8;
     struct Raw {
         u32x2 q[kPfTiles];

@@ -2,17 +2,20 @@
 //
 // Same math as the decode kernels (cpu.moeExpertAccumF32, cpu.zig:416-452, over
 // the gguf.zig block formats), organised for groups of tens to hundreds of tokens:
-//   - a workgroup takes a 64-token chunk of one expert's group and 128 weight rows
-//     of both gate and up (or 256 rows of down);
-//   - the chunk's activations are staged in LDS once per 64-column step and shared
-//     by the four wavefronts;
-//   - each wavefront dequantises its four 16-row tiles once per step to f16 (Q8_0,
-//     Q4_0: d * q rounded once; Q4_K, Q6_K: the quant exact, the sub-block scale
-//     and min as f16, one rounding in the FMA) and runs them against the chunk's
-//     16-token tiles, accumulating the whole K inside the MFMA;
-//   - activations carry one power of two per row (x as converted; the SwiGLU
-//     activations are rescaled to their row's largest descale while staged), so
-//     nothing is rescaled inside the K loop.
+//   - a workgroup takes 64 or 128 tokens of one expert's group (part of a chunk
+//     of the dispatch's work list) and 128 weight rows of both gate and up, or 256
+//     rows of down (all of K, or one of two K shares);
+//   - the tokens' activations go from memory straight into a four-slot LDS ring
+//     (direct-to-LDS loads, three steps ahead), shared by the four wavefronts;
+//   - each wavefront dequantises its four 16-row tiles once per 64-column step to
+//     f16 (Q8_0, Q4_0: d * q rounded once; Q4_K, Q6_K: the quant exact, the
+//     sub-block scale and min as f16, one rounding in the FMA) and runs them
+//     against the 16-token tiles, accumulating the whole K inside the MFMA;
+//   - activations carry one power of two per row: x as converted, and the SwiGLU
+//     activations (a power of two per 64-column group) rescaled in LDS to their
+//     row's largest descale before use, so nothing is rescaled inside the K loop;
+//   - gate/up: a wavefront holds gate and up of the same 32 rows, so SiLU(g) * u
+//     and the activation format's scale form in registers.
 #include <type_traits>
 
 #include "common.h"
@@ -21,239 +24,6 @@
 #include "mma.h"
 
 namespace anedvd {
-
-constexpr int kAStride = 72;  // halves per staged token row: 64 + 8 against LDS bank conflicts
-
-// Software pipelining of the K loop (1: a step's second half dequantised under its
-// first half's MFMAs and the next step's first half under its second half's), and
-// an interleave pattern for the scheduler (VALU instructions placed after each
-// MFMA; 0 = the compiler's order).
-#ifndef ANEDVD_PF_PIPE
-#define ANEDVD_PF_PIPE 0
-#endif
-#ifndef ANEDVD_PF_IL
-#define ANEDVD_PF_IL 0
-#endif
-
-// ------------------------------------------------------------ staging
-
-// Thread tid of a workgroup stages, per step, quarter q = tid / 64 of the step's
-// 64 columns (32 bytes) of token rows r = tid % 64 + 64 h, h < R: consecutive lanes
-// write consecutive rows, so the LDS writes of a wavefront hit distinct banks.  The
-// global loads land in a ring of NB register slots, so a step's activations can be
-// loaded several steps before they are written to LDS.
-template <int R, int NB>
-struct StageX {  // gate/up: token rows gathered through the dispatch; x has per-row descales
-    static constexpr int kSlots = NB;
-    rsrc_t q;
-    int off[R];
-    u32x4 v[NB][R][2];
-    template <int B>
-    __device__ inline void load(int s)
-    {
-#pragma unroll
-        for (int h = 0; h < R; h++) {
-            v[B][h][0] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep, 0);
-            v[B][h][1] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep + 16, 0);
-        }
-    }
-    template <int B>
-    __device__ inline void store(half_t *dst) const  // dst: this thread's first row, its quarter
-    {
-#pragma unroll
-        for (int h = 0; h < R; h++) {
-            *(u32x4 *)(dst + h * 64 * kAStride) = v[B][h][0];
-            *(u32x4 *)(dst + h * 64 * kAStride + 8) = v[B][h][1];
-        }
-    }
-};
-
-template <int R, int NB>
-struct StageAct {  // down: consecutive positions, rescaled from their group's descale to the row's
-    static constexpr int kSlots = NB;
-    rsrc_t q, ds;
-    int off[R], doff[R], ld4;
-    float inv_ref[R];
-    u32x4 v[NB][R][2];
-    float dg[NB][R];
-    template <int B>
-    __device__ inline void load(int s)
-    {
-#pragma unroll
-        for (int h = 0; h < R; h++) {
-            v[B][h][0] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep, 0);
-            v[B][h][1] = __builtin_amdgcn_raw_buffer_load_b128(q, off[h], s * 2 * kStep + 16, 0);
-            dg[B][h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ds, doff[h], s * ld4, 0));
-        }
-    }
-    template <int B>
-    __device__ inline void store(half_t *dst) const
-    {
-#pragma unroll
-        for (int h = 0; h < R; h++) {
-            const half_t f = (half_t)(dg[B][h] * inv_ref[h]);  // a power of two <= 1
-            *(half8 *)(dst + h * 64 * kAStride) = as_h8(v[B][h][0]) * f;
-            *(half8 *)(dst + h * 64 * kAStride + 8) = as_h8(v[B][h][1]) * f;
-        }
-    }
-};
-
-// Register slot b chosen at run time; inside the unrolled step loop b is a
-// constant and the branch folds away.
-template <class S>
-__device__ inline void stage_load(S &st, int b, int s)
-{
-    if (b == 0) st.template load<0>(s);
-    else if (b == 1) st.template load<1 % S::kSlots>(s);
-    else if (b == 2) st.template load<2 % S::kSlots>(s);
-    else st.template load<3 % S::kSlots>(s);
-}
-
-template <class S>
-__device__ inline void stage_store(const S &st, int b, half_t *dst)
-{
-    if (b == 0) st.template store<0>(dst);
-    else if (b == 1) st.template store<1 % S::kSlots>(dst);
-    else if (b == 2) st.template store<2 % S::kSlots>(dst);
-    else st.template store<3 % S::kSlots>(dst);
-}
-
-// ------------------------------------------------------------ main loop
-
-// Steps [s0, s0 + steps) of the wavefront's four tiles of row block rb against the MT
-// 16-token tiles staged in `abuf` (two buffers of 16 MT x kAStride halves):
-// acc[tt][mt] = sum_k W[64 rb + 16 tt + l % 16][k] * A[16 mt + 4 (l / 16) + i][k].
-// Weights are loaded F::kDepth steps ahead and activations F::kStageDepth steps
-// ahead (rings of register slots); every thread of the workgroup takes part in the staging, so all of
-// them reach the barriers.  Steps go in unrolled blocks of four (one scale unit of
-// the super-block formats), so the slots and the LDS buffers alternate at
-// compile-time indices.  Weight loads past the last step go out of range (zero, no
-// memory traffic).  s0 is a multiple of four (a scale unit starts there); the
-// staging offsets already point at step s0.
-template <class F, int MT, int MTL, class TS, class S>
-__device__ inline void pf_loop(const TS &W, int rb, int s0, int steps, int lane, S &stage, half_t *abuf,
-                               int srow, f32x4 (*acc)[MT])
-{
-    constexpr int U = 4;
-    constexpr int BUF = 16 * MT * kAStride;
-    static_assert(U % F::kSpu == 0, "a scale unit must fit an unrolled block");
-    const int n = lane & 15, g = lane >> 4;
-    const int so = (W.src(0).nrb - rb) * W.src(0).steps;
-    auto ws = [&](int x) { return x < steps ? s0 + x : so; };
-    constexpr int D = F::kDepth, DA = F::kStageDepth;
-    constexpr int R = D == 1 ? 2 : 4;    // ring of weight slots; divides the unrolled block
-    constexpr int RA = DA == 1 ? 2 : 4;  // ring of staging slots
-    static_assert(D >= 1 && D <= 3 && DA >= 1 && DA <= 3, "at most three steps ahead");
-    static_assert(S::kSlots == RA, "staging ring");
-    typename F::Raw w[R];
-    typename F::State st;
-    stage.template load<0>(0);
-#pragma unroll
-    for (int d = 0; d < D; d++) F::load(w[d], W, rb, ws(d), lane);
-    stage.template store<0>(abuf + srow);
-#pragma unroll
-    for (int d = 1; d < DA; d++)
-        if (d < steps) stage_load(stage, d, d);
-    constexpr bool kPipe = ANEDVD_PF_PIPE != 0;
-    half8 bn[kPfTiles];  // pipelined: the j = 0 operands of the step about to run
-    if constexpr (kPipe) {
-        F::begin(w[0], st, 0, lane);
-#pragma unroll
-        for (int tt = 0; tt < kPfTiles; tt++) bn[tt] = F::bop(w[0], st, 0, tt, 0, lane);
-    }
-    __syncthreads();
-    for (int s0 = 0; s0 < steps; s0 += U) {
-#pragma unroll
-        for (int k = 0; k < U; k++) {
-            const int s = s0 + k;
-            if (s >= steps) break;  // uniform; only for a step count that is not a multiple of 4
-            const bool more = s + 1 < steps;
-            if (s + DA < steps) stage_load(stage, (k + DA) % RA, s + DA);
-            F::load(w[(k + D) % R], W, rb, ws(s + D), lane);
-            __builtin_amdgcn_sched_barrier(0);
-            const int ss = k % F::kSpu;
-            const half_t *a = abuf + (k & 1) * BUF + n * kAStride + 16 * g;
-            if constexpr (kPipe) {
-                // j = 0 with the operands dequantised during the previous step, this
-                // step's j = 1 dequantised under them, then the next step's j = 0
-                // under the j = 1 MFMAs (past the last step its weights read as 0).
-                half8 av[2][MTL], b1[kPfTiles];
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-#pragma unroll
-                    for (int mt = 0; mt < MTL; mt++) av[j][mt] = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
-#pragma unroll
-                for (int tt = 0; tt < kPfTiles; tt++) b1[tt] = F::bop(w[k % R], st, ss, tt, 1, lane);
-#pragma unroll
-                for (int mt = 0; mt < MTL; mt++)
-#pragma unroll
-                    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av[0][mt], bn[tt], acc[tt][mt]);
-                const int sn = (k + 1) % F::kSpu;
-                F::begin(w[(k + 1) % R], st, sn, lane);
-#pragma unroll
-                for (int tt = 0; tt < kPfTiles; tt++) bn[tt] = F::bop(w[(k + 1) % R], st, sn, tt, 0, lane);
-#pragma unroll
-                for (int mt = 0; mt < MTL; mt++)
-#pragma unroll
-                    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av[1][mt], b1[tt], acc[tt][mt]);
-                if constexpr (ANEDVD_PF_IL > 0) {
-                    // the A reads, then each MFMA followed by IL VALU instructions
-                    __builtin_amdgcn_sched_group_barrier(0x100, 2 * MTL, 0);
-#pragma unroll
-                    for (int i = 0; i < 2 * kPfTiles * MTL; i++) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x002, ANEDVD_PF_IL, 0);
-                    }
-                }
-                if (more) stage_store(stage, (k + 1) % RA, abuf + ((k + 1) & 1) * BUF + srow);
-                __syncthreads();
-                continue;
-            }
-            F::begin(w[k % R], st, ss, lane);
-            // The step's activation fragments, read before the dequantisation so their
-            // LDS latency hides behind it (token tiles past the chunk's end read stale
-            // rows of the buffer that no MFMA uses), or, for decoders whose registers
-            // are tight, just before their MFMAs.
-            half8 av[2][MT];
-            if constexpr (F::kHoistA) {
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-#pragma unroll
-                    for (int mt = 0; mt < MTL; mt++) av[j][mt] = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                half8 b[kPfTiles];
-#pragma unroll
-                for (int tt = 0; tt < kPfTiles; tt++) b[tt] = F::bop(w[k % R], st, ss, tt, j, lane);
-#pragma unroll
-                for (int mt = 0; mt < MTL; mt++) {  // token tiles past the chunk's end stay zero
-                    if constexpr (!F::kHoistA) av[j][mt] = *(const half8 *)(a + mt * 16 * kAStride + 8 * j);
-#pragma unroll
-                    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av[j][mt], b[tt], acc[tt][mt]);
-                }
-            }
-            if (more) stage_store(stage, (k + 1) % RA, abuf + ((k + 1) & 1) * BUF + srow);
-            __syncthreads();
-        }
-    }
-}
-
-// pf_loop for the chunk's live 16-token tiles (uniform over the workgroup): one
-// instantiation per count, so a step holds no branch and the compiler may
-// interleave the dequantisation with the MFMAs.
-template <class F, int MT, int L = MT, class TS, class S>
-__device__ inline void pf_loop_live(const TS &W, int rb, int s0, int steps, int lane, S &stage, half_t *abuf,
-                                    int srow, int mt_live, f32x4 (*acc)[MT])
-{
-    if constexpr (L > 1) {
-        if (mt_live < L) {
-            pf_loop_live<F, MT, L - 1>(W, rb, s0, steps, lane, stage, abuf, srow, mt_live, acc);
-            return;
-        }
-    }
-    pf_loop<F, MT, L>(W, rb, s0, steps, lane, stage, abuf, srow, acc);
-}
 
 // ------------------------------------------------------------ direct-to-LDS staging
 
@@ -266,9 +36,6 @@ __device__ inline void pf_loop_live(const TS &W, int rb, int s0, int steps, int 
 // operand reads of 8 or 16 consecutive rows hit distinct banks.  The hardware
 // writes lane l of such a load at byte 16 l of its 1 KiB destination: a
 // wavefront's load fills 8 rows, lane l the physical piece l % 8 of row l / 8.
-#ifndef ANEDVD_PF_DMA
-#define ANEDVD_PF_DMA 1
-#endif
 constexpr int kXDepth = 3;
 
 __device__ inline int x_sw(int r) { return (r & 7) ^ ((r >> 3) & 1); }
@@ -533,12 +300,6 @@ __device__ inline bool pf_chunk(const Dispatch &d, int w, int sub, int &e, int &
     return true;
 }
 
-// LDS of one workgroup: the two staged activation tiles of the K loop.
-template <int MT>
-struct PfLds {
-    static constexpr int kA = 2 * 16 * MT * kAStride * 2;  // bytes
-};
-
 // ------------------------------------------------------------ gate / up
 
 // Grid nw8 * I/128 workgroups of 256 threads (pf_item's order).  Wave w:
@@ -561,9 +322,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
 {
     __shared__ float dvs[16 * MT];
     __shared__ float gmax[4][16 * MT];  // per wavefront: its 32 columns' largest |act| per token
-#if !ANEDVD_PF_DMA
-    __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
-#endif
     int e, p0, nt, w, rbg;
     const int nw = a.nchunk * a.sub;
     pf_item((int)blockIdx.x, pf_nw8(nw), a.contig, w, rbg);
@@ -579,7 +337,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
     // token m's descale for the epilogue, loaded by thread m before the K loop
     const float tdv = (int)threadIdx.x < 16 * MT ? a.x.ds[a.d.rows[p0 + min((int)threadIdx.x, nt - 1)]] : 0.0f;
     const int mt_live = __builtin_amdgcn_readfirstlane((nt + 15) / 16);
-#if ANEDVD_PF_DMA
     __shared__ __attribute__((aligned(1024))) half_t xs0[16 * MT * 64], xs1[16 * MT * 64], xs2[16 * MT * 64],
         xs3[16 * MT * 64];
     DmaX<MT> xd;
@@ -591,16 +348,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
         xd.off[i] = a.d.rows[p0 + min(row, nt - 1)] * a.H * 2 + 16 * ((lane & 7) ^ x_sw(row));
     }
     pf_loop_dma_live<F, MT>(W, rb, 0, a.H / kStep, lane, xd, xs0, xs1, xs2, xs3, mt_live, acc);
-#else
-    constexpr int R = MT / 4;
-    half_t *abuf = (half_t *)smem;
-    const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
-    StageX<R, F::kStageDepth == 1 ? 2 : 4> stage;
-    stage.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
-#pragma unroll
-    for (int h = 0; h < R; h++) stage.off[h] = a.d.rows[p0 + min(r + 64 * h, nt - 1)] * a.H * 2 + 32 * q;
-    pf_loop_live<F, MT>(W, rb, 0, a.H / kStep, lane, stage, abuf, r * kAStride + 16 * q, mt_live, acc);
-#endif
 
     if ((int)threadIdx.x < 16 * MT) dvs[threadIdx.x] = tdv;
     __syncthreads();
@@ -714,7 +461,6 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[tt][mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     const int mt_live = __builtin_amdgcn_readfirstlane((nt + 15) / 16);
-#if ANEDVD_PF_DMA
     __shared__ __attribute__((aligned(1024))) half_t ys0[16 * MT * 64], ys1[16 * MT * 64], ys2[16 * MT * 64],
         ys3[16 * MT * 64];
     __shared__ float dgs[4 * 4 * 64], rinv[16 * MT];
@@ -739,23 +485,6 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
         xd.doff = min(p0 + row, a.P - 1) * 4 + s0 * xd.ld4;
     }
     pf_loop_dma_live<F, MT>(W, rb, s0, ksteps, lane, xd, ys0, ys1, ys2, ys3, mt_live, acc);
-#else
-    constexpr int R = MT / 4;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[PfLds<MT>::kA];
-    const int r = threadIdx.x & 63, q = threadIdx.x >> 6;
-    StageAct<R, F::kStageDepth == 1 ? 2 : 4> stage;
-    stage.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
-    stage.ds = make_rsrc(a.x.ds, (size_t)G * ld * 4);
-    stage.ld4 = ld * 4;
-#pragma unroll
-    for (int h = 0; h < R; h++) {
-        const int pos = min(p0 + r + 64 * h, a.P - 1);
-        stage.off[h] = pos * a.I * 2 + 32 * q + s0 * 2 * kStep;
-        stage.doff[h] = pos * 4 + s0 * stage.ld4;
-        stage.inv_ref[h] = 1.0f / ref[r + 64 * h];
-    }
-    pf_loop_live<F, MT>(W, rb, s0, ksteps, lane, stage, (half_t *)smem, r * kAStride + 16 * q, mt_live, acc);
-#endif
     float *ypk = a.ypart + (size_t)kq * a.P * a.H;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
