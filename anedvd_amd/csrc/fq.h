@@ -18,6 +18,14 @@ namespace anedvd {
 #define ANEDVD_PF_DEPTH_L 1
 #endif
 constexpr int kPfTiles = 4;   // 16-row tiles per wavefront: each staged A read feeds four MFMAs
+// Cache policy of the weight loads.  The grouped GEMM reads an expert's weight
+// slice once per chunk of its group (the chunks of one row group run side by
+// side on one XCD), so the loads keep the default policy and the later chunks hit
+// in L2, where the decode kernels stream every weight once (non-temporal).
+#ifndef ANEDVD_PF_WAUX
+#define ANEDVD_PF_WAUX 0
+#endif
+constexpr int kPfAux = ANEDVD_PF_WAUX;
 
 __device__ inline half_t h_bits(uint32_t b)
 {
@@ -84,7 +92,7 @@ struct FF16 {
 #pragma unroll
             for (int j = 0; j < 2; j++)
                 r.q[tt][j] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).q, 32 * lane, qo + 2048 * ts.idx(tt) + 16 * j,
-                                                                   kNT);
+                                                                   kPfAux);
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
     __device__ static inline half8 bop(const Raw &r, const State &, int, int tt, int j, int) { return as_h8(r.q[tt][j]); }
@@ -106,8 +114,8 @@ struct FQ8_0 {
         const int qo = lane_plane_off(ts.src(0), rb, s, 16), so = row_plane_off(ts.src(0), rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).q, 16 * lane, qo + 1024 * ts.idx(tt), kNT);
-            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ts.idx(tt), kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).q, 16 * lane, qo + 1024 * ts.idx(tt), kPfAux);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ts.idx(tt), kPfAux);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -134,8 +142,8 @@ struct FQ4_0 {
         const int qo = lane_plane_off(ts.src(0), rb, s, 8), so = row_plane_off(ts.src(0), rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kNT);
-            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ts.idx(tt), kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kPfAux);
+            r.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ts.idx(tt), kPfAux);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -170,17 +178,17 @@ struct FQLegacy {
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
             const int ti = ts.idx(tt);
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ti, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ti, kPfAux);
             if constexpr (kHasMin)
-                r.s[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).s, 8 * (lane & 15), so + 128 * ti, kNT);
+                r.s[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).s, 8 * (lane & 15), so + 128 * ti, kPfAux);
             else
-                r.s[tt].x = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ti, kNT);
+                r.s[tt].x = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).s, 4 * (lane & 15), so + 64 * ti, kPfAux);
         }
         if constexpr (kFive) {
             const int ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, ho + 128 * ts.idx(tt), kNT);
+                r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, ho + 128 * ts.idx(tt), kPfAux);
         }
     }
     __device__ static inline void begin(const Raw &, State &, int, int) {}
@@ -229,12 +237,12 @@ struct FQ4_K {
         const int qo = lane_plane_off(p, rb, s, 8);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++)
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kPfAux);
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ts.idx(tt), kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ts.idx(tt), kPfAux);
         }
     }
     // The 6-bit scales and mins of getScaleMinK4 (gguf.zig:948-958) for all eight
@@ -296,14 +304,14 @@ struct FQ5_K {
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 2);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kNT);
-            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, ho + 128 * ts.idx(tt), kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kPfAux);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, ho + 128 * ts.idx(tt), kPfAux);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ts.idx(tt), kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ts.idx(tt), kPfAux);
         }
     }
     __device__ static inline void begin(const Raw &r, State &st, int ss, int lane)
@@ -351,21 +359,21 @@ struct FQ23K {
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
             const int ti = ts.idx(tt);
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).q, 4 * lane, qo + 256 * ti, kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).q, 4 * lane, qo + 256 * ti, kPfAux);
             if constexpr (kThree)
                 r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, lane_plane_off(p, rb, s, 2) + 128 * ti,
-                                                               kNT);
+                                                               kPfAux);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, kThree ? 2 : 4);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++) {
                 const int ti = ts.idx(tt);
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ti, kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ti, kPfAux);
                 if constexpr (kThree)
-                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).d, 2 * (lane & 15), dof + 32 * ti, kNT);
+                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).d, 2 * (lane & 15), dof + 32 * ti, kPfAux);
                 else
-                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).d, 4 * (lane & 15), dof + 64 * ti, kNT);
+                    r.dm[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).d, 4 * (lane & 15), dof + 64 * ti, kPfAux);
             }
         }
     }
@@ -430,16 +438,16 @@ struct FQ6_K {
         const int qo = lane_plane_off(p, rb, s, 8), ho = lane_plane_off(p, rb, s, 4);
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++) {
-            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kNT);
-            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).h, 4 * lane, ho + 256 * ts.idx(tt), kNT);
+            r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kPfAux);
+            r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).h, 4 * lane, ho + 256 * ts.idx(tt), kPfAux);
         }
         if ((s & 3) == 0) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, 2);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++) {
                 const int ti = ts.idx(tt);
-                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ti, kNT);
-                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).d, 2 * (lane & 15), dof + 32 * ti, kNT);
+                r.sc[tt] = __builtin_amdgcn_raw_buffer_load_b128(ts.src(tt).s, 16 * (lane & 15), so + 256 * ti, kPfAux);
+                r.d[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).d, 2 * (lane & 15), dof + 32 * ti, kPfAux);
             }
         }
     }
