@@ -325,6 +325,9 @@ __device__ inline void route_token(const float (&v)[4], int t, int E, int k, int
 //      16384 entries rank by segments instead (dispatch_segments: no atomics, the
 //      ids loaded once); beyond that the entries go in chunks of C, and a
 //      block-wide scan of the popcounts of the flattened bitmap gives the counts.
+//      (launch_dispatch sends calls of more than kDispBlock entries to
+//      k_dispatch_multi, one workgroup per block of entries; the routed-and-
+//      dispatched launch takes at most 16 tokens.)
 // Outputs: offsets[E+1]; rows/slots[T*k] grouped by expert, tokens ascending;
 // inv[t*k+s] = position of (t, s) or -1 for an expert id >= E; active[0..n) =
 // experts with tokens, ascending; meta[0] = n, meta[1] = largest group,
@@ -373,7 +376,7 @@ __device__ inline int wave_incl_scan(int v, int)
 // s.off gets the offsets.
 __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets, int32_t *__restrict__ active,
                                  int32_t *__restrict__ meta, uint64_t *__restrict__ chunks, int chunk, int n_routed,
-                                 DispLds &s)
+                                 DispLds &s, bool write = true)
 {
     int c[4], tot = 0, nz = 0, mx = 0;
 #pragma unroll
@@ -395,13 +398,17 @@ __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__res
         const int e = lane * 4 + q;
         if (e < E) {
             s.off[e] = run;
-            offsets[e] = run;
-            if (c[q]) active[runa++] = e;
-            if (chunks)
-                for (int j = 0; j * chunk < c[q]; j++) chunks[runc++] = chunk_entry(e, run + j * chunk, min(chunk, c[q] - j * chunk));
+            if (write) {
+                offsets[e] = run;
+                if (c[q]) active[runa++] = e;
+                if (chunks)
+                    for (int j = 0; j * chunk < c[q]; j++)
+                        chunks[runc++] = chunk_entry(e, run + j * chunk, min(chunk, c[q] - j * chunk));
+            }
             run += c[q];
         }
     }
+    if (!write) return;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
     if (lane == 63) {
@@ -795,6 +802,107 @@ __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__res
                                  d.n_routed, s);
 }
 
+// Dispatch of more entries than one workgroup ranks at once, by kDispBlock-entry
+// blocks, one workgroup each and no communication between them.  Every workgroup
+// counts all P entries per expert (the totals give the offsets) and, apart, the
+// entries before its block; then it ranks its own block's entries the way
+// dispatch_segments does (each wavefront 64 entries, same-id lanes found with
+// nine ballots, a prefix over the wavefronts): position = offset[e] + entries of
+// e in earlier blocks + earlier in this block.  Workgroup 0 also writes the
+// offsets, the active experts, the chunk list and meta.  The order is the
+// single-workgroup dispatch's: entries ascending within an expert.
+constexpr int kDispBlock = kDispThreads;  // entries per workgroup: one per thread
+
+// Lanes of the wavefront holding the same 9-bit id as this lane (ids >= E and
+// padding all share 0x1FF, which no expert has).
+__device__ inline uint64_t same_id_lanes(uint32_t e)
+{
+    uint64_t same = ~0ull;
+#pragma unroll
+    for (int bit = 0; bit < 9; bit++) {
+        const bool on = (e >> bit) & 1u;
+        const uint64_t bb = __ballot(on);
+        same &= on ? bb : ~bb;
+    }
+    return same;
+}
+
+__global__ __launch_bounds__(kDispThreads) void k_dispatch_multi(const uint32_t *__restrict__ idx, int P, int k, int E,
+                                                                 Dispatch d)
+{
+    constexpr int NW = kDispThreads / 64;
+    static_assert(NW * kMaxExperts <= kDispWords, "per-wavefront counts live in the bitmap's words");
+    __shared__ DispLds s;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int i0 = (int)blockIdx.x * kDispBlock;  // this block's first entry (a multiple of 64)
+    int32_t *wcnt = reinterpret_cast<int32_t *>(s.bits);  // [NW][kMaxExperts]: this block's counts per wavefront
+    for (int e = tid; e < E; e += kDispThreads) {
+        s.cnt[e] = 0;   // all entries of e
+        s.base[e] = 0;  // entries of e before this block
+    }
+    for (int i = tid; i < NW * kMaxExperts; i += kDispThreads) wcnt[i] = 0;
+    if (tid == 0) s.bad = 0;
+    const int i = i0 + 64 * wv + lane;  // this thread's entry of the block
+    uint32_t e = i < P ? idx[i] : 0x1FFu;
+    __syncthreads();
+    // 1. counts over all entries, 64 at a time per wavefront (eight batches' ids
+    // loaded at once); a group's lowest lane adds its size
+    constexpr int kB = 8;
+    int bad = 0;
+    for (int r0 = 64 * wv; r0 < P; r0 += 64 * NW * kB) {  // uniform per wavefront
+        uint32_t ids[kB];
+#pragma unroll
+        for (int q = 0; q < kB; q++) {
+            const int j = r0 + 64 * NW * q + lane;
+            ids[q] = j < P ? idx[j] : 0x1FFu;
+        }
+#pragma unroll
+        for (int q = 0; q < kB; q++) {
+            const int b0 = r0 + 64 * NW * q;
+            if (b0 >= P) break;  // uniform
+            uint32_t x = ids[q];
+            if (x >= (uint32_t)E) {
+                bad += b0 + lane < P;
+                x = 0x1FFu;
+            }
+            const uint64_t same = same_id_lanes(x);
+            if (x < (uint32_t)E && __popcll(same & ((1ull << lane) - 1ull)) == 0) {
+                const int c = __popcll(same);
+                atomicAdd(&s.cnt[x], c);
+                if (b0 < i0) atomicAdd(&s.base[x], c);
+            }
+        }
+    }
+    if (bad) atomicAdd(&s.bad, bad);
+    // 2. this block's entries: wavefront w the 64 from i0 + 64 w, ranked within the wavefront
+    if (e >= (uint32_t)E) e = 0x1FFu;
+    const uint64_t same = same_id_lanes(e);
+    const int below = __popcll(same & ((1ull << lane) - 1ull));
+    if (e < (uint32_t)E && below == 0) wcnt[wv * kMaxExperts + e] = __popcll(same);
+    __syncthreads();
+    // 3. the wavefronts' exclusive prefix per expert, and the offsets
+    for (int x = tid; x < E; x += kDispThreads) {
+        int run = 0;
+        for (int w = 0; w < NW; w++) {
+            const int v = wcnt[w * kMaxExperts + x];
+            wcnt[w * kMaxExperts + x] = run;
+            run += v;
+        }
+    }
+    if (wv == NW - 1) dispatch_offsets(E, lane, d.offsets, d.active, d.meta, d.chunks, d.chunk, d.n_routed, s, blockIdx.x == 0);
+    __syncthreads();
+    // 4. positions
+    if (i < P) {
+        int pos = -1;
+        if (e < (uint32_t)E) {
+            pos = s.off[e] + s.base[e] + wcnt[wv * kMaxExperts + e] + below;
+            d.rows[pos] = i / k;
+            d.slots[pos] = i % k;
+        }
+        d.inv[i] = pos;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_act_prep(const float *__restrict__ x, int rows, int K, ActQ xq)
 {
     act_prep_wave(x, rows, K, xq, (size_t)blockIdx.x * 4 + (threadIdx.x >> 6), threadIdx.x & 63);
@@ -839,7 +947,12 @@ int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &
 {
     if (T <= 0) return ANEDVD_OK;
     ANEDVD_TRY(check_route_shape(T, E, k));
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(kDispThreads), 0, st, d_idx, T, k, E, d);
+    const long P = (long)T * k;
+    if (P > kDispBlock)
+        hipLaunchKernelGGL(k_dispatch_multi, dim3((unsigned)((P + kDispBlock - 1) / kDispBlock)), dim3(kDispThreads), 0,
+                           st, d_idx, (int)P, k, E, d);
+    else
+        hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(kDispThreads), 0, st, d_idx, T, k, E, d);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }
