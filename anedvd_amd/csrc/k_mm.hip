@@ -48,6 +48,17 @@ constexpr int kWaves = 4;
 #ifndef ANEDVD_PF_WIDE_MIN
 #define ANEDVD_PF_WIDE_MIN 64
 #endif
+// Groups of at most this many tokens (one decode tile) leave the grouped GEMM for
+// the decode kernels, which stream their weights once per 16-token tile without
+// staging, on a second stream beside the grouped launches; only while the mean
+// group is below ANEDVD_SMALL_MEAN (skewed routing of many experts: most groups
+// then hold a few tokens).  0 turns the split off.
+#ifndef ANEDVD_SMALL_GROUP
+#define ANEDVD_SMALL_GROUP 16
+#endif
+#ifndef ANEDVD_SMALL_MEAN
+#define ANEDVD_SMALL_MEAN 64
+#endif
 constexpr int kCUs = 256;  // MI355X compute units
 #ifdef ANEDVD_MM_WPE
 #define MM_ATTR __attribute__((amdgpu_waves_per_eu(ANEDVD_MM_WPE)))
@@ -910,6 +921,18 @@ static int steps_per_unit(int type) { return tile_fmt(type).spu; }
 
 bool mm_supported(int type) { return tile_fmt(type).qb != 0; }
 
+MmPlan plan_small(const MmPlan &p, int max_u)
+{
+    MmPlan q{};
+    q.kind = kMmDecode;
+    q.mt = 1;
+    q.chunk = 16;
+    q.nchunk = max_u;  // one entry per small group
+    q.ks_gu = 1;
+    q.ks_dn = p.ks_dn;
+    return q;
+}
+
 // Splits a K axis of `units` scale units over ks workgroups, ks dividing units
 // and at most kMaxKS (the partials the combine reads): the smallest ks that gives
 // `wg_per_ks * ks` >= ANEDVD_WG_TARGET workgroups while every wavefront keeps >=
@@ -962,6 +985,8 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u)
         p.ks_dn = I / kStep >= 128 && 10 * r2 <= 18 * r1 && grouped_down_ks_ok(down_type, I, 2) ? 2 : 1;
         p.mt = std::max(p.mt_gu, p.mt_dn);
         p.contig = P >= 2 * 16 * p.mt * (long)max_u;  // experts average two chunks or more
+        // (the decode down writes one K partial: the combine reads the same count for every row)
+        p.small = mean < ANEDVD_SMALL_MEAN && p.ks_dn == 1 ? std::min(ANEDVD_SMALL_GROUP, 16) : 0;
     } else {
         p.kind = kMmDecode;
         p.mt = 1;

@@ -334,7 +334,9 @@ __device__ inline void route_token(const float (&v)[4], int t, int E, int k, int
 // meta[2] = entries with expert id >= E (never written out of bounds); and, when
 // `chunks` is given, the expert kernels' work list: chunks[c] = chunk_entry(e, p0,
 // nt) for each `chunk`-token slice of expert e's group (first position p0, nt
-// tokens), experts ascending, meta[3] = their count.
+// tokens), experts ascending, meta[3] = their count.  With `small` > 0, groups of
+// 1..small tokens go instead to a second list, chunks_s[c] = chunk_entry(e, p0,
+// n), one entry per group, experts ascending, and meta[7] = its count.
 constexpr int kDispWords = 4096;
 
 struct DispLds {
@@ -376,7 +378,7 @@ __device__ inline int wave_incl_scan(int v, int)
 // s.off gets the offsets.
 __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets, int32_t *__restrict__ active,
                                  int32_t *__restrict__ meta, uint64_t *__restrict__ chunks, int chunk, int n_routed,
-                                 DispLds &s, bool write = true)
+                                 uint64_t *__restrict__ chunks_s, int small, DispLds &s, bool write = true)
 {
     int c[4], tot = 0, nz = 0, mx = 0;
 #pragma unroll
@@ -387,12 +389,18 @@ __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__res
         nz += c[q] > 0;
         if (n_routed <= 0 || e < n_routed) mx = max(mx, c[q]);
     }
-    int nch = 0;
+    // groups of 1..small tokens go to the second list, one entry each
+    auto is_small = [&](int n) { return n > 0 && n <= small; };
+    int nch = 0, nsm = 0;
 #pragma unroll
-    for (int q = 0; q < 4; q++) nch += (c[q] + chunk - 1) / chunk;
+    for (int q = 0; q < 4; q++) {
+        if (is_small(c[q])) nsm++;
+        else nch += (c[q] + chunk - 1) / chunk;
+    }
     int run = wave_incl_scan(tot, lane) - tot;
     int runa = wave_incl_scan(nz, lane) - nz;
     int runc = wave_incl_scan(nch, lane) - nch;
+    int runs = wave_incl_scan(nsm, lane) - nsm;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int e = lane * 4 + q;
@@ -401,7 +409,9 @@ __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__res
             if (write) {
                 offsets[e] = run;
                 if (c[q]) active[runa++] = e;
-                if (chunks)
+                if (chunks && is_small(c[q]))
+                    chunks_s[runs++] = chunk_entry(e, run, c[q]);
+                else if (chunks)
                     for (int j = 0; j * chunk < c[q]; j++)
                         chunks[runc++] = chunk_entry(e, run + j * chunk, min(chunk, c[q] - j * chunk));
             }
@@ -415,6 +425,7 @@ __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__res
         offsets[E] = run;
         meta[0] = runa;
         meta[3] = runc;
+        if (small) meta[7] = runs;
     }
     if (lane == 0) {
         meta[1] = mx;
@@ -439,7 +450,7 @@ __device__ __forceinline__ void dispatch_segments(const uint32_t *__restrict__ i
                                   int32_t *__restrict__ offsets, int32_t *__restrict__ rows,
                                   int32_t *__restrict__ slots, int32_t *__restrict__ inv, int32_t *__restrict__ active,
                                   int32_t *__restrict__ meta, uint64_t *__restrict__ chunks, int chunk, int n_routed,
-                                  DispLds &s)
+                                  uint64_t *__restrict__ chunks_s, int small, DispLds &s)
 {
     constexpr int NW = NTH / 64;
     static_assert(NW * kMaxExperts <= kDispWords, "per-wavefront counts live in the bitmap's words");
@@ -494,7 +505,7 @@ __device__ __forceinline__ void dispatch_segments(const uint32_t *__restrict__ i
         s.cnt[e] = run;
     }
     __syncthreads();
-    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, s);
+    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, chunks_s, small, s);
     __syncthreads();
     // Each entry's position (inv, written in entry order); the entries go to LDS by
     // position, so rows and slots are written in position order (coalesced) rather
@@ -536,7 +547,7 @@ template <int NTH>
 __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
                                int32_t *__restrict__ rows, int32_t *__restrict__ slots, int32_t *__restrict__ inv,
                                int32_t *__restrict__ active, int32_t *__restrict__ meta, uint64_t *__restrict__ chunks,
-                               int chunk, int n_routed, DispLds &s)
+                               int chunk, int n_routed, uint64_t *__restrict__ chunks_s, int small, DispLds &s)
 {
     static_assert(NTH >= 128, "wavefront 0 computes the offsets while the others prefix the bitmap");
     const int P = T * k, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -563,7 +574,7 @@ __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx,
         if (bad) atomicAdd(&s.bad, bad);
         __syncthreads();
         if (wv == 0) {
-            dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, s);
+            dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, chunks_s, small, s);
         } else {
             for (int e = tid - 64; e < E; e += NTH - 64) {
                 int run = 0;
@@ -589,7 +600,8 @@ __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx,
         return;
     }
     if (P <= (NTH / 64) * 64 * kSegBatches) {
-        dispatch_segments<NTH>(idx, P, k, E, offsets, rows, slots, inv, active, meta, chunks, chunk, n_routed, s);
+        dispatch_segments<NTH>(idx, P, k, E, offsets, rows, slots, inv, active, meta, chunks, chunk, n_routed, chunks_s,
+                               small, s);
         return;
     }
     for (int e = tid; e < E; e += NTH) {
@@ -606,7 +618,7 @@ __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx,
     }
     if (bad) atomicAdd(&s.bad, bad);
     __syncthreads();
-    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, s);
+    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, chunks_s, small, s);
     // bitmap words per expert per chunk of entries
     const int W = max(1, kDispWords / E);
     const int C = 32 * W, NW = W * E;
@@ -791,7 +803,7 @@ __global__ __launch_bounds__(kDispThreads) void k_route_dispatch(RouteArgs a, Di
         ids[(i / a.n_sh) * a.kk + a.k + i % a.n_sh] = (uint32_t)(a.E + i % a.n_sh);
     __syncthreads();
     dispatch_block<kDispThreads>(ids, a.T, a.kk, a.E + a.n_sh, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta,
-                                 d.chunks, d.chunk, d.n_routed, s);
+                                 d.chunks, d.chunk, d.n_routed, d.chunks_s, d.small, s);
 }
 
 __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
@@ -799,7 +811,7 @@ __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__res
 {
     __shared__ DispLds s;
     dispatch_block<kDispThreads>(idx, T, k, E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, d.chunks, d.chunk,
-                                 d.n_routed, s);
+                                 d.n_routed, d.chunks_s, d.small, s);
 }
 
 // Dispatch of more entries than one workgroup ranks at once, by kDispBlock-entry
@@ -889,7 +901,8 @@ __global__ __launch_bounds__(kDispThreads) void k_dispatch_multi(const uint32_t 
             run += v;
         }
     }
-    if (wv == NW - 1) dispatch_offsets(E, lane, d.offsets, d.active, d.meta, d.chunks, d.chunk, d.n_routed, s, blockIdx.x == 0);
+    if (wv == NW - 1) dispatch_offsets(E, lane, d.offsets, d.active, d.meta, d.chunks, d.chunk, d.n_routed, d.chunks_s, d.small,
+                                      s, blockIdx.x == 0);
     __syncthreads();
     // 4. positions
     if (i < P) {

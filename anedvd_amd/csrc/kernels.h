@@ -19,11 +19,27 @@ struct ActQ {
 // of active experts, meta[1] = largest group, meta[2] = ids >= E, meta[3] = number
 // of chunks; chunks[] (optional) = chunk_entry(e, p0, nt) for each `chunk`-token
 // slice of expert e's group, experts ascending -- the expert kernels' work list.
+// With small > 0, groups of 1..small tokens are listed in chunks_s instead (one
+// entry per group, experts ascending; meta[7] = their count, meta holding 8 ints).
 struct Dispatch {
     int32_t *offsets, *rows, *slots, *inv, *active, *meta;
     uint64_t *chunks;  // the work list: chunk_entry(e, first position, tokens) per chunk
     int chunk;
     int n_routed;  // meta[1] counts experts below this one only (0 = all): merged shared pieces are not groups
+    uint64_t *chunks_s;  // the small groups' list (small > 0)
+    int small;
+
+    // The small groups' list as a work list of its own (count in meta[3] of the view).
+    Dispatch small_view(int chunk_s) const
+    {
+        Dispatch v = *this;
+        v.meta = meta + 4;
+        v.chunks = chunks_s;
+        v.chunk = chunk_s;
+        v.chunks_s = nullptr;
+        v.small = 0;
+        return v;
+    }
 };
 
 // A work-list entry: expert e (< 256), the chunk's first position p0 and its
@@ -85,10 +101,14 @@ struct MmPlan {
     int contig;   // grouped GEMM: XCD-contiguous workgroup order
     int chunk;    // tokens per work-list chunk (16 mt), the dispatch's `chunk`
     int nchunk;   // bound on the work list's length: P / chunk + max_u
+    int small;    // grouped GEMM: groups of at most this many tokens go to the decode kernels (0 = none)
 };
 bool mm_supported(int type);
 // P (token, slot) entries over at most max_u experts.
 MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u);
+// The decode-kernel plan for the small groups of a grouped plan (p.small > 0):
+// one 16-token chunk per group, K not split, the same down partial count.
+MmPlan plan_small(const MmPlan &p, int max_u);
 // gate/up + SiLU(gate)*up for every dispatched (token, expert) position, written
 // to `act` [P][I] in the activation format.  With plan.ks_gu > 1 the K partials
 // go to `part` [ks][P][2][I] and a second launch finishes them.

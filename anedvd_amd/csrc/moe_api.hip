@@ -250,10 +250,14 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     x.d.slots = c.take<int32_t>(P);
     x.d.inv = c.take<int32_t>(P);
     x.d.active = c.take<int32_t>(E);
-    x.d.meta = c.take<int32_t>(4);
+    x.d.meta = c.take<int32_t>(8);
     x.d.chunks = c.take<uint64_t>((size_t)x.plan.nchunk);
     x.d.chunk = x.plan.chunk;
     x.d.n_routed = L->E;
+    if (x.plan.small) {
+        x.d.chunks_s = c.take<uint64_t>((size_t)x.max_u);
+        x.d.small = x.plan.small;
+    }
     x.xq = ActQ{c.take<half_t>((size_t)T * H), c.take<float>((size_t)T * (H / kStep)), T};
     x.act = ActQ{c.take<half_t>((size_t)P * I), c.take<float>((size_t)P * (I / kStep)), P};
     x.part = x.plan.ks_gu > 1 ? c.take<float>((size_t)x.plan.ks_gu * P * 2 * I) : nullptr;
@@ -310,6 +314,18 @@ __global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__res
     if (threadIdx.x == 0) scale[t] = shared_sigmoid(g);
 }
 
+// The gate/up (which 0) or down (1) of the groups of at most plan.small tokens, on
+// the decode kernels from the dispatch's second list: they write their own
+// positions of act and rows of ypart, so they may run beside the grouped launches.
+static int launch_small_groups(const anedvd_moe_layer *L, const Fwd &f, int which, hipStream_t st)
+{
+    const int H = L->H, I = L->I, kk = L->k + (int)L->n_sh;
+    const MmPlan ps = plan_small(f.plan, f.max_u);
+    const Dispatch dsm = f.d.small_view(ps.chunk);
+    return which == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, dsm, f.P, ps, nullptr, f.act, L->gelu, st)
+                      : launch_expert_down(L->down, f.act, H, I, dsm, f.P, ps, f.ypart, kk, st);
+}
+
 // One forward call on stream st.  With `resid` the output is resid + the block's
 // output (the engine's x += proj, main.zig:519), as a stack of layers chains it.
 int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_logits, float *d_out, const Fwd &f,
@@ -335,7 +351,10 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
     // the routed experts, joined before the combine.  With stage events everything
     // stays on `st`, so the stages time one at a time.
     const bool separate = L->Is && !L->n_sh;
-    const bool fork = separate && !ev;
+    // Groups of a few tokens (plan.small) run on the decode kernels beside the
+    // grouped GEMM, on the second stream.
+    const bool small = f.plan.small > 0;
+    const bool fork = (separate || small) && !ev;
     hipStream_t ss = fork ? L->ctx->aux : st;
     if (fork) {
         ANEDVD_HIP(hipEventRecord(L->ctx->fork, st));
@@ -350,12 +369,18 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
         return launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_ypart, 1, ss);
     };
     if (fork) {
-        ANEDVD_TRY(shared());
+        if (small) {
+            ANEDVD_TRY(launch_small_groups(L, f, 0, ss));
+            ANEDVD_TRY(launch_small_groups(L, f, 1, ss));
+        }
+        if (separate) ANEDVD_TRY(shared());
         ANEDVD_HIP(hipEventRecord(L->ctx->join, ss));
     }
     ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act, L->gelu, st));
+    if (small && !fork) ANEDVD_TRY(launch_small_groups(L, f, 0, st));
     mark(2);
     ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart, kk, st));
+    if (small && !fork) ANEDVD_TRY(launch_small_groups(L, f, 1, st));
     mark(3);
     if (fork) ANEDVD_HIP(hipStreamWaitEvent(st, L->ctx->join, 0));
     else if (separate) ANEDVD_TRY(shared());
@@ -939,9 +964,9 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *L, const float *h, size_t T, cons
     ANEDVD_HIP(hipMemcpyAsync(f.h_in, h, T * L->H * 4, hipMemcpyHostToDevice, st));
     if (logits) ANEDVD_HIP(hipMemcpyAsync(f.l_in, logits, T * L->E * 4, hipMemcpyHostToDevice, st));
     ANEDVD_TRY(forward_device(L, f.h_in, (int)T, logits ? f.l_in : nullptr, f.out, f, st, nullptr));
-    int32_t meta[4] = {0, 0, 0, 0};
+    int32_t meta[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     ANEDVD_HIP(hipMemcpyAsync(out, f.out, T * L->H * 4, hipMemcpyDeviceToHost, st));
-    ANEDVD_HIP(hipMemcpyAsync(meta, f.d.meta, 16, hipMemcpyDeviceToHost, st));
+    ANEDVD_HIP(hipMemcpyAsync(meta, f.d.meta, sizeof(meta), hipMemcpyDeviceToHost, st));
     ANEDVD_HIP(hipStreamSynchronize(st));
     if (stats) {
         stats->n_tokens = (uint32_t)T;
@@ -952,6 +977,7 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *L, const float *h, size_t T, cons
         stats->path = f.plan.kind == kMmStaged ? 1 : 0;
         stats->chunk = (uint32_t)f.plan.chunk;
         stats->down_ks = (uint32_t)f.plan.ks_dn;
+        stats->small_groups = f.plan.small ? (uint32_t)meta[7] : 0u;
     }
     return ANEDVD_OK;
 }
@@ -1182,7 +1208,8 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
     }
     if (kernel_ms && (flags & ANEDVD_TIME_EXPERT_SOLO)) {
         // The routed expert products alone: `iters` back-to-back launches of the
-        // gate/up (then the down) kernels over the rotated layers, reading the
+        // gate/up (then the down) kernels over the rotated layers (with the small
+        // groups' launch after each grouped one, serially), reading the
         // dispatch, activations and gate/up output the last call left in place (the
         // calls above routed the same inputs).  Events bracket each loop only.
         const int H = layers[0]->H, I = layers[0]->I, P = (int)T * (int)(layers[0]->k + layers[0]->n_sh);
@@ -1195,10 +1222,12 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
                 const anedvd_moe_layer *L = layers[(size_t)i % n_layers];
                 if (s == 2)  // the router GEMV alone: T tokens of d_h against the layer's [E][H] f16 router
                     return launch_router(L->router_t, L->router, d_h, (int)T, (int)L->E, H, f.logits, st);
-                return s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act,
-                                                     L->gelu, st)
-                              : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart,
-                                                   (int)(L->k + L->n_sh), st);
+                const int rc = s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part,
+                                                             f.act, L->gelu, st)
+                                      : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart,
+                                                           (int)(L->k + L->n_sh), st);
+                // the small groups' decode launch after it, on the same stream
+                return rc == ANEDVD_OK && f.plan.small ? launch_small_groups(L, f, s, st) : rc;
             };
             for (int i = 0; i < warmup && src == ANEDVD_OK; i++) src = launch(i);
             if (src == ANEDVD_OK && hipEventRecord(a, st) != hipSuccess) src = ANEDVD_E_HIP;

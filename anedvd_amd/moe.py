@@ -73,7 +73,7 @@ class GgufMoeOpts(C.Structure):
 class Stats(C.Structure):
     _fields_ = [("n_tokens", C.c_uint32), ("touched_experts", C.c_uint32), ("weight_bytes", C.c_uint64),
                 ("max_group", C.c_uint32), ("path", C.c_uint32), ("chunk", C.c_uint32),
-                ("down_ks", C.c_uint32)]
+                ("down_ks", C.c_uint32), ("small_groups", C.c_uint32)]
 
 
 # every symbol include/anedvd_moe.h declares, with its ctypes signature
@@ -395,7 +395,7 @@ class MoeLayer:
         if stats:
             return out, {"touched_experts": st.touched_experts, "weight_bytes": st.weight_bytes,
                          "max_group": st.max_group, "path": st.path, "chunk": st.chunk,
-                         "down_ks": st.down_ks}
+                         "down_ks": st.down_ks, "small_groups": st.small_groups}
         return out
 
     def forward_device(self, d_h: int, n_tokens: int, d_logits: int | None, d_out: int):

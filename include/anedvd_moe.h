@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define ANEDVD_MOE_ABI_VERSION 3
+#define ANEDVD_MOE_ABI_VERSION 4
 
 /* ggml tensor type ids as stored in GGUF (gguf.zig:30-46). */
 enum anedvd_ggml_type {
@@ -89,6 +89,7 @@ typedef struct {
     uint32_t path;                 /* expert kernels: 0 = decode (16-token tiles), 1 = grouped GEMM */
     uint32_t chunk;                /* tokens per expert-kernel work item: 16, 64 or 128 */
     uint32_t down_ks;              /* K shares of the down product (partial planes the combine adds) */
+    uint32_t small_groups;         /* grouped GEMM calls: groups of <= 16 tokens run on the decode kernels */
 } anedvd_moe_stats;
 
 /* ------------------------------------------------------------------ lifetime */

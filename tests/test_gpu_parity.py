@@ -404,6 +404,63 @@ def test_forward_grouped_split_k_down(ctx, types):
     assert st["path"] == 1 and st["down_ks"] == 2
 
 
+# Sixteen groups averaging 42.5 tokens (the grouped GEMM), six of them of 1 to 16
+# tokens (the decode kernels, beside it).
+SMALL_SIZES = [1, 3, 8, 16, 17, 30, 64, 65, 90, 120, 130, 10, 5, 50, 40, 31]
+SMALL_SHARED = [dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="small-shared-merged", hidden=256, inter=4096,
+                                    n_experts=16, k=2, shared_inter=4096, shared_gated=True),
+                dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="small-shared-separate", hidden=256, inter=4096,
+                                    n_experts=16, k=2, shared_inter=2048, shared_type=W.Q4_0, shared_gated=True)]
+
+
+@pytest.mark.parametrize("types", FORMATS, ids=lambda t: "/".join(W.TYPE_NAMES[x] for x in t))
+def test_forward_grouped_small_groups(ctx, types):
+    """A skewed call on the grouped GEMM: the groups of at most 16 tokens go to the
+    dispatch's second work list and run on the decode kernels (second stream), the
+    rest on the grouped GEMM, every format."""
+    lg = _logits_for_groups(SMALL_SIZES, seed=31)
+    spec = dataclasses.replace(W.MIXTRAL_8X7B_Q4_0, name="small-groups", hidden=256, inter=4096, n_experts=16,
+                               gate_type=types[0], up_type=types[1], down_type=types[2], scale_sigma=0.01)
+    L = synth.make_layer(spec, seed=31)
+    h = synth.activations(spec, lg.shape[0], seed=31)
+    layer = moe.MoeLayer(ctx, spec, L)
+    got, st = layer.forward(h, lg, stats=True)
+    layer.free()
+    want = O.OracleLayer(spec, L).forward(h, lg, fast=True)
+    err = moe.rel_l2(got, want)
+    print(f"\nsmall groups {types}: rel-L2 {err:.3e}, small groups {st['small_groups']}")
+    assert err <= REL_L2_TOL
+    assert st["path"] == 1 and st["max_group"] == max(SMALL_SIZES)
+    assert st["small_groups"] == sum(1 for n in SMALL_SIZES if n <= 16)
+
+
+@pytest.mark.parametrize("spec", SMALL_SHARED, ids=lambda s: s.name)
+def test_forward_small_groups_with_shared_expert(ctx, spec):
+    """Small groups beside a shared expert merged as pieces (large groups of their
+    own) and beside a separate one (both on the second stream, one join); the
+    stage-timed call (one stream) and the HIP-graph replay compute the same bits
+    as the direct call."""
+    lg = _logits_for_groups(SMALL_SIZES, seed=37)
+    T = lg.shape[0]
+    L = synth.make_layer(spec, seed=37)
+    h = synth.activations(spec, T, seed=37)
+    layer = moe.MoeLayer(ctx, spec, L)
+    got, st = layer.forward(h, lg, stats=True)
+    want = O.OracleLayer(spec, L).forward(h, lg, fast=True)
+    err = moe.rel_l2(got, want)
+    print(f"\n{spec.name}: rel-L2 {err:.3e}, small groups {st['small_groups']}")
+    assert err <= REL_L2_TOL
+    assert st["path"] == 1 and st["small_groups"] == sum(1 for n in SMALL_SIZES if n <= 16)
+    d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lg), ctx.alloc(T * spec.hidden * 4)
+    for kw in (dict(stages=True), dict(graph=True), dict()):
+        moe.time_forward([layer], d_h, T, d_lg, d_out, 0, 2, **kw)
+        again = ctx.from_device(d_out, (T, spec.hidden), np.float32)
+        assert np.array_equal(bits(again), bits(got)), kw
+    for p in (d_h, d_lg, d_out):
+        ctx.free(p)
+    layer.free()
+
+
 @pytest.mark.parametrize("T", [1, 16, 160])
 def test_forward_mixtral_shape_q4_0(ctx, T):
     """Mixtral-8x7B proportions (hidden 4096, top-2 of 8) with the expert width cut to
