@@ -669,6 +669,36 @@ int launch_f32_to_f16(const float *d_src, uint16_t *d_dst, size_t n, hipStream_t
     return ANEDVD_OK;
 }
 
+// f16 -> f32 (exact), eight values per thread: the f16-activation forward's input
+// widened into the call's staging.
+__global__ __launch_bounds__(256) void k_f16_to_f32(const uint16_t *__restrict__ src, float *__restrict__ dst,
+                                                   size_t n)
+{
+    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i + 8 <= n && (((uintptr_t)(src + i) | (uintptr_t)(dst + i)) & 15) == 0) {
+        const uint4 v = *(const uint4 *)(src + i);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        float4 lo, hi;
+        lo.x = f16_bits_to_f32((uint16_t)w[0]); lo.y = f16_bits_to_f32((uint16_t)(w[0] >> 16));
+        lo.z = f16_bits_to_f32((uint16_t)w[1]); lo.w = f16_bits_to_f32((uint16_t)(w[1] >> 16));
+        hi.x = f16_bits_to_f32((uint16_t)w[2]); hi.y = f16_bits_to_f32((uint16_t)(w[2] >> 16));
+        hi.z = f16_bits_to_f32((uint16_t)w[3]); hi.w = f16_bits_to_f32((uint16_t)(w[3] >> 16));
+        *(float4 *)(dst + i) = lo;
+        *(float4 *)(dst + i + 4) = hi;
+    } else {
+        for (size_t j = i; j < n && j < i + 8; j++) dst[j] = f16_bits_to_f32(src[j]);
+    }
+}
+
+int launch_f16_to_f32(const uint16_t *d_src, float *d_dst, size_t n, hipStream_t st)
+{
+    if (n == 0) return ANEDVD_OK;
+    const size_t threads = (n + 7) / 8;
+    hipLaunchKernelGGL(k_f16_to_f32, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, d_src, d_dst, n);
+    ANEDVD_HIP(hipGetLastError());
+    return ANEDVD_OK;
+}
+
 int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st)
 {
     const size_t n = (size_t)m.rows * (m.cols / block_elems(m.type));

@@ -55,6 +55,7 @@ int launch_dequant_gguf(int type, const uint8_t *d_src, size_t n_blocks, float *
 int launch_repack(const QMat &m, const uint8_t *d_src, hipStream_t st);
 int launch_dequant_tiles(const QMat &m, int mat, float *d_out, hipStream_t st);
 int launch_f32_to_f16(const float *d_src, uint16_t *d_dst, size_t n, hipStream_t st);
+int launch_f16_to_f32(const uint16_t *d_src, float *d_dst, size_t n, hipStream_t st);
 
 // k_route.hip
 constexpr int kMaxRouteExperts = 256;  // experts the route and dispatch kernels take (ids fit a byte)

@@ -994,6 +994,21 @@ int anedvd_moe_layer_forward_device(anedvd_moe_layer *L, const float *d_h, size_
     return forward_device(L, d_h, (int)T, d_logits, d_out, f, L->ctx->stream, nullptr);
 }
 
+int anedvd_moe_layer_forward_device_f16(anedvd_moe_layer *L, const uint16_t *d_h, size_t T, const float *d_logits,
+                                        float *d_out)
+{
+    if (!d_h || !d_out) {
+        set_error("layer_forward_device_f16: null pointer");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    Fwd f;
+    ANEDVD_TRY(prepare(L, T, true, f));
+    if (!T) return ANEDVD_OK;
+    hipStream_t st = L->ctx->stream;
+    ANEDVD_TRY(launch_f16_to_f32(d_h, f.h_in, T * L->H, st));
+    return forward_device(L, f.h_in, (int)T, d_logits, d_out, f, st, nullptr);
+}
+
 int anedvd_moe_layer_forward_device_noalloc(anedvd_moe_layer *L, const float *d_h, size_t T, const float *d_logits,
                                             float *d_out)
 {

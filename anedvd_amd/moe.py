@@ -100,6 +100,7 @@ SIGNATURES = {
     "anedvd_moe_layer_forward": (_i, [_vp, _vp, _sz, _vp, _vp, C.POINTER(Stats)]),
     "anedvd_moe_layer_forward_device": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "anedvd_moe_layer_forward_device_noalloc": (_i, [_vp, _vp, _sz, _vp, _vp]),
+    "anedvd_moe_layer_forward_device_f16": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "anedvd_moe_device_alloc": (_i, [_vp, _sz, C.POINTER(_vp)]),
     "anedvd_moe_device_free": (_i, [_vp, _vp]),
     "anedvd_moe_memcpy_h2d": (_i, [_vp, _vp, _vp, _sz]),
@@ -400,6 +401,10 @@ class MoeLayer:
 
     def forward_device(self, d_h: int, n_tokens: int, d_logits: int | None, d_out: int):
         _check(lib().anedvd_moe_layer_forward_device(self.h, d_h, n_tokens, d_logits, d_out))
+
+    def forward_device_f16(self, d_h16: int, n_tokens: int, d_logits: int | None, d_out: int):
+        """forward_device with [T][H] f16 activations (bits), widened exactly on the device."""
+        _check(lib().anedvd_moe_layer_forward_device_f16(self.h, d_h16, n_tokens, d_logits, d_out))
 
     def forward_device_noalloc(self, d_h: int, n_tokens: int, d_logits: int | None, d_out: int):
         """forward_device on the library's static per-GPU scratch: no allocation."""

@@ -237,6 +237,14 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *layer, const float *h, size_t n_t
 int anedvd_moe_layer_forward_device(anedvd_moe_layer *layer, const float *d_h, size_t n_tokens,
                                     const float *d_logits, float *d_out);
 
+/* Same with f16 activations: d_h holds [T][H] IEEE binary16 bits (the fp16
+ * activations of the benchmarked Mixtral-8x7B layer).  Each value is widened to
+ * f32 exactly on the device and the call then equals anedvd_moe_layer_forward_device
+ * on the widened rows, bit for bit (the reference's blocks take f32 h,
+ * cpu.zig:1141-1185; main.zig:488-520).  Output and logits stay f32. */
+int anedvd_moe_layer_forward_device_f16(anedvd_moe_layer *layer, const uint16_t *d_h, size_t n_tokens,
+                                        const float *d_logits, float *d_out);
+
 /* anedvd_moe_layer_forward_device without any allocation.  It has no counterpart
  * in the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The

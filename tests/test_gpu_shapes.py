@@ -335,3 +335,31 @@ def test_call_above_the_token_limit_is_rejected(ctx):
     assert ei.value.name == "InvalidArgument"
     ctx.free(d_h)
     layer.free()
+
+
+@pytest.mark.parametrize("T", [1, 64, 300])
+def test_forward_f16_activations(ctx, T):
+    """fp16 activations (the Mixtral-8x7B workload's input option): the f16 entry
+    widens each value exactly, so it computes the f32 entry's bits on the widened
+    rows, at decode (1, 64 tokens) and grouped-GEMM (300 tokens) sizes; and the
+    oracle agrees on the widened rows."""
+    spec = dataclasses.replace(W.MIXTRAL_8X7B_Q4_0, name="f16-activations", inter=2048)
+    L = synth.make_layer(spec, seed=41)
+    h16 = (synth.activations(spec, T, seed=41) * 0.75).astype(np.float16)
+    h32 = h16.astype(np.float32)
+    layer = moe.MoeLayer(ctx, spec, L)
+    n = T * spec.hidden
+    d16, d32, o16, o32 = ctx.to_device(h16.view(np.uint16)), ctx.to_device(h32), ctx.alloc(n * 4), ctx.alloc(n * 4)
+    layer.forward_device_f16(d16, T, None, o16)
+    layer.forward_device(d32, T, None, o32)
+    got = ctx.from_device(o16, (T, spec.hidden), np.float32)
+    ref = ctx.from_device(o32, (T, spec.hidden), np.float32)
+    for p in (d16, d32, o16, o32):
+        ctx.free(p)
+    layer.free()
+    assert np.array_equal(bits(got), bits(ref))
+    rows = sample_rows(T, min(T, 16), seed=41)
+    want = O.OracleLayer(spec, L).forward(h32[rows], fast=True)
+    err = moe.rel_l2(got[rows], want)
+    print(f"\nf16 activations T={T}: rel-L2 {err:.3e} on {len(rows)} tokens")
+    assert err <= REL_L2_TOL
