@@ -477,6 +477,33 @@ struct AOp {
     int ld4;
 };
 
+// The same operands from LDS: the fused-reduce down kernel's prologue writes its
+// 16 MT rows there, for its steps [s0, s0 + n) only (rows of rowb bytes in the
+// activation format; descales [step][16 MT]).
+template <int MT>
+struct AOpL {
+    const char *q;
+    const float *ds;
+    int qoff[MT];  // byte offset of the lane's row and lane group
+    int doff[MT];  // float offset of its first result token's descale within a step
+    int s0;
+};
+
+template <int MT, int MODE>
+__device__ inline void load_a(AStep<MT, MODE> &x, const AOpL<MT> &a, int s)
+{
+    const int o = (s - a.s0) * 2 * kStep;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        x.a0[mt] = *(const half8 *)(a.q + a.qoff[mt] + o);
+        x.a1[mt] = *(const half8 *)(a.q + a.qoff[mt] + o + 16);
+    }
+    if (MODE == kStepDs) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) x.dv[mt] = *(const f32x4 *)(a.ds + (s - a.s0) * 16 * MT + a.doff[mt]);
+    }
+}
+
 template <int MT, int MODE>
 __device__ inline void load_a(AStep<MT, MODE> &x, const AOp<MT> &a, int s)
 {
@@ -551,9 +578,8 @@ __device__ inline void mm_step(const typename D::Raw &w, typename D::State &st, 
 // at the end of the matrix's planes: out of range, so they read 0 without touching
 // memory.  Activation loads repeat the last step (L2 hits).  sched_barrier keeps
 // the scheduler from sinking the prefetches down to their uses.
-template <class D, int MT, int MODE>
-__device__ inline void mm_steps(const Planes &W, int rb, int s0, int s1, int lane, const AOp<MT> &A,
-                                f32x4 (*acc)[4])
+template <class D, int MT, int MODE, class AS>
+__device__ inline void mm_steps(const Planes &W, int rb, int s0, int s1, int lane, const AS &A, f32x4 (*acc)[4])
 {
     if (s0 >= s1) return;
     const int sl = s1 - 1, so = (W.nrb - rb) * W.steps;
@@ -584,6 +610,7 @@ struct MmArgs {
     ActQ act;        // gate/up output [P][I]
     float *ypart;    // down output [KS][P][H], rows in (token, slot) order
     int H, I, KS, P, use_gelu;
+    int KSg;         // down with KSg > 1: its input is gate/up's KSg partials in `part`, finished in LDS
     int kk;          // slots per token row of ypart
     int nchunk;      // chunk rows of the grid: blockIdx.x = chunk + nchunk * (row block, K share)
 };
@@ -730,7 +757,13 @@ __global__ __launch_bounds__(256) void k_act_reduce(MmArgs a)
 // are consecutive, so tokens past the group's end read other groups' (or, past
 // the last position, out-of-range zero) activations and are not stored.  Position
 // p's result goes to row rows[p] * kk + slots[p] of the output.
-template <class D, int MT>
+//
+// kPart: gate/up split its K over KSg workgroups and left the partials in `part`.
+// The workgroup finishes the activations it reads itself, k_act_reduce's sums in
+// the same order (so the same bits), for its chunk's tokens and its K range only,
+// into LDS (dynamic: 16 MT rows of its steps, and their descales); the K loop then
+// reads them from there.  No launch between gate/up and down.
+template <class D, int MT, bool kPart>
 __global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
 {
     int e, p0, nt;
@@ -738,19 +771,9 @@ __global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
     const int wv = wave_id(), lane = threadIdx.x & 63;
     const int rbk = (int)(blockIdx.x / a.nchunk);
     const int rb = kWaves * (rbk / a.KS) + wv, ks = rbk % a.KS;
-    if (rb >= a.H / kRowBlock) return;  // no barriers in this kernel
     const int units = a.I / kStep / D::kSpu, upw = units / a.KS, u0 = ks * upw;
     const int n = lane & 15, gq = lane >> 4;
     const Planes W = planes(a.w0, e);
-    AOp<MT> A;
-    A.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
-    A.ds = make_rsrc(a.x.ds, (size_t)(a.I / kStep) * a.x.ld * 4);
-    A.ld4 = a.x.ld * 4;
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        A.qoff[mt] = (p0 + 16 * mt + n) * a.I * 2 + 32 * gq;
-        A.doff[mt] = (p0 + 16 * mt + 4 * gq) * 4;
-    }
     int orow[MT][4];  // output rows of the lane's positions (loaded before the K loop)
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
@@ -764,7 +787,55 @@ __global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int t = 0; t < 4; t++) acc[mt][t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    mm_steps<D, MT, kStepDs>(W, rb, u0 * D::kSpu, (u0 + upw) * D::kSpu, lane, A, acc);
+    if constexpr (kPart) {
+        extern __shared__ __attribute__((aligned(16))) char lds_act[];
+        const int sw = upw * D::kSpu, s0 = u0 * D::kSpu;  // the workgroup's steps
+        const int rowb = sw * 2 * kStep;
+        float *lds_ds = reinterpret_cast<float *>(lds_act + 16 * MT * rowb);
+        for (int i = threadIdx.x; i < (16 * MT - nt) * rowb / 16; i += 256)
+            reinterpret_cast<u32x4 *>(lds_act + nt * rowb)[i] = (u32x4){0u, 0u, 0u, 0u};
+        for (int i = threadIdx.x; i < sw * 16 * MT; i += 256)
+            if (i % (16 * MT) >= nt) lds_ds[i] = 0.0f;
+        // one wavefront per (token, step) of the range: sum the KSg partials of
+        // gate and up in partial order, SiLU(g) * u, the group's power of two
+        for (int t = wv; t < nt * sw; t += kWaves) {  // uniform per wavefront
+            const int m = t / sw, g = t - m * sw;
+            const size_t c = (size_t)kStep * (s0 + g) + lane;
+            const float *pp = a.part + ((size_t)(p0 + m) * 2) * a.I + c;
+            const size_t qs = (size_t)a.P * 2 * a.I;
+            float gs = 0.0f, us = 0.0f;
+            for (int q = 0; q < a.KSg; q++) {
+                gs += pp[q * qs];
+                us += pp[q * qs + a.I];
+            }
+            act_group(gate_act(gs, a.use_gelu) * us, lane, reinterpret_cast<half_t *>(lds_act + m * rowb + g * 2 * kStep),
+                      lds_ds + g * 16 * MT + m);
+        }
+        __syncthreads();
+        if (rb >= a.H / kRowBlock) return;  // no barriers after this one
+        AOpL<MT> A;
+        A.q = lds_act;
+        A.ds = lds_ds;
+        A.s0 = s0;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            A.qoff[mt] = (16 * mt + n) * rowb + 32 * gq;
+            A.doff[mt] = 16 * mt + 4 * gq;
+        }
+        mm_steps<D, MT, kStepDs>(W, rb, s0, s0 + sw, lane, A, acc);
+    } else {
+        if (rb >= a.H / kRowBlock) return;  // no barriers in this kernel
+        AOp<MT> A;
+        A.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
+        A.ds = make_rsrc(a.x.ds, (size_t)(a.I / kStep) * a.x.ld * 4);
+        A.ld4 = a.x.ld * 4;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            A.qoff[mt] = (p0 + 16 * mt + n) * a.I * 2 + 32 * gq;
+            A.doff[mt] = (p0 + 16 * mt + 4 * gq) * 4;
+        }
+        mm_steps<D, MT, kStepDs>(W, rb, u0 * D::kSpu, (u0 + upw) * D::kSpu, lane, A, acc);
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
@@ -919,6 +990,16 @@ __global__ __launch_bounds__(256) void k_combine_rows(const float *__restrict__ 
 
 static int steps_per_unit(int type) { return tile_fmt(type).spu; }
 
+// Dynamic LDS of a kPart down workgroup: 16 rows of its steps in the activation
+// format, and a descale per (step, row).
+constexpr size_t kFuseLdsMax = 64 * 1024;
+static size_t down_part_lds(int down_type, int I, int ks_dn)
+{
+    const int spu = steps_per_unit(down_type);
+    const size_t sw = (size_t)(I / kStep / spu / ks_dn) * spu;
+    return 16 * sw * 2 * kStep + sw * 16 * 4;
+}
+
 bool mm_supported(int type) { return tile_fmt(type).qb != 0; }
 
 MmPlan plan_small(const MmPlan &p, int max_u)
@@ -1004,6 +1085,9 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u)
 #ifdef ANEDVD_KS_DN
     if (max_u > 64 && (I / kStep / steps_per_unit(down_type)) % ANEDVD_KS_DN == 0) p.ks_dn = ANEDVD_KS_DN;
 #endif
+    // A K-split gate/up is finished inside the down kernel (k_mm_down<kPart>) when
+    // a down workgroup's rows of its K range fit the LDS budget.
+    p.fuse = p.ks_gu > 1 && down_part_lds(down_type, I, p.ks_dn) <= kFuseLdsMax;
     return p;
 }
 
@@ -1021,8 +1105,14 @@ static int launch_gateup_t(const MmArgs &a, hipStream_t st)
 template <class D, int MT>
 static int launch_down_t(const MmArgs &a, hipStream_t st)
 {
+    static_assert(MT == 1, "the kPart LDS budget is sized for 16-token chunks");
     const size_t wgs = (size_t)a.nchunk * ((a.H / kRowBlock + kWaves - 1) / kWaves) * a.KS;
-    hipLaunchKernelGGL((k_mm_down<D, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    if (a.KSg > 1) {
+        const size_t lds = down_part_lds(a.w0.type, a.I, a.KS);
+        hipLaunchKernelGGL((k_mm_down<D, MT, true>), dim3((unsigned)wgs), dim3(256), lds, st, a);
+    } else {
+        hipLaunchKernelGGL((k_mm_down<D, MT, false>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    }
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }
@@ -1079,7 +1169,7 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
         set_error("expert gate/up: ggml type %d has no kernel", gate.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
     }
-    if (rc != ANEDVD_OK || plan.ks_gu == 1) return rc;
+    if (rc != ANEDVD_OK || plan.ks_gu == 1 || plan.fuse) return rc;  // fuse: the down kernel finishes them
     const size_t waves = (size_t)P * (I / kStep);
     hipLaunchKernelGGL(k_act_reduce, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
     ANEDVD_HIP(hipGetLastError());
@@ -1087,10 +1177,11 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
 }
 
 int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P,
-                       const MmPlan &plan, float *ypart, int kk, hipStream_t st)
+                       const MmPlan &plan, const float *part, int use_gelu, float *ypart, int kk, hipStream_t st)
 {
-    if (!d.rows || !d.slots || !ypart || kk <= 0) {
-        set_error("down: the dispatch's rows and slots and the output are needed (kk %d)", kk);
+    if (!d.rows || !d.slots || !ypart || kk <= 0 || (plan.fuse && !part)) {
+        set_error("down: the dispatch's rows and slots, the output and a fused gate/up's partials are needed (kk %d)",
+                  kk);
         return ANEDVD_E_INVALID_ARG;
     }
     if (plan.kind == kMmStaged)
@@ -1107,6 +1198,11 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
     a.KS = plan.ks_dn;
     a.P = P;
     a.nchunk = plan.nchunk;
+    if (plan.fuse) {
+        a.part = const_cast<float *>(part);
+        a.KSg = plan.ks_gu;
+        a.use_gelu = use_gelu;
+    }
     switch (down.type) {
     case ANEDVD_Q8_0:
     case ANEDVD_Q8_1: return launch_down_d<MQ8_0>(a, plan.mt, st);

@@ -103,6 +103,7 @@ struct MmPlan {
     int chunk;    // tokens per work-list chunk (16 mt), the dispatch's `chunk`
     int nchunk;   // bound on the work list's length: P / chunk + max_u
     int small;    // grouped GEMM: groups of at most this many tokens go to the decode kernels (0 = none)
+    int fuse;     // decode, ks_gu > 1: the down kernel finishes gate/up's K partials (no k_act_reduce)
 };
 bool mm_supported(int type);
 // P (token, slot) entries over at most max_u experts.
@@ -112,14 +113,17 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u);
 MmPlan plan_small(const MmPlan &p, int max_u);
 // gate/up + SiLU(gate)*up for every dispatched (token, expert) position, written
 // to `act` [P][I] in the activation format.  With plan.ks_gu > 1 the K partials
-// go to `part` [ks][P][2][I] and a second launch finishes them.
+// go to `part` [ks][P][2][I] and a second launch finishes them, or, with
+// plan.fuse, the down launch does (act is then not written).
 int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
                          const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st);
 // down for every position: ypart [ks_dn][T * kk][H] in (token, slot) order --
 // position p's output row is rows[p] * kk + slots[p] -- so the combine reads a
 // token's slots without going through `inv` (the combine adds the K partials).
+// With plan.fuse its input is gate/up's partials `part` (SiLU or geluTanh by
+// use_gelu), not `act`.
 int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P,
-                       const MmPlan &plan, float *ypart, int kk, hipStream_t st);
+                       const MmPlan &plan, const float *part, int use_gelu, float *ypart, int kk, hipStream_t st);
 // k_pf.hip -- the grouped GEMM for prefill-sized groups (chunks of 16 mt tokens)
 bool grouped_supported(int H, int I);
 bool grouped_wide(int type);  // the type has a 128-token-chunk grouped kernel

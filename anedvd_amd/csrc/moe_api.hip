@@ -323,7 +323,7 @@ static int launch_small_groups(const anedvd_moe_layer *L, const Fwd &f, int whic
     const MmPlan ps = plan_small(f.plan, f.max_u);
     const Dispatch dsm = f.d.small_view(ps.chunk);
     return which == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, dsm, f.P, ps, nullptr, f.act, L->gelu, st)
-                      : launch_expert_down(L->down, f.act, H, I, dsm, f.P, ps, f.ypart, kk, st);
+                      : launch_expert_down(L->down, f.act, H, I, dsm, f.P, ps, nullptr, L->gelu, f.ypart, kk, st);
 }
 
 // One forward call on stream st.  With `resid` the output is resid + the block's
@@ -366,7 +366,7 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
         ANEDVD_HIP(hipGetLastError());
         ANEDVD_TRY(launch_expert_gateup(L->sgate, L->sup, f.xq, H, Is, f.sd, T, f.splan, f.sh_part, f.sact,
                                         L->gelu, ss));
-        return launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_ypart, 1, ss);
+        return launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_part, L->gelu, f.sh_ypart, 1, ss);
     };
     if (fork) {
         if (small) {
@@ -379,7 +379,7 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
     ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act, L->gelu, st));
     if (small && !fork) ANEDVD_TRY(launch_small_groups(L, f, 0, st));
     mark(2);
-    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart, kk, st));
+    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.part, L->gelu, f.ypart, kk, st));
     if (small && !fork) ANEDVD_TRY(launch_small_groups(L, f, 1, st));
     mark(3);
     if (fork) ANEDVD_HIP(hipStreamWaitEvent(st, L->ctx->join, 0));
@@ -881,7 +881,7 @@ int anedvd_moe_expert_accum(anedvd_moe_layer *L, uint32_t expert, const float *h
     ANEDVD_HIP(hipMemcpyAsync(f.probs, &weight, 4, hipMemcpyHostToDevice, st));
     ANEDVD_TRY(launch_act_prep(f.h_in, 1, H, f.xq, st));
     ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, 1, f.plan, f.part, f.act, L->gelu, st));
-    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, 1, f.plan, f.ypart, 1, st));
+    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, 1, f.plan, f.part, L->gelu, f.ypart, 1, st));
     ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, 1, 1, H, f.plan.ks_dn, 1, nullptr, nullptr, 0, f.out, st));
     std::vector<float> y(H);
     ANEDVD_HIP(hipMemcpyAsync(y.data(), f.out, (size_t)H * 4, hipMemcpyDeviceToHost, st));
@@ -1239,8 +1239,8 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
                     return launch_router(L->router_t, L->router, d_h, (int)T, (int)L->E, H, f.logits, st);
                 const int rc = s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part,
                                                              f.act, L->gelu, st)
-                                      : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.ypart,
-                                                           (int)(L->k + L->n_sh), st);
+                                      : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.part, L->gelu,
+                                                           f.ypart, (int)(L->k + L->n_sh), st);
                 // the small groups' decode launch after it, on the same stream
                 return rc == ANEDVD_OK && f.plan.small ? launch_small_groups(L, f, s, st) : rc;
             };
