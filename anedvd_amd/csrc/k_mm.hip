@@ -796,20 +796,38 @@ __global__ __launch_bounds__(256) MM_ATTR void k_mm_down(MmArgs a)
             reinterpret_cast<u32x4 *>(lds_act + nt * rowb)[i] = (u32x4){0u, 0u, 0u, 0u};
         for (int i = threadIdx.x; i < sw * 16 * MT; i += 256)
             if (i % (16 * MT) >= nt) lds_ds[i] = 0.0f;
-        // one wavefront per (token, step) of the range: sum the KSg partials of
-        // gate and up in partial order, SiLU(g) * u, the group's power of two
-        for (int t = wv; t < nt * sw; t += kWaves) {  // uniform per wavefront
-            const int m = t / sw, g = t - m * sw;
-            const size_t c = (size_t)kStep * (s0 + g) + lane;
-            const float *pp = a.part + ((size_t)(p0 + m) * 2) * a.I + c;
-            const size_t qs = (size_t)a.P * 2 * a.I;
-            float gs = 0.0f, us = 0.0f;
+        // four (token, step) pieces per wavefront at once, one per 16-lane row (lane
+        // l: columns 4 l .. 4 l + 3): the KSg partials of gate and up summed in
+        // partial order, SiLU(g) * u, the piece's power of two from the row's
+        // largest magnitude -- act_group's values, max and rounding
+        const size_t qs = (size_t)a.P * 2 * a.I;
+        const int l = lane & 15;
+        for (int t0 = 4 * wv; t0 < nt * sw; t0 += 4 * kWaves) {  // uniform per wavefront
+            const int t = t0 + (lane >> 4);
+            const bool live = t < nt * sw;
+            const int tt = live ? t : t0;
+            const int m = tt / sw, g = tt - m * sw;
+            const float *pp = a.part + ((size_t)(p0 + m) * 2) * a.I + (size_t)kStep * (s0 + g) + 4 * l;
+            float gs[4] = {0.0f, 0.0f, 0.0f, 0.0f}, us[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             for (int q = 0; q < a.KSg; q++) {
-                gs += pp[q * qs];
-                us += pp[q * qs + a.I];
+                const float4 x = *reinterpret_cast<const float4 *>(pp + q * qs);
+                const float4 y = *reinterpret_cast<const float4 *>(pp + q * qs + a.I);
+                gs[0] += x.x; gs[1] += x.y; gs[2] += x.z; gs[3] += x.w;
+                us[0] += y.x; us[1] += y.y; us[2] += y.z; us[3] += y.w;
             }
-            act_group(gate_act(gs, a.use_gelu) * us, lane, reinterpret_cast<half_t *>(lds_act + m * rowb + g * 2 * kStep),
-                      lds_ds + g * 16 * MT + m);
+            float v[4], mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = gate_act(gs[i], a.use_gelu) * us[i];
+                mx = fmaxf(mx, fabsf(v[i]));
+            }
+            const float sc = pow2_scale(row_max_f32(mx));
+            if (live) {
+                half_t *dq = reinterpret_cast<half_t *>(lds_act + m * rowb + g * 2 * kStep);
+#pragma unroll
+                for (int i = 0; i < 4; i++) dq[mma_pos(4 * l + i)] = (half_t)(v[i] * sc);
+                if (l == 0) lds_ds[g * 16 * MT + m] = 1.0f / sc;
+            }
         }
         __syncthreads();
         if (rb >= a.H / kRowBlock) return;  // no barriers after this one
@@ -1031,7 +1049,7 @@ static int choose_ks(int units, int spu, long wg_per_ks, int waves_per_k, int mi
     return best;
 }
 
-MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u)
+MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u, int T)
 {
     MmPlan p{};
     // The grouped GEMM (64-token chunks of a group, activations staged in LDS and
@@ -1086,8 +1104,12 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u)
     if (max_u > 64 && (I / kStep / steps_per_unit(down_type)) % ANEDVD_KS_DN == 0) p.ks_dn = ANEDVD_KS_DN;
 #endif
     // A K-split gate/up is finished inside the down kernel (k_mm_down<kPart>) when
-    // a down workgroup's rows of its K range fit the LDS budget.
-    p.fuse = p.ks_gu > 1 && down_part_lds(down_type, I, p.ks_dn) <= kFuseLdsMax;
+    // a down workgroup's rows of its K range fit the LDS budget and its prologue
+    // has at most 64 (token, step) pieces, four memory round trips (16 pieces each),
+    // even if every token of the call sends a slot to the same expert (a chunk
+    // holds at most min(T, 16) tokens).  Otherwise k_act_reduce finishes them.
+    const int sw = I / kStep / steps_per_unit(down_type) / p.ks_dn * steps_per_unit(down_type);
+    p.fuse = p.ks_gu > 1 && down_part_lds(down_type, I, p.ks_dn) <= kFuseLdsMax && std::min(T, 16) * sw <= 64;
     return p;
 }
 

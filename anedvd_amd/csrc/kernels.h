@@ -106,8 +106,8 @@ struct MmPlan {
     int fuse;     // decode, ks_gu > 1: the down kernel finishes gate/up's K partials (no k_act_reduce)
 };
 bool mm_supported(int type);
-// P (token, slot) entries over at most max_u experts.
-MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u);
+// P (token, slot) entries of T tokens over at most max_u experts.
+MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u, int T);
 // The decode-kernel plan for the small groups of a grouped plan (p.small > 0):
 // one 16-token chunk per group, K not split, the same down partial count.
 MmPlan plan_small(const MmPlan &p, int max_u);

@@ -240,7 +240,7 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     Fwd x{};
     x.P = P;
     x.max_u = std::min(E, P);
-    x.plan = plan_mm(L->gate.type, L->down.type, H, I, P, x.max_u);
+    x.plan = plan_mm(L->gate.type, L->down.type, H, I, P, x.max_u, T);
     Carve c{base};
     x.logits = c.take<float>((size_t)T * L->E);
     x.probs = c.take<float>(P);
@@ -264,7 +264,7 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
     x.ypart = c.take<float>((size_t)x.plan.ks_dn * P * H);
     if (L->Is && !L->n_sh) {
         const int Is = (int)L->Is;
-        x.splan = plan_mm(L->sgate.type, L->sdown.type, H, Is, T, 1);
+        x.splan = plan_mm(L->sgate.type, L->sdown.type, H, Is, T, 1, T);
         x.sd.offsets = c.take<int32_t>(2);
         x.sd.rows = c.take<int32_t>(T);
         x.sd.slots = c.take<int32_t>(T);

@@ -235,6 +235,20 @@ def test_forward_qwen3_30b_a3b_q8_0(ctx, T):
     assert st["touched_experts"] == len(np.unique(oi))
 
 
+@pytest.mark.parametrize("T", [2, 8])
+def test_forward_k_split_finished_in_down_crowded(ctx, T):
+    """Decode batches whose gate/up splits K and whose down kernel finishes the
+    partials in its prologue, with every token routed to the same eight experts:
+    chunks of T tokens, the most (token, step) pieces that prologue takes."""
+    spec = W.QWEN3_30B_A3B_Q8_0
+    rng = np.random.default_rng(43)
+    lg = rng.uniform(-6.0, -5.0, size=(T, spec.n_experts)).astype(np.float32)
+    lg[:, 17:25] = rng.uniform(1.0, 2.0, size=(T, 8)).astype(np.float32)
+    _, _, err, st = _forward_case(ctx, spec, T, seed=43, logits=lg)
+    assert err <= REL_L2_TOL
+    assert st["touched_experts"] == 8 and st["max_group"] == T
+
+
 @pytest.mark.parametrize("T", [1, 64])
 def test_forward_qwen3_uniform_logits(ctx, T):
     """The decode workload routes i.i.d. U(0,1) logits instead of the router GEMV."""
