@@ -950,6 +950,7 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart
 // Large calls: one thread per (token, 4 columns), slots in order, eight slots'
 // loads issued together (indices clamped rather than branched on).  Grid: T * H/4
 // threads.
+template <int NS>
 __global__ __launch_bounds__(256) void k_combine_rows(const float *__restrict__ ypart, const int32_t *__restrict__ inv,
                                                       const float *__restrict__ probs, int T, int k, int H, int KS,
                                                       int P, const float *__restrict__ shared,
@@ -961,13 +962,13 @@ __global__ __launch_bounds__(256) void k_combine_rows(const float *__restrict__ 
     if (id >= (size_t)T * H4) return;
     const int t = (int)(id / H4), h = (int)(id % H4) * 4;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < k; s0 += 8) {
-        int pos[8];
-        float p[8];
-        bool ok[8];
-        float4 y[8];
+    for (int s0 = 0; s0 < k; s0 += NS) {  // NS slots per pass, their loads issued together
+        int pos[NS];
+        float p[NS];
+        bool ok[NS];
+        float4 y[NS];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < NS; i++) {
             const int s = min(s0 + i, k - 1);
             pos[i] = (int)((size_t)t * k + s);
             const int iv = inv[pos[i]];
@@ -977,13 +978,13 @@ __global__ __launch_bounds__(256) void k_combine_rows(const float *__restrict__ 
         }
         for (int q = 0; q < KS; q++) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < NS; i++) {
                 const float4 z = *(const float4 *)(ypart + ((size_t)q * P + pos[i]) * H + h);
                 y[i].x += z.x; y[i].y += z.y; y[i].z += z.z; y[i].w += z.w;
             }
         }
 #pragma unroll
-        for (int i = 0; i < 8; i++)
+        for (int i = 0; i < NS; i++)
             if (ok[i]) {
                 acc.x += p[i] * y[i].x; acc.y += p[i] * y[i].y; acc.z += p[i] * y[i].z; acc.w += p[i] * y[i].w;
             }
@@ -1255,8 +1256,16 @@ int launch_combine(const float *ypart, const int32_t *inv, const float *probs, i
     }
     const size_t threads = (size_t)T * (H / 4);
     if (threads >= 65536) {  // enough (token, column) threads to fill the GPU: slots in order per thread
-        hipLaunchKernelGGL(k_combine_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, ypart, inv, probs,
-                           T, k, H, KS, P, shared, shared_scale, sKS, resid, out);
+        const dim3 grid((unsigned)((threads + 255) / 256));
+        if (k <= 2)  // as many slot loads per pass as there are slots (Mixtral: 2, not 8 clamped copies)
+            hipLaunchKernelGGL(k_combine_rows<2>, grid, dim3(256), 0, st, ypart, inv, probs, T, k, H, KS, P, shared,
+                               shared_scale, sKS, resid, out);
+        else if (k <= 4)
+            hipLaunchKernelGGL(k_combine_rows<4>, grid, dim3(256), 0, st, ypart, inv, probs, T, k, H, KS, P, shared,
+                               shared_scale, sKS, resid, out);
+        else
+            hipLaunchKernelGGL(k_combine_rows<8>, grid, dim3(256), 0, st, ypart, inv, probs, T, k, H, KS, P, shared,
+                               shared_scale, sKS, resid, out);
     } else {  // decode: spread the slots over lanes so each thread waits on one slot's loads
         const dim3 grid((unsigned)((H / 4 + kCombCols - 1) / kCombCols), (unsigned)std::min(T, 65535));
         hipLaunchKernelGGL(k_combine, grid, dim3(kCombLanes * kCombCols), 0, st, ypart, inv, probs, T, k, H, KS, P,
