@@ -3,8 +3,10 @@
 //
 // Every block routine follows the reference dequantiser named beside it
 // (gguf.zig:743-1071) in the same f32 operations.  Each product of a quant and
-// its scale is exact in f32 (see DESIGN.md's dequant note), so contraction could
-// not change a value; it is switched off anyway so the code says what it does.
+// its scale is exact in f32 (an f16 scale carries 11 significant bits, a
+// sub-block scale at most 7 and a quant at most 7, which fit f32's 24), so
+// contraction could not change a value; it is switched off anyway so the code
+// says what it does.
 #pragma clang fp contract(off)
 
 #include "common.h"

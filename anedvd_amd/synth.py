@@ -2,7 +2,7 @@
 
 Every random value is a pure function of (seed, stream, index): a SplitMix64
 finaliser over a counter, so the same bytes come out whether a whole tensor or
-one expert of it is generated, and whether on the build host or the GPU box.
+one expert of it is generated, and on whichever host generates it.
 
 Quantised tensors are written in GGUF byte layout (the block structs of
 gguf.zig:763-1059), stacked `[E][rows][cols]` with the expert axis slowest, as

@@ -1,7 +1,7 @@
 /*
  * moe_oracle.c -- CPU restatement of ANEDVD's quantised MoE FFN path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP library, and the CPU
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP library, and the CPU
  * baseline that bench.py times beside it.  Nothing in the product links it.
  *
  * Each function follows one reference function (file:line in the comment)

@@ -1,7 +1,7 @@
 /*
  * moe_oracle.h -- CPU restatement of ANEDVD's quantised MoE FFN path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker the GPU path is
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle the GPU path is
  * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
  * CPU-baseline leg may load it; the product library never links it and
  * never falls back to it.
