@@ -1093,6 +1093,7 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u, int
     }
     p.chunk = 16 * p.mt;
     p.nchunk = P / p.chunk + max_u;
+    p.xper = p.kind == kMmStaged && p.contig ? (p.nchunk + 7) / 8 : 0;  // the grouped grid's work items per XCD
     if (p.kind != kMmDecode) {
         p.ks_gu = 1;
         return p;

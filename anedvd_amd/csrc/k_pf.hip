@@ -266,15 +266,24 @@ struct PfArgs {
 // two or more chunks) each XCD takes a contiguous range of work items, so the
 // consecutive chunks of one expert also share its weight slices in one L2
 // (Mixtral 2048 tokens: fabric reads of the gate/up launch 2.58 -> 2.24 GB,
-// 1197 -> 1121 us).  Otherwise work items go round robin, which spreads unequal
-// groups evenly over the XCDs (contiguous ranges measured 23 % slower on the
-// Zipf-routed Qwen3 512-token prefill).
-__device__ inline void pf_item(int b, int nw8, int contig, int &w, int &rest)
+// 1197 -> 1121 us).  With one work item per chunk, the ranges are the dispatch's
+// (xr): whole experts per XCD where each fits a range, so no expert's slices are
+// read by two L2s (gate/up fabric reads 2.13 -> 1.63 GB, 984 -> 946 us).
+// Otherwise work items go round robin, which spreads unequal groups evenly over
+// the XCDs (contiguous ranges measured 23 % slower on the Zipf-routed Qwen3
+// 512-token prefill).
+__device__ inline void pf_item(const Dispatch &d, int sub, int b, int nw8, int contig, int &w, int &rest)
 {
     if (contig) {
         const int per = nw8 >> 3, x = b & 7, j = b >> 3;
-        w = x * per + j % per;
         rest = j / per;
+        if (sub == 1 && d.xper == per) {  // the dispatch's XCD ranges: whole experts where they fit
+            const int lo = d.xr[x], hi = d.xr[x + 1];
+            w = lo + j % per;
+            if (w >= hi) w = 1 << 30;  // past this range: nothing
+        } else {
+            w = x * per + j % per;
+        }
     } else {
         w = b % nw8;
         rest = b / nw8;
@@ -324,7 +333,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
     __shared__ float gmax[4][16 * MT];  // per wavefront: its 32 columns' largest |act| per token
     int e, p0, nt, w, rbg;
     const int nw = a.nchunk * a.sub;
-    pf_item((int)blockIdx.x, pf_nw8(nw), a.contig, w, rbg);
+    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, w, rbg);
     if (w >= nw || !pf_chunk<MT>(a.d, w, a.sub, e, p0, nt)) return;  // uniform over the workgroup
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int t0 = 2 * (wv & 1), rb = 2 * rbg + (wv >> 1);
@@ -421,7 +430,7 @@ __global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
     __shared__ float ref4[256 / (16 * MT)][16 * MT];
     int e, p0, nt, w, rest;
     const int nw = a.nchunk * a.sub;
-    pf_item((int)blockIdx.x, pf_nw8(nw), a.contig, w, rest);
+    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, w, rest);
     if (w >= nw || !pf_chunk<MT>(a.d, w, a.sub, e, p0, nt)) return;
     const int rbg = rest / a.ks, kq = rest - rbg * a.ks;
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;

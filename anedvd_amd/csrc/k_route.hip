@@ -373,13 +373,25 @@ __device__ inline int wave_incl_scan(int v, int)
     return v;
 }
 
+// Where the dispatch puts the work list beyond `chunks`: the small groups' list
+// and the XCD ranges (Dispatch's chunks_s / small and xr / xper).
+struct ListOpts {
+    uint64_t *chunks_s;
+    int small;
+    int32_t *xr;
+    int xper;
+};
+__device__ inline ListOpts list_opts(const Dispatch &d) { return ListOpts{d.chunks_s, d.small, d.xr, d.xper}; }
+
 // Wavefront 0 of the dispatch: offsets[E+1], the active experts, the chunk list
 // and meta from the per-expert counts in s.cnt (4 experts per lane, E <= 256);
 // s.off gets the offsets.
 __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets, int32_t *__restrict__ active,
                                  int32_t *__restrict__ meta, uint64_t *__restrict__ chunks, int chunk, int n_routed,
-                                 uint64_t *__restrict__ chunks_s, int small, DispLds &s, bool write = true)
+                                 ListOpts lo, DispLds &s, bool write = true)
 {
+    uint64_t *__restrict__ chunks_s = lo.chunks_s;
+    const int small = lo.small;
     int c[4], tot = 0, nz = 0, mx = 0;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -431,6 +443,35 @@ __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__res
         meta[1] = mx;
         meta[2] = s.bad;
     }
+    // The work list cut into 8 XCD ranges of at most xper chunks, whole experts in
+    // list order (next fit), so an expert's chunks share their weight slices in one
+    // L2; if an expert does not fit, the even split x * xper.
+    if (lo.xper > 0 && chunks && lane == 0) {
+        int32_t start[9];
+        int x = 0, fill = 0, pos = 0;
+        bool ok = true;
+        start[0] = 0;
+        for (int e = 0; e < E && ok; e++) {
+            const int n = s.cnt[e];
+            const int nc = (n == 0 || (small && n <= small)) ? 0 : (n + chunk - 1) / chunk;
+            if (nc == 0) continue;
+            if (nc > lo.xper) {
+                ok = false;
+            } else {
+                if (fill + nc > lo.xper) {
+                    if (++x == 8) {
+                        ok = false;
+                        break;
+                    }
+                    start[x] = pos;
+                    fill = 0;
+                }
+                fill += nc;
+                pos += nc;
+            }
+        }
+        for (int y = 0; y <= 8; y++) lo.xr[y] = ok ? (y <= x ? start[y] : pos) : y * lo.xper;
+    }
 }
 
 // Calls of more entries than threads (or too many for the one-pass bitmap), up to
@@ -450,7 +491,7 @@ __device__ __forceinline__ void dispatch_segments(const uint32_t *__restrict__ i
                                   int32_t *__restrict__ offsets, int32_t *__restrict__ rows,
                                   int32_t *__restrict__ slots, int32_t *__restrict__ inv, int32_t *__restrict__ active,
                                   int32_t *__restrict__ meta, uint64_t *__restrict__ chunks, int chunk, int n_routed,
-                                  uint64_t *__restrict__ chunks_s, int small, DispLds &s)
+                                  ListOpts lo, DispLds &s)
 {
     constexpr int NW = NTH / 64;
     static_assert(NW * kMaxExperts <= kDispWords, "per-wavefront counts live in the bitmap's words");
@@ -505,7 +546,7 @@ __device__ __forceinline__ void dispatch_segments(const uint32_t *__restrict__ i
         s.cnt[e] = run;
     }
     __syncthreads();
-    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, chunks_s, small, s);
+    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, lo, s);
     __syncthreads();
     // Each entry's position (inv, written in entry order); the entries go to LDS by
     // position, so rows and slots are written in position order (coalesced) rather
@@ -547,7 +588,7 @@ template <int NTH>
 __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx, int T, int k, int E, int32_t *__restrict__ offsets,
                                int32_t *__restrict__ rows, int32_t *__restrict__ slots, int32_t *__restrict__ inv,
                                int32_t *__restrict__ active, int32_t *__restrict__ meta, uint64_t *__restrict__ chunks,
-                               int chunk, int n_routed, uint64_t *__restrict__ chunks_s, int small, DispLds &s)
+                               int chunk, int n_routed, ListOpts lo, DispLds &s)
 {
     static_assert(NTH >= 128, "wavefront 0 computes the offsets while the others prefix the bitmap");
     const int P = T * k, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -574,7 +615,7 @@ __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx,
         if (bad) atomicAdd(&s.bad, bad);
         __syncthreads();
         if (wv == 0) {
-            dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, chunks_s, small, s);
+            dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, lo, s);
         } else {
             for (int e = tid - 64; e < E; e += NTH - 64) {
                 int run = 0;
@@ -600,8 +641,7 @@ __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx,
         return;
     }
     if (P <= (NTH / 64) * 64 * kSegBatches) {
-        dispatch_segments<NTH>(idx, P, k, E, offsets, rows, slots, inv, active, meta, chunks, chunk, n_routed, chunks_s,
-                               small, s);
+        dispatch_segments<NTH>(idx, P, k, E, offsets, rows, slots, inv, active, meta, chunks, chunk, n_routed, lo, s);
         return;
     }
     for (int e = tid; e < E; e += NTH) {
@@ -618,7 +658,7 @@ __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx,
     }
     if (bad) atomicAdd(&s.bad, bad);
     __syncthreads();
-    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, chunks_s, small, s);
+    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, lo, s);
     // bitmap words per expert per chunk of entries
     const int W = max(1, kDispWords / E);
     const int C = 32 * W, NW = W * E;
@@ -803,7 +843,7 @@ __global__ __launch_bounds__(kDispThreads) void k_route_dispatch(RouteArgs a, Di
         ids[(i / a.n_sh) * a.kk + a.k + i % a.n_sh] = (uint32_t)(a.E + i % a.n_sh);
     __syncthreads();
     dispatch_block<kDispThreads>(ids, a.T, a.kk, a.E + a.n_sh, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta,
-                                 d.chunks, d.chunk, d.n_routed, d.chunks_s, d.small, s);
+                                 d.chunks, d.chunk, d.n_routed, list_opts(d), s);
 }
 
 __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__restrict__ idx, int T, int k, int E,
@@ -811,7 +851,7 @@ __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__res
 {
     __shared__ DispLds s;
     dispatch_block<kDispThreads>(idx, T, k, E, d.offsets, d.rows, d.slots, d.inv, d.active, d.meta, d.chunks, d.chunk,
-                                 d.n_routed, d.chunks_s, d.small, s);
+                                 d.n_routed, list_opts(d), s);
 }
 
 // Dispatch of more entries than one workgroup ranks at once, by kDispBlock-entry
@@ -901,7 +941,7 @@ __global__ __launch_bounds__(kDispThreads) void k_dispatch_multi(const uint32_t 
             run += v;
         }
     }
-    if (wv == NW - 1) dispatch_offsets(E, lane, d.offsets, d.active, d.meta, d.chunks, d.chunk, d.n_routed, d.chunks_s, d.small,
+    if (wv == NW - 1) dispatch_offsets(E, lane, d.offsets, d.active, d.meta, d.chunks, d.chunk, d.n_routed, list_opts(d),
                                       s, blockIdx.x == 0);
     __syncthreads();
     // 4. positions

@@ -21,6 +21,7 @@ struct ActQ {
 // slice of expert e's group, experts ascending -- the expert kernels' work list.
 // With small > 0, groups of 1..small tokens are listed in chunks_s instead (one
 // entry per group, experts ascending; meta[7] = their count, meta holding 8 ints).
+// With xper > 0, xr[9] gives each XCD's range of the work list (see below).
 struct Dispatch {
     int32_t *offsets, *rows, *slots, *inv, *active, *meta;
     uint64_t *chunks;  // the work list: chunk_entry(e, first position, tokens) per chunk
@@ -28,6 +29,10 @@ struct Dispatch {
     int n_routed;  // meta[1] counts experts below this one only (0 = all): merged shared pieces are not groups
     uint64_t *chunks_s;  // the small groups' list (small > 0)
     int small;
+    // With xper > 0: xr[0..8], the work list cut into 8 XCD ranges of at most xper
+    // chunks, whole experts per range where they fit (else xr[x] = x * xper).
+    int32_t *xr;
+    int xper;
 
     // The small groups' list as a work list of its own (count in meta[3] of the view).
     Dispatch small_view(int chunk_s) const
@@ -103,6 +108,7 @@ struct MmPlan {
     int chunk;    // tokens per work-list chunk (16 mt), the dispatch's `chunk`
     int nchunk;   // bound on the work list's length: P / chunk + max_u
     int small;    // grouped GEMM: groups of at most this many tokens go to the decode kernels (0 = none)
+    int xper;     // grouped GEMM with contig: chunks per XCD range of the work list (0 = none)
     int fuse;     // decode, ks_gu > 1: the down kernel finishes gate/up's K partials (no k_act_reduce)
 };
 bool mm_supported(int type);

@@ -258,6 +258,10 @@ size_t fwd_layout(const anedvd_moe_layer *L, int T, int k, Fwd *f, uint8_t *base
         x.d.chunks_s = c.take<uint64_t>((size_t)x.max_u);
         x.d.small = x.plan.small;
     }
+    if (x.plan.xper) {
+        x.d.xr = c.take<int32_t>(9);
+        x.d.xper = x.plan.xper;
+    }
     x.xq = ActQ{c.take<half_t>((size_t)T * H), c.take<float>((size_t)T * (H / kStep)), T};
     x.act = ActQ{c.take<half_t>((size_t)P * I), c.take<float>((size_t)P * (I / kStep)), P};
     x.part = x.plan.ks_gu > 1 ? c.take<float>((size_t)x.plan.ks_gu * P * 2 * I) : nullptr;

@@ -418,6 +418,26 @@ def test_forward_grouped_split_k_down(ctx, types):
     assert st["path"] == 1 and st["down_ks"] == 2
 
 
+@pytest.mark.parametrize("sizes", [[400] * 8, [1600, 320, 320, 320, 320, 160, 80, 80]], ids=["whole", "one-too-big"])
+def test_forward_grouped_xcd_ranges(ctx, sizes):
+    """Large groups over few experts (the contiguous workgroup order): the dispatch
+    cuts the work list into 8 XCD ranges of whole experts where each fits (eight
+    groups of 4 chunks), and into even ranges when one group has more chunks than
+    a range holds (13 chunks against 5)."""
+    lg = _logits_for_groups(sizes, seed=47)
+    spec = dataclasses.replace(W.MIXTRAL_8X7B_Q4_0, name="xcd-ranges", hidden=256, inter=4096, scale_sigma=0.01)
+    L = synth.make_layer(spec, seed=47)
+    h = synth.activations(spec, lg.shape[0], seed=47)
+    layer = moe.MoeLayer(ctx, spec, L)
+    got, st = layer.forward(h, lg, stats=True)
+    layer.free()
+    want = O.OracleLayer(spec, L).forward(h, lg, fast=True)
+    err = moe.rel_l2(got, want)
+    print(f"\nxcd ranges {sizes[:2]}: rel-L2 {err:.3e}, chunk {st['chunk']}")
+    assert err <= REL_L2_TOL
+    assert st["path"] == 1 and st["chunk"] == 128 and st["max_group"] == max(sizes)
+
+
 # Sixteen groups averaging 42.5 tokens (the grouped GEMM), six of them of 1 to 16
 # tokens (the decode kernels, beside it).
 SMALL_SIZES = [1, 3, 8, 16, 17, 30, 64, 65, 90, 120, 130, 10, 5, 50, 40, 31]
