@@ -416,6 +416,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
 
 // ---------------------------------------------------------------- down
 
+// Three wavefronts per SIMD for the down decoder built for them (FQ6_KDown),
+// else the compiler's choice.
+template <class F, int MT>
+constexpr int pf_dn_waves()
+{
+    return std::is_same<F, FQ6_KDown>::value ? 3 : 1;
+}
+
 // Grid nw8 * H/256 * ks workgroups of 256 threads (pf_item's order).  Wave w: row
 // block 4 x + w, K share kq.  Before the K loop the workgroup finds each position's largest descale
 // over the I/64 groups (the row reference); staging scales every group to it, and
@@ -423,7 +431,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
 // end are computed on the next group's (or, past the last position, the last
 // position's) activations and not stored.
 template <class F, int MT>
-__global__ __launch_bounds__(256) void k_pf_down(PfArgs a)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_dn_waves<F, MT>()))) void k_pf_down(PfArgs a)
 {
     __shared__ float ref[16 * MT];
     __shared__ int orow[16 * MT];  // output rows of the chunk's positions, (token, slot) order
@@ -578,7 +586,8 @@ static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStr
     case ANEDVD_Q3_K: return launch_pf_mt<FQ3_K, false>(a, mt, gateup, st);
     case ANEDVD_Q4_K: return launch_pf_mt<FQ4_K, false>(a, mt, gateup, st);
     case ANEDVD_Q5_K: return launch_pf_mt<FQ5_K, false>(a, mt, gateup, st);
-    case ANEDVD_Q6_K: return launch_pf_mt<FQ6_K, false>(a, mt, gateup, st);
+    case ANEDVD_Q6_K:
+        return gateup ? launch_pf_mt<FQ6_K, false>(a, mt, gateup, st) : launch_pf_mt<FQ6_KDown, false>(a, mt, gateup, st);
     default:
         set_error("grouped GEMM: ggml type %d has no kernel", type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
