@@ -418,6 +418,15 @@ def test_forward_grouped_split_k_down(ctx, types):
     assert st["path"] == 1 and st["down_ks"] == 2
 
 
+@pytest.mark.parametrize("k", [1, 3])
+def test_forward_large_call_combine_partial_pass(ctx, k):
+    """The large-call combine loads 2, 4 or 8 slots per pass: top-1 and top-3 leave
+    part of a pass empty (300 tokens x 1024 columns, one thread per column group)."""
+    spec = dataclasses.replace(W.QWEN3_30B_A3B_Q8_0, name=f"combine-k{k}", hidden=1024, inter=512, n_experts=16, k=k)
+    _, _, err, st = _forward_case(ctx, spec, 300, seed=53)
+    assert err <= REL_L2_TOL
+
+
 @pytest.mark.parametrize("sizes", [[400] * 8, [1600, 320, 320, 320, 320, 160, 80, 80]], ids=["whole", "one-too-big"])
 def test_forward_grouped_xcd_ranges(ctx, sizes):
     """Large groups over few experts (the contiguous workgroup order): the dispatch
