@@ -277,7 +277,7 @@ def run_config(name: str, ctx, warmup: int, steps: int, with_parity: bool) -> di
     flops = spec.call_flops(T, with_router=False)
     lbytes = spec.call_bytes(st["touched_experts"], T, with_router=False)
     r.update({"touched_experts": st["touched_experts"], "max_group": st["max_group"],
-              "path": "grouped GEMM" if st["path"] else "decode GEMV",
+              "path": "grouped GEMM" if st["path"] else "decode MFMA kernels",
               "ms_per_call": round(ms / n_calls, 4), "tokens_per_s": round(T / t, 1),
               "TFLOPs": round(flops / t / 1e12, 2), "mfma_frac": round(flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
               "layer_GBps": round(lbytes / t / 1e9, 1), "hbm_frac": round(lbytes / t / 1e9 / HBM_PEAK_GBS, 4),
