@@ -2,8 +2,9 @@
 what anedvd_moe_layer_forward_device computes, bit for bit, through the C ABI:
 two calls in a row on each layer, the second smaller than the first (the static
 scratch keeps the first call's contents), on the decode kernels, the grouped
-GEMM and a separately run shared expert; and a call whose scratch exceeds the
-array is refused."""
+GEMM (with Zipf routing also its groups of a few tokens, run on the context's
+second stream) and a separately run shared expert; and a call whose scratch
+exceeds the array is refused."""
 import dataclasses
 import re
 
@@ -23,9 +24,9 @@ def ctx():
     c.close()
 
 
-def run(ctx, layer, spec, T, seed, noalloc):
+def run(ctx, layer, spec, T, seed, noalloc, routing="uniform"):
     h = synth.activations(spec, T, seed=seed)
-    lg = synth.uniform_logits(spec, T, seed=seed)
+    lg = (synth.zipf_logits if routing == "zipf" else synth.uniform_logits)(spec, T, seed=seed)
     d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lg), ctx.alloc(T * spec.hidden * 4)
     (layer.forward_device_noalloc if noalloc else layer.forward_device)(d_h, T, d_lg, d_out)
     out = ctx.from_device(d_out, (T, spec.hidden), np.float32)
@@ -35,20 +36,26 @@ def run(ctx, layer, spec, T, seed, noalloc):
 
 
 SPECS = [
-    (W.QWEN3_30B_A3B_Q8_0, (64, 8)),
-    (W.QWEN3_30B_A3B_Q4_K_M, (512, 64)),
+    (W.QWEN3_30B_A3B_Q8_0, (64, 8), "uniform"),
+    (W.QWEN3_30B_A3B_Q4_K_M, (512, 64), "uniform"),
+    (W.QWEN3_30B_A3B_Q4_K_M, (512, 300), "zipf"),
     (dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="separate-shared", hidden=512, inter=512, n_experts=8, k=2,
-                         shared_inter=1024, shared_type=W.Q4_0, shared_gated=True), (300, 16)),
+                         shared_inter=1024, shared_type=W.Q4_0, shared_gated=True), (300, 16), "uniform"),
 ]
 
 
-@pytest.mark.parametrize("spec,sizes", SPECS, ids=lambda x: x.name.split()[0] if hasattr(x, "name") else str(x))
-def test_noalloc_forward_matches_forward_device(ctx, spec, sizes):
+@pytest.mark.parametrize("spec,sizes,routing", SPECS,
+                         ids=lambda x: x.name.split()[0] if hasattr(x, "name") else str(x))
+def test_noalloc_forward_matches_forward_device(ctx, spec, sizes, routing):
     layer = moe.MoeLayer(ctx, spec, synth.make_layer(spec, seed=3))
+    if routing == "zipf":  # the case exists: skewed routing leaves groups of at most 16 tokens
+        h = synth.activations(spec, sizes[0], seed=30)
+        _, st = layer.forward(h, synth.zipf_logits(spec, sizes[0], seed=30), stats=True)
+        assert st["path"] == 1 and st["small_groups"] > 0, st
     for i, T in enumerate(sizes):
-        want = run(ctx, layer, spec, T, 30 + i, noalloc=False)
-        got = run(ctx, layer, spec, T, 30 + i, noalloc=True)
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (spec.name, T)
+        want = run(ctx, layer, spec, T, 30 + i, noalloc=False, routing=routing)
+        got = run(ctx, layer, spec, T, 30 + i, noalloc=True, routing=routing)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (spec.name, T, routing)
     layer.free()
 
 
