@@ -48,11 +48,12 @@ constexpr int kWaves = 4;
 #ifndef ANEDVD_PF_WIDE_MIN
 #define ANEDVD_PF_WIDE_MIN 64
 #endif
-// Groups of at most this many tokens (one decode tile) leave the grouped GEMM for
-// the decode kernels, which stream their weights once per 16-token tile without
-// staging, on a second stream beside the grouped launches; only while the mean
-// group is below ANEDVD_SMALL_MEAN (skewed routing of many experts: most groups
-// then hold a few tokens).  0 turns the split off.
+// Groups of at most this many tokens (one 16-token tile) leave the grouped GEMM's
+// work list for its small-group workgroups (the same launch, after the grouped
+// ones), which read their activations straight from memory instead of staging
+// them in LDS; only while the mean group is below ANEDVD_SMALL_MEAN (skewed
+// routing of many experts: most groups then hold a few tokens).  0 turns the
+// split off.
 #ifndef ANEDVD_SMALL_GROUP
 #define ANEDVD_SMALL_GROUP 16
 #endif
@@ -1021,18 +1022,6 @@ static size_t down_part_lds(int down_type, int I, int ks_dn)
 
 bool mm_supported(int type) { return tile_fmt(type).qb != 0; }
 
-MmPlan plan_small(const MmPlan &p, int max_u)
-{
-    MmPlan q{};
-    q.kind = kMmDecode;
-    q.mt = 1;
-    q.chunk = 16;
-    q.nchunk = max_u;  // one entry per small group
-    q.ks_gu = 1;
-    q.ks_dn = p.ks_dn;
-    return q;
-}
-
 // Splits a K axis of `units` scale units over ks workgroups, ks dividing units
 // and at most kMaxKS (the partials the combine reads): the smallest ks that gives
 // `wg_per_ks * ks` >= ANEDVD_WG_TARGET workgroups while every wavefront keeps >=
@@ -1086,7 +1075,8 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u, int
         p.mt = std::max(p.mt_gu, p.mt_dn);
         p.contig = P >= 2 * 16 * p.mt * (long)max_u;  // experts average two chunks or more
         // (the decode down writes one K partial: the combine reads the same count for every row)
-        p.small = mean < ANEDVD_SMALL_MEAN && p.ks_dn == 1 ? std::min(ANEDVD_SMALL_GROUP, 16) : 0;
+        p.small = mean < ANEDVD_SMALL_MEAN && p.ks_dn == 1 && p.mt == 4 ? std::min(ANEDVD_SMALL_GROUP, 16) : 0;
+        p.nsmall = p.small ? max_u : 0;
     } else {
         p.kind = kMmDecode;
         p.mt = 1;
@@ -1157,7 +1147,8 @@ int launch_expert_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H,
                          const MmPlan &plan, float *part, const ActQ &act, int use_gelu, hipStream_t st)
 {
     if (plan.kind == kMmStaged)
-        return launch_grouped_gateup(gate, up, x, H, I, d, P, plan.mt_gu, plan.nchunk, plan.contig, act, use_gelu, st);
+        return launch_grouped_gateup(gate, up, x, H, I, d, P, plan.mt_gu, plan.nchunk, plan.contig, plan.nsmall, act,
+                                     use_gelu, st);
     if (gate.type != up.type) {
         set_error("expert gate/up: gate type %d and up type %d differ", gate.type, up.type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
@@ -1209,8 +1200,8 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
         return ANEDVD_E_INVALID_ARG;
     }
     if (plan.kind == kMmStaged)
-        return launch_grouped_down(down, act, H, I, d, P, plan.mt_dn, plan.nchunk, plan.contig, plan.ks_dn, ypart, kk,
-                                   st);
+        return launch_grouped_down(down, act, H, I, d, P, plan.mt_dn, plan.nchunk, plan.contig, plan.nsmall, plan.ks_dn,
+                                   ypart, kk, st);
     MmArgs a{};
     a.w0 = down;
     a.x = act;

@@ -163,7 +163,7 @@ __device__ inline void x_barrier()
 // loads issued at steps s - 1 and s and the activation loads of steps s + 2 and
 // s + 3 that exist.  The slot step s + 4 will fill is the one step s reads, free
 // after that barrier.
-template <class F, int MT, int MTL, class TS, class X>
+template <class F, int MT, int MTL, bool kPeel, class TS, class X>
 __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int lane, X &x, half_t *xs0,
                                    half_t *xs1, half_t *xs2, half_t *xs3, f32x4 (*acc)[MT])
 {
@@ -193,57 +193,184 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int 
     x_barrier();
     // the lane's operand offsets in a slot (halves): row n of a token tile, piece 2 g + j
     const int ao0 = n * 64 + (((2 * g) ^ x_sw(n)) << 3), ao1 = n * 64 + (((2 * g + 1) ^ x_sw(n)) << 3);
+    // Step s = s0 + k of an unrolled block (k a constant).  With kPeel, the blocks
+    // whose steps all lie DA or more before the end (kTail false) issue every
+    // prefetch unguarded with constant wait counts, and only the remaining blocks
+    // keep the guards.  (The gate/up kernels peel: Qwen3 Q4_K_M 512-token gate/up
+    // 74 -> 69 us.  The down kernels do not: their register pressure rose with it,
+    // the Q6_K kernel's spill from 36 to 112 bytes per lane and the 128-token Q8_0
+    // kernel's registers from 226 to 274, and they ran slower.)
+    auto step = [&](auto kc, auto tailc, int s0) {
+        constexpr int k = decltype(kc)::value;
+        constexpr bool kTail = decltype(tailc)::value;
+        const int s = s0 + k;
+        F::load(w[(k + D) % R], W, rb, kTail ? ws(s + D) : s0w + s + D, lane);
+        if (!kTail || s + DA < steps) x.issue(slot((k + DA) & 3), s + DA, (k + DA) & 3);
+        __builtin_amdgcn_sched_barrier(0);
+        const int ss = k % F::kSpu;
+        const half_t *a = slot(k);
+        F::begin(w[k % R], st, ss, lane);
+        half8 av[2][MT];
+        if constexpr (F::kHoistA) {
+#pragma unroll
+            for (int mt = 0; mt < MTL; mt++) {
+                av[0][mt] = *(const half8 *)(a + mt * 16 * 64 + ao0);
+                av[1][mt] = *(const half8 *)(a + mt * 16 * 64 + ao1);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            half8 b[kPfTiles];
+#pragma unroll
+            for (int tt = 0; tt < kPfTiles; tt++) b[tt] = F::bop(w[k % R], st, ss, tt, j, lane);
+#pragma unroll
+            for (int mt = 0; mt < MTL; mt++) {
+                if constexpr (!F::kHoistA) av[j][mt] = *(const half8 *)(a + mt * 16 * 64 + (j ? ao1 : ao0));
+#pragma unroll
+                for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av[j][mt], b[tt], acc[tt][mt]);
+            }
+        }
+        if constexpr (!kTail) {
+            x_wait<F, X>(2);
+            x.fix(slot((k + 1) & 3), (k + 1) & 3);
+            x_barrier();
+        } else if (s + 1 < steps) {
+            x_wait<F, X>((s + 2 < steps) + (s + 3 < steps));
+            x.fix(slot((k + 1) & 3), (k + 1) & 3);
+            x_barrier();
+        }
+    };
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    using C2 = std::integral_constant<int, 2>;
+    using C3 = std::integral_constant<int, 3>;
+    static_assert(U == 4, "the blocks below unroll four steps");
+    int s0 = 0;
+    if constexpr (kPeel)
+        for (; s0 + U + DA - 1 < steps; s0 += U) {
+            step(C0{}, std::false_type{}, s0);
+            step(C1{}, std::false_type{}, s0);
+            step(C2{}, std::false_type{}, s0);
+            step(C3{}, std::false_type{}, s0);
+        }
+    for (; s0 < steps; s0 += U) {
+        step(C0{}, std::true_type{}, s0);
+        if (s0 + 1 < steps) step(C1{}, std::true_type{}, s0);  // uniform
+        if (s0 + 2 < steps) step(C2{}, std::true_type{}, s0);
+        if (s0 + 3 < steps) step(C3{}, std::true_type{}, s0);
+    }
+}
+
+// ------------------------------------------------------------ small groups
+//
+// A group of at most 16 tokens is one 16-token tile: its workgroup would stage a
+// mostly empty ring and wait at a barrier every step for it.  Its wavefronts read
+// their activation fragments straight from memory instead (L2 hits: the rows are
+// shared by the workgroups of every row group), like the weights, two steps ahead
+// in registers, with no LDS and no barrier in the K loop.  The weights go through
+// the same decoders as the grouped GEMM (each step dequantised once, scales folded
+// into the f16 weights), so a small group costs the same dequantisation as one
+// grouped chunk and none of the decode kernels' per-block f32 rescaling.
+
+// gate/up: the lane's token row of x (one power of two per row, no rescale).
+struct DirX {
+    struct Frag {
+        u32x4 v[2];
+    };
+    rsrc_t q;
+    int off;  // the lane's token row + its 32-byte piece of a 64-column step (bytes)
+    __device__ inline void load(Frag &f, int s) const
+    {
+        f.v[0] = __builtin_amdgcn_raw_buffer_load_b128(q, off, s * 2 * kStep, 0);
+        f.v[1] = __builtin_amdgcn_raw_buffer_load_b128(q, off + 16, s * 2 * kStep, 0);
+    }
+    __device__ inline void prep(const Frag &f, half8 *av) const
+    {
+        av[0] = as_h8(f.v[0]);
+        av[1] = as_h8(f.v[1]);
+    }
+};
+
+// down: the SwiGLU activations of the lane's position carry a power of two per
+// 64-column group (one per step); each step's fragments are rescaled to the row's
+// reference (the largest descale, so the factor is a power of two <= 1, exact) and
+// the result is multiplied by the reference once at the end, as the ring does.
+struct DirAct {
+    struct Frag {
+        u32x4 v[2];
+        float d;
+    };
+    rsrc_t q, ds;
+    int off, doff, ld4;
+    float rinv;
+    __device__ inline void load(Frag &f, int s) const
+    {
+        f.v[0] = __builtin_amdgcn_raw_buffer_load_b128(q, off, s * 2 * kStep, 0);
+        f.v[1] = __builtin_amdgcn_raw_buffer_load_b128(q, off + 16, s * 2 * kStep, 0);
+        f.d = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ds, doff, s * ld4, 0));
+    }
+    __device__ inline void prep(const Frag &f, half8 *av) const
+    {
+        const half_t k = (half_t)(f.d * rinv);
+        av[0] = as_h8(f.v[0]) * k;
+        av[1] = as_h8(f.v[1]) * k;
+    }
+};
+
+// Steps [0, steps) of the wavefront's four tiles against one 16-token tile whose
+// activation fragments come from `as`: weights and activations two steps ahead in
+// a four-register ring (the same unconditional loads as pf_loop_dma: weights past
+// the last step read 0 out of range, activations repeat the last step).
+template <class F, class TS, class AS>
+__device__ inline void pf_loop_direct(const TS &W, int rb, int steps, int lane, const AS &as, f32x4 (*acc)[1])
+{
+    constexpr int U = 4, D = 2, R = 4;
+    static_assert(U % F::kSpu == 0, "a scale unit must fit an unrolled block");
+    const int so = (W.src(0).nrb - rb) * W.src(0).steps;
+    auto ws = [&](int v) { return v < steps ? v : so; };
+    typename F::Raw w[R];
+    typename F::State st;
+    typename AS::Frag xa[R];
+#pragma unroll
+    for (int v = 0; v < D; v++) {
+        F::load(w[v], W, rb, ws(v), lane);
+        as.load(xa[v], min(v, steps - 1));
+    }
     for (int s0 = 0; s0 < steps; s0 += U) {
 #pragma unroll
         for (int k = 0; k < U; k++) {
             const int s = s0 + k;
             if (s >= steps) break;  // uniform
             F::load(w[(k + D) % R], W, rb, ws(s + D), lane);
-            if (s + DA < steps) x.issue(slot((k + DA) & 3), s + DA, (k + DA) & 3);
+            as.load(xa[(k + D) % R], min(s + D, steps - 1));
             __builtin_amdgcn_sched_barrier(0);
             const int ss = k % F::kSpu;
-            const half_t *a = slot(k);
             F::begin(w[k % R], st, ss, lane);
-            half8 av[2][MT];
-            if constexpr (F::kHoistA) {
-#pragma unroll
-                for (int mt = 0; mt < MTL; mt++) {
-                    av[0][mt] = *(const half8 *)(a + mt * 16 * 64 + ao0);
-                    av[1][mt] = *(const half8 *)(a + mt * 16 * 64 + ao1);
-                }
-            }
+            half8 av[2];
+            as.prep(xa[k % R], av);
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 half8 b[kPfTiles];
 #pragma unroll
                 for (int tt = 0; tt < kPfTiles; tt++) b[tt] = F::bop(w[k % R], st, ss, tt, j, lane);
 #pragma unroll
-                for (int mt = 0; mt < MTL; mt++) {
-                    if constexpr (!F::kHoistA) av[j][mt] = *(const half8 *)(a + mt * 16 * 64 + (j ? ao1 : ao0));
-#pragma unroll
-                    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av[j][mt], b[tt], acc[tt][mt]);
-                }
-            }
-            if (s + 1 < steps) {
-                x_wait<F, X>((s + 2 < steps) + (s + 3 < steps));
-                x.fix(slot((k + 1) & 3), (k + 1) & 3);
-                x_barrier();
+                for (int tt = 0; tt < kPfTiles; tt++) acc[tt][0] = mfma(av[j], b[tt], acc[tt][0]);
             }
         }
     }
 }
 
-template <class F, int MT, int L = MT, class TS, class X>
+template <class F, int MT, bool kPeel, int L = MT, class TS, class X>
 __device__ inline void pf_loop_dma_live(const TS &W, int rb, int s0w, int steps, int lane, X &x, half_t *xs0,
                                         half_t *xs1, half_t *xs2, half_t *xs3, int mt_live, f32x4 (*acc)[MT])
 {
     if constexpr (L > 1) {
         if (mt_live < L) {
-            pf_loop_dma_live<F, MT, L - 1>(W, rb, s0w, steps, lane, x, xs0, xs1, xs2, xs3, mt_live, acc);
+            pf_loop_dma_live<F, MT, kPeel, L - 1>(W, rb, s0w, steps, lane, x, xs0, xs1, xs2, xs3, mt_live, acc);
             return;
         }
     }
-    pf_loop_dma<F, MT, L>(W, rb, s0w, steps, lane, x, xs0, xs1, xs2, xs3, acc);
+    pf_loop_dma<F, MT, L, kPeel>(W, rb, s0w, steps, lane, x, xs0, xs1, xs2, xs3, acc);
 }
 
 struct PfArgs {
@@ -257,6 +384,7 @@ struct PfArgs {
     int sub;      // workgroups per work-list chunk: d.chunk / (16 MT)
     int ks;       // down: K shares (planes of ypart)
     int contig;   // pf_item's contiguous order
+    int nsmall;   // capacity of the small groups' list (d.chunks_s): workgroups per row group after the grouped ones
 };
 
 // Workgroup order.  The hardware deals workgroups to the 8 XCDs round robin
@@ -311,13 +439,102 @@ __device__ inline bool pf_chunk(const Dispatch &d, int w, int sub, int &e, int &
 
 // ------------------------------------------------------------ gate / up
 
-// Grid nw8 * I/128 workgroups of 256 threads (pf_item's order).  Wave w:
-// tiles t0 = 2 (w & 1) and t0 + 1 of both gate and up of row block 2 x + (w >> 1),
-// x the workgroup's row-block pair, so SiLU(g) * u forms in registers.  A token's
-// 64-column activation group (one row block) is split over the wavefront pair
-// (w, w ^ 1): each takes its 32 columns' largest magnitude (in-lane over two tiles,
-// DPP over the 16 lanes of a row), the pair meets in LDS, and each writes its 32
-// columns scaled by the group's power of two.
+// The gate/up epilogue of a workgroup's 16 MT tokens (positions p0 .. p0 + nt - 1):
+// act = SiLU(g dv) * (u dv) over the gate accumulators (token tiles past the
+// chunk's live ones hold zeros, and stay zero), a power of two per (token,
+// 64-column group) from the wavefront pair's largest magnitudes (met in LDS:
+// gmax[wv][m], 16 MT floats per wavefront), f16 pairs stored.  tdv: thread m's
+// token descale (m < 16 MT); dvs: LDS [16 MT].
+template <int MT>
+__device__ inline void pf_gu_epilogue(const PfArgs &a, f32x4 (*acc)[MT], int p0, int nt, int rb, int t0, int wv,
+                                      int lane, float tdv, float *dvs, float *gmax)
+{
+    const int n = lane & 15, g = lane >> 4;
+    if ((int)threadIdx.x < 16 * MT) dvs[threadIdx.x] = tdv;
+    __syncthreads();
+    // the activation choice is uniform, taken once outside the unrolled loops
+    auto act_pass = [&](auto gelu) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * mt + 4 * g + i;
+                const float dv = dvs[m];
+                float mx = 0.0f;
+#pragma unroll
+                for (int tp = 0; tp < 2; tp++) {
+                    const float v = gate_act(acc[tp][mt][i] * dv, decltype(gelu)::value) * (acc[2 + tp][mt][i] * dv);
+                    acc[tp][mt][i] = v;
+                    mx = fmaxf(mx, fabsf(v));
+                }
+                mx = row_max_f32(mx);
+                if (n == 0) gmax[wv * 16 * MT + m] = mx;
+            }
+    };
+    if (a.use_gelu) act_pass(std::true_type{});
+    else act_pass(std::false_type{});
+    __syncthreads();
+    // Lane n even stores the f16 pair of columns (n, n + 1), adjacent in the
+    // activation format, through a buffer descriptor: the token row's offset is
+    // scalar, the lane's row and column offset fixed.
+    const bool even = (n & 1) == 0;
+    const rsrc_t aq = make_rsrc(a.act.q, (size_t)a.P * a.I * 2);
+    const rsrc_t ads = make_rsrc(a.act.ds, (size_t)(a.I / kStep) * a.act.ld * 4);
+    const int lrow = 4 * g * a.I * 2;
+    const int col[2] = {2 * (kStep * rb + mma_pos(16 * t0 + n)), 2 * (kStep * rb + mma_pos(16 * (t0 + 1) + n))};
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * mt + 4 * g + i;
+            const float sc = pow2_scale(fmaxf(gmax[wv * 16 * MT + m], gmax[(wv ^ 1) * 16 * MT + m]));
+            const int srow = (p0 + 16 * mt + i) * a.I * 2;  // uniform
+#pragma unroll
+            for (int tp = 0; tp < 2; tp++) {
+                const float v = acc[tp][mt][i] * sc;
+                const float vn = dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]: lane n ^ 1's value
+                if (m < nt && even) {
+                    const h2 pr = {(half_t)v, (half_t)vn};
+                    __builtin_amdgcn_raw_buffer_store_b32(h2_bits(pr), aq, lrow + col[tp], srow, 0);
+                }
+            }
+            if (m < nt && t0 == 0 && n == 0)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pow2_recip(sc)), ads, 16 * g,
+                                                      (rb * a.act.ld + p0 + 16 * mt + i) * 4, 0);
+        }
+}
+
+// Workgroup b of a small group's part of the gate/up grid: group b % nsmall of
+// the small list, row-block pair b / nsmall, the grouped kernel's wavefront
+// mapping (gate and up of the same 32 rows per wavefront) on one 16-token tile.
+template <class F>
+__device__ inline void pf_small_gateup(const PfArgs &a, int b, float *dvs, float *gmax)
+{
+    const int item = b % a.nsmall, rbg = b / a.nsmall;
+    const uint64_t c = a.d.chunks_s[item];  // item < the list's capacity: loaded beside the count
+    if (item >= a.d.meta[7]) return;        // uniform over the workgroup
+    const int e = (int)(c & 0xFFu), nt = (int)((c >> 8) & 0xFFu), p0 = (int)(c >> 16);
+    const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int t0 = 2 * (wv & 1), rb = 2 * rbg + (wv >> 1);
+    const Tiles2 W{planes(a.w0, e), planes(a.w1, e), t0};
+    f32x4 acc[kPfTiles][1];
+#pragma unroll
+    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][0] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    const float tdv = (int)threadIdx.x < 16 ? a.x.ds[a.d.rows[p0 + min((int)threadIdx.x, nt - 1)]] : 0.0f;
+    DirX xs;
+    xs.q = make_rsrc(a.x.q, (size_t)a.x.ld * a.H * 2);
+    xs.off = a.d.rows[p0 + min(n, nt - 1)] * a.H * 2 + 32 * g;
+    pf_loop_direct<F>(W, rb, a.H / kStep, lane, xs, acc);
+    pf_gu_epilogue<1>(a, acc, p0, nt, rb, t0, wv, lane, tdv, dvs, gmax);
+}
+
+// Grid nw8 * I/128 workgroups of 256 threads (pf_item's order), then nsmall * I/128
+// for the small groups.  Wave w: tiles t0 = 2 (w & 1) and t0 + 1 of both gate and
+// up of row block 2 x + (w >> 1), x the workgroup's row-block pair, so SiLU(g) * u
+// forms in registers.  A token's 64-column activation group (one row block) is
+// split over the wavefront pair (w, w ^ 1): each takes its 32 columns' largest
+// magnitude (in-lane over two tiles, DPP over the 16 lanes of a row), the pair
+// meets in LDS, and each writes its 32 columns scaled by the group's power of two.
 // Three wavefronts per SIMD where the decoder fits them without spilling (Q4_K at
 // 64-token workgroups: 170 -> 168 VGPRs), else the compiler's choice.
 template <class F, int MT>
@@ -333,9 +550,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
     __shared__ float gmax[4][16 * MT];  // per wavefront: its 32 columns' largest |act| per token
     int e, p0, nt, w, rbg;
     const int nw = a.nchunk * a.sub;
+    if constexpr (MT == 4) {
+        const int nbig = pf_nw8(nw) * (a.I / (2 * kRowBlock));
+        if ((int)blockIdx.x >= nbig) {
+            pf_small_gateup<F>(a, (int)blockIdx.x - nbig, dvs, &gmax[0][0]);
+            return;
+        }
+    }
     pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, w, rbg);
     if (w >= nw || !pf_chunk<MT>(a.d, w, a.sub, e, p0, nt)) return;  // uniform over the workgroup
-    const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int wv = wave_id(), lane = threadIdx.x & 63;
     const int t0 = 2 * (wv & 1), rb = 2 * rbg + (wv >> 1);
     const Tiles2 W{planes(a.w0, e), planes(a.w1, e), t0};
     f32x4 acc[kPfTiles][MT];  // [0, 1]: gate tiles t0, t0 + 1; [2, 3]: up
@@ -356,62 +580,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
         const int row = 8 * (wv * DmaX<MT>::kInst + i) + (lane >> 3);
         xd.off[i] = a.d.rows[p0 + min(row, nt - 1)] * a.H * 2 + 16 * ((lane & 7) ^ x_sw(row));
     }
-    pf_loop_dma_live<F, MT>(W, rb, 0, a.H / kStep, lane, xd, xs0, xs1, xs2, xs3, mt_live, acc);
-
-    if ((int)threadIdx.x < 16 * MT) dvs[threadIdx.x] = tdv;
-    __syncthreads();
-    // act = SiLU(g dv) * (u dv) over the gate accumulators (token tiles past the
-    // chunk's live ones hold zeros, and stay zero); the activation choice is
-    // uniform, taken once outside the unrolled loops
-    auto act_pass = [&](auto gelu) {
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 16 * mt + 4 * g + i;
-                const float dv = dvs[m];
-                float mx = 0.0f;
-#pragma unroll
-                for (int tp = 0; tp < 2; tp++) {
-                    const float v = gate_act(acc[tp][mt][i] * dv, decltype(gelu)::value) * (acc[2 + tp][mt][i] * dv);
-                    acc[tp][mt][i] = v;
-                    mx = fmaxf(mx, fabsf(v));
-                }
-                mx = row_max_f32(mx);
-                if (n == 0) gmax[wv][m] = mx;
-            }
-    };
-    if (a.use_gelu) act_pass(std::true_type{});
-    else act_pass(std::false_type{});
-    __syncthreads();
-    // Lane n even stores the f16 pair of columns (n, n + 1), adjacent in the
-    // activation format, through a buffer descriptor: the token row's offset is
-    // scalar, the lane's row and column offset fixed.
-    const bool even = (n & 1) == 0;
-    const rsrc_t aq = make_rsrc(a.act.q, (size_t)a.P * a.I * 2);
-    const rsrc_t ads = make_rsrc(a.act.ds, (size_t)(a.I / kStep) * a.act.ld * 4);
-    const int lrow = 4 * g * a.I * 2;
-    const int col[2] = {2 * (kStep * rb + mma_pos(16 * t0 + n)), 2 * (kStep * rb + mma_pos(16 * (t0 + 1) + n))};
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 16 * mt + 4 * g + i;
-            const float sc = pow2_scale(fmaxf(gmax[wv][m], gmax[wv ^ 1][m]));
-            const int srow = (p0 + 16 * mt + i) * a.I * 2;  // uniform
-#pragma unroll
-            for (int tp = 0; tp < 2; tp++) {
-                const float v = acc[tp][mt][i] * sc;
-                const float vn = dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]: lane n ^ 1's value
-                if (m < nt && even) {
-                    const h2 pr = {(half_t)v, (half_t)vn};
-                    __builtin_amdgcn_raw_buffer_store_b32(h2_bits(pr), aq, lrow + col[tp], srow, 0);
-                }
-            }
-            if (m < nt && t0 == 0 && n == 0)
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pow2_recip(sc)), ads, 16 * g,
-                                                      (rb * a.act.ld + p0 + 16 * mt + i) * 4, 0);
-        }
+    pf_loop_dma_live<F, MT, true>(W, rb, 0, a.H / kStep, lane, xd, xs0, xs1, xs2, xs3, mt_live, acc);
+    pf_gu_epilogue<MT>(a, acc, p0, nt, rb, t0, wv, lane, tdv, dvs, &gmax[0][0]);
 }
 
 // ---------------------------------------------------------------- down
@@ -424,8 +594,63 @@ constexpr int pf_dn_waves()
     return std::is_same<F, FQ6_KDown>::value ? 3 : 1;
 }
 
-// Grid nw8 * H/256 * ks workgroups of 256 threads (pf_item's order).  Wave w: row
-// block 4 x + w, K share kq.  Before the K loop the workgroup finds each position's largest descale
+// Workgroup b of a small group's part of the down grid (K not split): group
+// b % nsmall of the small list, row-block group b / nsmall (wave w: row block
+// 4 (b / nsmall) + w), one 16-position tile; the positions' row references found
+// as the grouped kernel does (ref, orow, red: LDS of 16, 16 and 256 entries).
+template <class F>
+__device__ inline void pf_small_down(const PfArgs &a, int b, float *ref, int *orow, float *red)
+{
+    const int item = b % a.nsmall, rbg = b / a.nsmall;
+    const uint64_t c = a.d.chunks_s[item];  // item < the list's capacity: loaded beside the count
+    if (item >= a.d.meta[7]) return;        // uniform over the workgroup
+    const int e = (int)(c & 0xFFu), nt = (int)((c >> 8) & 0xFFu), p0 = (int)(c >> 16);
+    const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int rb = 4 * rbg + wv;
+    const int G = a.I / kStep, ld = a.x.ld;
+    {
+        // thread (part, m): every 16th group of position m; the 16 partial maxima meet in LDS
+        const int m = threadIdx.x & 15, part = threadIdx.x >> 4;
+        const int pr = min(p0 + m, a.P - 1);
+        if (part == 0) orow[m] = a.d.rows[pr] * a.kk + a.d.slots[pr];
+        float mx = 0.0f;
+        for (int g0 = part; g0 < G; g0 += 16) mx = fmaxf(mx, a.x.ds[(size_t)g0 * ld + pr]);
+        red[part * 16 + m] = mx;
+        __syncthreads();
+        if (part == 0) {
+            float r = red[m];
+#pragma unroll
+            for (int i = 1; i < 16; i++) r = fmaxf(r, red[i * 16 + m]);
+            ref[m] = r;
+        }
+        __syncthreads();
+    }
+    f32x4 acc[kPfTiles][1];
+#pragma unroll
+    for (int tt = 0; tt < kPfTiles; tt++) acc[tt][0] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    const int pn = min(p0 + n, a.P - 1);  // the lane's position
+    DirAct xs;
+    xs.q = make_rsrc(a.x.q, (size_t)a.P * a.I * 2);
+    xs.ds = make_rsrc(a.x.ds, (size_t)G * ld * 4);
+    xs.off = pn * a.I * 2 + 32 * g;
+    xs.doff = pn * 4;
+    xs.ld4 = ld * 4;
+    xs.rinv = 1.0f / ref[n];
+    pf_loop_direct<F>(Tiles1{planes(a.w0, e)}, rb, G, lane, xs, acc);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int m = 4 * g + i;
+        if (m < nt) {
+            float *yp = a.ypart + (size_t)orow[m] * a.H + (size_t)kRowBlock * rb + n;
+#pragma unroll
+            for (int tt = 0; tt < kPfTiles; tt++) yp[16 * tt] = acc[tt][0][i] * ref[m];
+        }
+    }
+}
+
+// Grid nw8 * H/256 * ks workgroups of 256 threads (pf_item's order), then
+// nsmall * H/256 for the small groups (ks = 1).  Wave w: row block 4 x + w, K share
+// kq.  Before the K loop the workgroup finds each position's largest descale
 // over the I/64 groups (the row reference); staging scales every group to it, and
 // the results are multiplied by it once at the end.  Positions past the group's
 // end are computed on the next group's (or, past the last position, the last
@@ -438,6 +663,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_dn_waves
     __shared__ float ref4[256 / (16 * MT)][16 * MT];
     int e, p0, nt, w, rest;
     const int nw = a.nchunk * a.sub;
+    if constexpr (MT == 4) {
+        const int nbig = pf_nw8(nw) * (a.H / (4 * kRowBlock)) * a.ks;
+        if ((int)blockIdx.x >= nbig) {
+            pf_small_down<F>(a, (int)blockIdx.x - nbig, ref, orow, &ref4[0][0]);
+            return;
+        }
+    }
     pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, w, rest);
     if (w >= nw || !pf_chunk<MT>(a.d, w, a.sub, e, p0, nt)) return;
     const int rbg = rest / a.ks, kq = rest - rbg * a.ks;
@@ -501,7 +733,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_dn_waves
         const int j = min(lane, 8 * kI - 1), row = 8 * (wv * kI + j / 8) + j % 8;
         xd.doff = min(p0 + row, a.P - 1) * 4 + s0 * xd.ld4;
     }
-    pf_loop_dma_live<F, MT>(W, rb, s0, ksteps, lane, xd, ys0, ys1, ys2, ys3, mt_live, acc);
+    pf_loop_dma_live<F, MT, false>(W, rb, s0, ksteps, lane, xd, ys0, ys1, ys2, ys3, mt_live, acc);
     float *ypk = a.ypart + (size_t)kq * a.P * a.H;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
@@ -539,11 +771,15 @@ static int pf_sub(const Dispatch &d, int mt)
 template <class F, int MT>
 static int launch_pf(const PfArgs &a, bool gateup, hipStream_t st)
 {
+    if (a.nsmall && (MT != 4 || a.ks != 1 || !a.d.chunks_s)) {
+        set_error("grouped GEMM: small groups need 64-token workgroups, an unsplit K and the dispatch's list");
+        return ANEDVD_E_INVALID_ARG;
+    }
     if (gateup) {
-        const size_t wgs = (size_t)pf_nw8(a.nchunk * a.sub) * (a.I / (2 * kRowBlock));
+        const size_t wgs = ((size_t)pf_nw8(a.nchunk * a.sub) + a.nsmall) * (a.I / (2 * kRowBlock));
         hipLaunchKernelGGL((k_pf_gateup<F, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     } else {
-        const size_t wgs = (size_t)pf_nw8(a.nchunk * a.sub) * (a.H / (4 * kRowBlock)) * a.ks;
+        const size_t wgs = ((size_t)pf_nw8(a.nchunk * a.sub) * a.ks + a.nsmall) * (a.H / (4 * kRowBlock));
         hipLaunchKernelGGL((k_pf_down<F, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     }
     ANEDVD_HIP(hipGetLastError());
@@ -595,7 +831,7 @@ static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStr
 }
 
 int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
-                          int mt, int nchunk, int contig, const ActQ &act, int use_gelu, hipStream_t st)
+                          int mt, int nchunk, int contig, int nsmall, const ActQ &act, int use_gelu, hipStream_t st)
 {
     if (gate.type != up.type) {
         set_error("grouped gate/up: gate type %d and up type %d differ", gate.type, up.type);
@@ -614,12 +850,13 @@ int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H
     a.use_gelu = use_gelu;
     a.ks = 1;
     a.contig = contig;
+    a.nsmall = nsmall;
     if (!(a.sub = pf_sub(d, mt))) return ANEDVD_E_INVALID_ARG;
     return launch_pf_type(gate.type, a, mt, true, st);
 }
 
 int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
-                        int nchunk, int contig, int ks, float *ypart, int kk, hipStream_t st)
+                        int nchunk, int contig, int nsmall, int ks, float *ypart, int kk, hipStream_t st)
 {
     if (!grouped_down_ks_ok(down.type, I, ks)) {
         set_error("grouped down: %d K shares do not split %d steps into whole blocks of four", ks, I / kStep);
@@ -637,6 +874,7 @@ int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const D
     a.nchunk = nchunk;
     a.ks = ks;
     a.contig = contig;
+    a.nsmall = nsmall;
     if (!(a.sub = pf_sub(d, mt))) return ANEDVD_E_INVALID_ARG;
     return launch_pf_type(down.type, a, mt, false, st);
 }

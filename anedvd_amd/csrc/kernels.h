@@ -34,17 +34,6 @@ struct Dispatch {
     int32_t *xr;
     int xper;
 
-    // The small groups' list as a work list of its own (count in meta[3] of the view).
-    Dispatch small_view(int chunk_s) const
-    {
-        Dispatch v = *this;
-        v.meta = meta + 4;
-        v.chunks = chunks_s;
-        v.chunk = chunk_s;
-        v.chunks_s = nullptr;
-        v.small = 0;
-        return v;
-    }
 };
 
 // A work-list entry: expert e (< 256), the chunk's first position p0 and its
@@ -107,16 +96,14 @@ struct MmPlan {
     int contig;   // grouped GEMM: XCD-contiguous workgroup order
     int chunk;    // tokens per work-list chunk (16 mt), the dispatch's `chunk`
     int nchunk;   // bound on the work list's length: P / chunk + max_u
-    int small;    // grouped GEMM: groups of at most this many tokens go to the decode kernels (0 = none)
+    int small;    // grouped GEMM: groups of at most this many tokens run on one 16-token tile each (0 = none)
+    int nsmall;   // grouped GEMM with small: capacity of the small groups' list (max_u)
     int xper;     // grouped GEMM with contig: chunks per XCD range of the work list (0 = none)
     int fuse;     // decode, ks_gu > 1: the down kernel finishes gate/up's K partials (no k_act_reduce)
 };
 bool mm_supported(int type);
 // P (token, slot) entries of T tokens over at most max_u experts.
 MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u, int T);
-// The decode-kernel plan for the small groups of a grouped plan (p.small > 0):
-// one 16-token chunk per group, K not split, the same down partial count.
-MmPlan plan_small(const MmPlan &p, int max_u);
 // gate/up + SiLU(gate)*up for every dispatched (token, expert) position, written
 // to `act` [P][I] in the activation format.  With plan.ks_gu > 1 the K partials
 // go to `part` [ks][P][2][I] and a second launch finishes them, or, with
@@ -135,11 +122,13 @@ bool grouped_supported(int H, int I);
 bool grouped_wide(int type);  // the type has a 128-token-chunk grouped kernel
 // A workgroup takes 16 mt tokens of a work-list chunk of d.chunk tokens.
 // contig: XCD-contiguous workgroup order (experts averaging two or more chunks).
+// nsmall > 0 (mt 4, K not split): the same launch also runs the groups of the
+// dispatch's small list (d.chunks_s, capacity nsmall), a 16-token tile each.
 int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H, int I, const Dispatch &d, int P,
-                          int mt, int nchunk, int contig, const ActQ &act, int use_gelu, hipStream_t st);
+                          int mt, int nchunk, int contig, int nsmall, const ActQ &act, int use_gelu, hipStream_t st);
 // With ks > 1 the K axis is split over ks workgroups, each writing plane ks of ypart.
 int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const Dispatch &d, int P, int mt,
-                        int nchunk, int contig, int ks, float *ypart, int kk, hipStream_t st);
+                        int nchunk, int contig, int nsmall, int ks, float *ypart, int kk, hipStream_t st);
 bool grouped_down_ks_ok(int type, int I, int ks);  // I/64 steps split into ks whole scale-unit blocks
 
 // k_ops.hip -- cpu.moeExpertAccumF32 / moeExpertAccum on caller weight slices

@@ -318,18 +318,6 @@ __global__ void k_shared_prep(const float *__restrict__ h, const uint16_t *__res
     if (threadIdx.x == 0) scale[t] = shared_sigmoid(g);
 }
 
-// The gate/up (which 0) or down (1) of the groups of at most plan.small tokens, on
-// the decode kernels from the dispatch's second list: they write their own
-// positions of act and rows of ypart, so they may run beside the grouped launches.
-static int launch_small_groups(const anedvd_moe_layer *L, const Fwd &f, int which, hipStream_t st)
-{
-    const int H = L->H, I = L->I, kk = L->k + (int)L->n_sh;
-    const MmPlan ps = plan_small(f.plan, f.max_u);
-    const Dispatch dsm = f.d.small_view(ps.chunk);
-    return which == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, dsm, f.P, ps, nullptr, f.act, L->gelu, st)
-                      : launch_expert_down(L->down, f.act, H, I, dsm, f.P, ps, nullptr, L->gelu, f.ypart, kk, st);
-}
-
 // One forward call on stream st.  With `resid` the output is resid + the block's
 // output (the engine's x += proj, main.zig:519), as a stack of layers chains it.
 int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_logits, float *d_out, const Fwd &f,
@@ -353,17 +341,11 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
     // A shared expert that is not merged into the routed launches needs only x
     // (converted by the route launch): it runs on the context's second stream beside
     // the routed experts, joined before the combine.  With stage events everything
-    // stays on `st`, so the stages time one at a time.
+    // stays on `st`, so the stages time one at a time.  (Groups of a few tokens,
+    // plan.small, run inside the grouped launches.)
     const bool separate = L->Is && !L->n_sh;
-    // Groups of a few tokens (plan.small) run on the decode kernels beside the
-    // grouped GEMM, on the second stream.
-    const bool small = f.plan.small > 0;
-    const bool fork = (separate || small) && !ev;
+    const bool fork = separate && !ev;
     hipStream_t ss = fork ? L->ctx->aux : st;
-    if (fork) {
-        ANEDVD_HIP(hipEventRecord(L->ctx->fork, st));
-        ANEDVD_HIP(hipStreamWaitEvent(ss, L->ctx->fork, 0));
-    }
     auto shared = [&]() -> int {
         const int Is = (int)L->Is;
         hipLaunchKernelGGL(k_shared_prep, dim3(T), dim3(64), 0, ss, d_h, L->sgate_lin, T, H, f.sd, f.sh_scale);
@@ -372,22 +354,36 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
                                         L->gelu, ss));
         return launch_expert_down(L->sdown, f.sact, H, Is, f.sd, T, f.splan, f.sh_part, L->gelu, f.sh_ypart, 1, ss);
     };
+    auto routed = [&]() -> int {
+        ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act, L->gelu, st));
+        mark(2);
+        ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.part, L->gelu, f.ypart, kk, st));
+        mark(3);
+        return ANEDVD_OK;
+    };
     if (fork) {
-        if (small) {
-            ANEDVD_TRY(launch_small_groups(L, f, 0, ss));
-            ANEDVD_TRY(launch_small_groups(L, f, 1, ss));
+        ANEDVD_HIP(hipEventRecord(L->ctx->fork, st));
+        ANEDVD_HIP(hipStreamWaitEvent(ss, L->ctx->fork, 0));
+        // Once forked, the main stream waits for the second one on every path, so an
+        // error never leaves its kernels writing the workspace into the next call.
+        int rc = shared();
+        const int jrc = hipEventRecord(L->ctx->join, ss) == hipSuccess ? ANEDVD_OK : ANEDVD_E_HIP;
+        if (rc == ANEDVD_OK) rc = jrc;
+        if (rc == ANEDVD_OK) rc = routed();
+        if (jrc == ANEDVD_OK) {
+            if (hipStreamWaitEvent(st, L->ctx->join, 0) != hipSuccess && rc == ANEDVD_OK) {
+                set_error("forward: joining the second stream failed");
+                rc = ANEDVD_E_HIP;
+            }
+        } else if (hipStreamSynchronize(ss) != hipSuccess && rc == ANEDVD_OK) {
+            rc = ANEDVD_E_HIP;
         }
+        if (jrc != ANEDVD_OK && rc == ANEDVD_E_HIP) set_error("forward: recording the second stream's join failed");
+        ANEDVD_TRY(rc);
+    } else {
+        ANEDVD_TRY(routed());
         if (separate) ANEDVD_TRY(shared());
-        ANEDVD_HIP(hipEventRecord(L->ctx->join, ss));
     }
-    ANEDVD_TRY(launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act, L->gelu, st));
-    if (small && !fork) ANEDVD_TRY(launch_small_groups(L, f, 0, st));
-    mark(2);
-    ANEDVD_TRY(launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.part, L->gelu, f.ypart, kk, st));
-    if (small && !fork) ANEDVD_TRY(launch_small_groups(L, f, 1, st));
-    mark(3);
-    if (fork) ANEDVD_HIP(hipStreamWaitEvent(st, L->ctx->join, 0));
-    else if (separate) ANEDVD_TRY(shared());
     mark(4);
     ANEDVD_TRY(launch_combine(f.ypart, f.d.inv, f.probs, T, kk, H, f.plan.ks_dn, P, separate ? f.sh_ypart : nullptr,
                               (separate && L->sgate_lin) ? f.sh_scale : nullptr, separate ? f.splan.ks_dn : 0, d_out,
@@ -1241,12 +1237,10 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
                 const anedvd_moe_layer *L = layers[(size_t)i % n_layers];
                 if (s == 2)  // the router GEMV alone: T tokens of d_h against the layer's [E][H] f16 router
                     return launch_router(L->router_t, L->router, d_h, (int)T, (int)L->E, H, f.logits, st);
-                const int rc = s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part,
-                                                             f.act, L->gelu, st)
-                                      : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.part, L->gelu,
-                                                           f.ypart, (int)(L->k + L->n_sh), st);
-                // the small groups' decode launch after it, on the same stream
-                return rc == ANEDVD_OK && f.plan.small ? launch_small_groups(L, f, s, st) : rc;
+                return s == 0 ? launch_expert_gateup(L->gate, L->up, f.xq, H, I, f.d, P, f.plan, f.part, f.act,
+                                                     L->gelu, st)
+                              : launch_expert_down(L->down, f.act, H, I, f.d, P, f.plan, f.part, L->gelu, f.ypart,
+                                                   (int)(L->k + L->n_sh), st);
             };
             for (int i = 0; i < warmup && src == ANEDVD_OK; i++) src = launch(i);
             if (src == ANEDVD_OK && hipEventRecord(a, st) != hipSuccess) src = ANEDVD_E_HIP;

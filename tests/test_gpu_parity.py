@@ -448,7 +448,7 @@ def test_forward_grouped_xcd_ranges(ctx, sizes):
 
 
 # Sixteen groups averaging 42.5 tokens (the grouped GEMM), six of them of 1 to 16
-# tokens (the decode kernels, beside it).
+# tokens (the grouped launches' small-group workgroups).
 SMALL_SIZES = [1, 3, 8, 16, 17, 30, 64, 65, 90, 120, 130, 10, 5, 50, 40, 31]
 SMALL_SHARED = [dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="small-shared-merged", hidden=256, inter=4096,
                                     n_experts=16, k=2, shared_inter=4096, shared_gated=True),
@@ -459,8 +459,9 @@ SMALL_SHARED = [dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="small-shared-
 @pytest.mark.parametrize("types", FORMATS, ids=lambda t: "/".join(W.TYPE_NAMES[x] for x in t))
 def test_forward_grouped_small_groups(ctx, types):
     """A skewed call on the grouped GEMM: the groups of at most 16 tokens go to the
-    dispatch's second work list and run on the decode kernels (second stream), the
-    rest on the grouped GEMM, every format."""
+    dispatch's second work list and run in the same launches on one 16-token tile
+    each (activations read straight from memory), the rest on the staged grouped
+    GEMM, every format."""
     lg = _logits_for_groups(SMALL_SIZES, seed=31)
     spec = dataclasses.replace(W.MIXTRAL_8X7B_Q4_0, name="small-groups", hidden=256, inter=4096, n_experts=16,
                                gate_type=types[0], up_type=types[1], down_type=types[2], scale_sigma=0.01)
@@ -480,7 +481,7 @@ def test_forward_grouped_small_groups(ctx, types):
 @pytest.mark.parametrize("spec", SMALL_SHARED, ids=lambda s: s.name)
 def test_forward_small_groups_with_shared_expert(ctx, spec):
     """Small groups beside a shared expert merged as pieces (large groups of their
-    own) and beside a separate one (both on the second stream, one join); the
+    own) and beside a separate one (on the second stream, one join); the
     stage-timed call (one stream) and the HIP-graph replay compute the same bits
     as the direct call."""
     lg = _logits_for_groups(SMALL_SIZES, seed=37)
