@@ -45,6 +45,10 @@ struct anedvd_moe_ctx {
     hipEvent_t fork = nullptr, join = nullptr;
     Workspace ws;
     Workspace io;  // staging for the host-pointer entry points
+    // The last forward call on this context (route counts read its dispatch).
+    const anedvd_moe_layer *last_layer = nullptr;
+    const int32_t *last_offsets = nullptr;
+    int last_tokens = 0;
 };
 
 struct anedvd_moe_layer {
@@ -324,6 +328,9 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
                    hipStream_t st, hipEvent_t *ev, const float *resid = nullptr)
 {
     const int H = L->H, I = L->I, E = L->E, k = L->k, kk = k + (int)L->n_sh, P = T * kk;
+    L->ctx->last_layer = L;
+    L->ctx->last_offsets = f.d.offsets;
+    L->ctx->last_tokens = T;
     auto mark = [&](int i) {
         if (ev) (void)hipEventRecord(ev[i], st);
     };
@@ -586,6 +593,7 @@ void anedvd_moe_layer_free(anedvd_moe_layer *L)
     if (L->ctx) {
         (void)hipSetDevice(L->ctx->device);
         (void)hipStreamSynchronize(L->ctx->stream);
+        if (L->ctx->last_layer == L) L->ctx->last_layer = nullptr;
     }
     free_qmat(L->gate);
     free_qmat(L->up);
@@ -979,6 +987,25 @@ int anedvd_moe_layer_forward(anedvd_moe_layer *L, const float *h, size_t T, cons
         stats->down_ks = (uint32_t)f.plan.ks_dn;
         stats->small_groups = f.plan.small ? (uint32_t)meta[7] : 0u;
     }
+    return ANEDVD_OK;
+}
+
+int anedvd_moe_layer_route_counts(anedvd_moe_layer *L, uint32_t *counts, uint32_t *n_tokens)
+{
+    if (!L || !counts) {
+        set_error("layer_route_counts: null layer or counts");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    anedvd_moe_ctx *ctx = L->ctx;
+    if (ctx->last_layer != L || !ctx->last_offsets) {
+        set_error("layer_route_counts: the last forward call on this context was not this layer's");
+        return ANEDVD_E_INVALID_ARG;
+    }
+    std::vector<int32_t> off(L->E + 1);
+    ANEDVD_HIP(hipMemcpyAsync(off.data(), ctx->last_offsets, off.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ANEDVD_HIP(hipStreamSynchronize(ctx->stream));
+    for (uint32_t e = 0; e < L->E; e++) counts[e] += (uint32_t)(off[e + 1] - off[e]);
+    if (n_tokens) *n_tokens += (uint32_t)ctx->last_tokens;
     return ANEDVD_OK;
 }
 

@@ -98,6 +98,7 @@ SIGNATURES = {
     "anedvd_moe_expert_accum": (_i, [_vp, C.c_uint32, _vp, _f, _vp]),
     "anedvd_moe_layer_route": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
     "anedvd_moe_layer_forward": (_i, [_vp, _vp, _sz, _vp, _vp, C.POINTER(Stats)]),
+    "anedvd_moe_layer_route_counts": (_i, [_vp, _vp, _vp]),
     "anedvd_moe_layer_forward_device": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "anedvd_moe_layer_forward_device_noalloc": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "anedvd_moe_layer_forward_device_f16": (_i, [_vp, _vp, _sz, _vp, _vp]),
@@ -401,6 +402,18 @@ class MoeLayer:
 
     def forward_device(self, d_h: int, n_tokens: int, d_logits: int | None, d_out: int):
         _check(lib().anedvd_moe_layer_forward_device(self.h, d_h, n_tokens, d_logits, d_out))
+
+    def route_counts(self, counts: np.ndarray | None = None) -> tuple:
+        """Engine.route_counts for this layer (engine.zig:726-731, 1190-1195): adds
+        the last forward call's per-expert choices into `counts` (uint32 [E], a
+        new zero array if None) and returns (counts, tokens of that call)."""
+        if counts is None:
+            counts = np.zeros(self.spec.n_experts, dtype=np.uint32)
+        if counts.dtype != np.uint32 or counts.shape != (self.spec.n_experts,) or not counts.flags.c_contiguous:
+            raise ValueError("counts must be a contiguous uint32 array of n_experts entries")
+        n = C.c_uint32(0)
+        _check(lib().anedvd_moe_layer_route_counts(self.h, _p(counts), C.byref(n)))
+        return counts, n.value
 
     def forward_device_f16(self, d_h16: int, n_tokens: int, d_logits: int | None, d_out: int):
         """forward_device with [T][H] f16 activations (bits), widened exactly on the device."""

@@ -13,11 +13,12 @@ copies of the layer so the 256 MB Infinity Cache cannot serve the weights.
 Beside it (`configs`): the Qwen3 Q4_K_M 512-token prefill with Zipf routing,
 Mixtral-8x7B Q4_0 at 1 and 2048 tokens, and the DeepSeek-V2-Lite 26-layer stack
 (26 distinct layers chained x += proj, at decode batch 32 and a 1024-token
-prefill).  Every workload's output is checked against the oracle on sampled
-tokens of the same run, and the oracle (the CPU restatement of the reference
-path, AVX2 build) is timed on one pinned host core in two modes: streaming (the
-engine's expert reads, per token or per 128-token prefill chunk) and resident
-f32 experts.
+prefill); the Mixtral and DeepSeek calls run their layer's router GEMV on their
+own input inside the timed call.  Every workload's output is checked against the oracle on sampled
+tokens of the same run (a stack layer by layer), and the oracle (the CPU
+restatement of the reference path, AVX2 build) is timed on one pinned host core in
+two modes: streaming (the engine's expert reads, per token or per 128-token
+prefill chunk) and resident f32 experts.
 
 Prints ONE JSON line (rank 0, N=1).
 """
@@ -41,6 +42,8 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 METRIC = "MoE-layer tok/s + % HBM roofline (decode), % MFMA peak (prefill), 30B-A3B shape"
 CPU_RUNS = 5                   # the CPU baseline reports the median of this many runs
+CPU_RUNS_LONG = 3              # ... or of this many when one run takes longer than CPU_LONG_S
+CPU_LONG_S = 3.0
 
 
 def log(msg: str):
@@ -95,9 +98,11 @@ def pinned_core():
 
 
 def cpu_median(fn) -> tuple:
+    t0 = time.perf_counter()
     fn()  # warm-up
+    runs = CPU_RUNS_LONG if time.perf_counter() - t0 > CPU_LONG_S else CPU_RUNS
     ts = []
-    for _ in range(CPU_RUNS):
+    for _ in range(runs):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
@@ -105,7 +110,8 @@ def cpu_median(fn) -> tuple:
 
 
 def cpu_baseline(spec, L, h, lg, mode_a: tuple, n_b: int) -> dict:
-    """The oracle timed on one pinned core, median of CPU_RUNS runs after a warm-up.
+    """The oracle timed on one pinned core, median of CPU_RUNS runs after a warm-up
+    (CPU_RUNS_LONG when the warm-up run takes more than CPU_LONG_S).
     Mode A is the engine's streaming path: ("stream", n) runs the per-token decode
     loop (engine.zig:705-779: route, read each selected expert's three projections
     from the GGUF bytes to f32, moeExpertAccumF32) over n tokens; ("chunk", n) runs
@@ -124,20 +130,20 @@ def cpu_baseline(spec, L, h, lg, mode_a: tuple, n_b: int) -> dict:
     exp_b = spec.expert_bytes()
     out = {}
     with pinned_core() as core:
-        ta, _ = cpu_median(lambda: ol.forward(ha, la, streaming=(kind == "stream"), fast=True))
+        ta, tsa = cpu_median(lambda: ol.forward(ha, la, streaming=(kind == "stream"), fast=True))
         R = ol.resident(np.unique(ib), fast=True)
-        tb, _ = cpu_median(lambda: R.forward(hb, lb))
+        tb, tsb = cpu_median(lambda: R.forward(hb, lb))
         R.free()
     # bytes the CPU path reads: streaming, every (token, slot) reads its expert; a
     # prefill chunk reads each touched expert once; resident, f32 weights per slot
     bytes_a = (n_a * spec.k if kind == "stream" else touched_a) * exp_b + n_a * spec.shared_bytes()
     bytes_b = n_b * spec.k * 3 * spec.inter * spec.hidden * 4
     out["mode_a"] = {"tokens_per_s": round(n_a / ta, 3), "GBps": round(bytes_a / ta / 1e9, 3),
-                     "median_s": round(ta, 4), "runs": CPU_RUNS,
+                     "median_s": round(ta, 4), "runs": len(tsa),
                      "sample": (f"per-token streaming decode of {n_a} tokens" if kind == "stream" else
                                 f"batched prefill of one {n_a}-token chunk ({touched_a} experts read once)")}
     out["mode_b"] = {"tokens_per_s": round(n_b / tb, 3), "GBps": round(bytes_b / tb / 1e9, 3),
-                     "median_s": round(tb, 4), "runs": CPU_RUNS,
+                     "median_s": round(tb, 4), "runs": len(tsb),
                      "sample": f"decode loop over {n_b} tokens on resident f32 experts ({len(np.unique(ib))} held)"}
     out.update({"cores": 1, "core": core, "kind": "port",
                 "build": "oracle/moe_oracle.c, gcc -O3 -mavx2 -mno-fma -ffp-contract=off (8-lane loops vectorised, "
@@ -148,25 +154,31 @@ def cpu_baseline(spec, L, h, lg, mode_a: tuple, n_b: int) -> dict:
 # ------------------------------------------------------------------ workloads
 
 CONFIGS = {
-    # spec: workloads attribute; T tokens; routing of the logits; copies of the layer
-    # rotated (stack: distinct chained layers); parity: tokens sampled against the
-    # oracle; cpu_a: mode A of the CPU baseline; cpu_b: tokens of mode B
+    # spec: workloads attribute; T tokens; routing: the logits given to the call (zipf,
+    # uniform) or "router": none, the layer routes each call from its own input with
+    # its router GEMV inside the timed call (main.zig:493, engine.zig:715, 1178);
+    # copies of the layer rotated (stack: distinct chained layers); parity: tokens
+    # sampled against the oracle; cpu_a: mode A of the CPU baseline (prefill: one
+    # 128-token chunk, the engine's prefill chunk, engine.zig:45); cpu_b: tokens of mode B
     "qwen3-q4km-512": dict(spec="QWEN3_30B_A3B_Q4_K_M", T=512, routing="zipf", copies=2, parity=32,
-                           cpu_a=("chunk", 32), cpu_b=32),
-    "mixtral-q4_0-2048": dict(spec="MIXTRAL_8X7B_Q4_0", T=2048, routing="normal", copies=3, parity=16,
-                              cpu_a=("chunk", 4), cpu_b=4),
-    "mixtral-q4_0-1": dict(spec="MIXTRAL_8X7B_Q4_0", T=1, routing="normal", copies=3, parity=1,
+                           cpu_a=("chunk", 128), cpu_b=32),
+    "mixtral-q4_0-2048": dict(spec="MIXTRAL_8X7B_Q4_0", T=2048, routing="router", copies=3, parity=16,
+                              cpu_a=("chunk", 128), cpu_b=4),
+    "mixtral-q4_0-1": dict(spec="MIXTRAL_8X7B_Q4_0", T=1, routing="router", copies=8, parity=1,
                            cpu_a=("stream", 1), cpu_b=1),
-    "deepseek-v2-lite-32-x26": dict(spec="DEEPSEEK_V2_LITE_Q8_0", T=32, routing="uniform", stack=26, parity=6,
+    "deepseek-v2-lite-32-x26": dict(spec="DEEPSEEK_V2_LITE_Q8_0", T=32, routing="router", stack=26, parity=6,
                                     cpu_a=("stream", 8), cpu_b=16),
-    "deepseek-v2-lite-1024-x26": dict(spec="DEEPSEEK_V2_LITE_Q8_0", T=1024, routing="uniform", stack=26, parity=6,
-                                      cpu_a=("chunk", 32), cpu_b=16),
+    "deepseek-v2-lite-1024-x26": dict(spec="DEEPSEEK_V2_LITE_Q8_0", T=1024, routing="router", stack=26, parity=6,
+                                      cpu_a=("chunk", 128), cpu_b=16),
 }
 _LAYERS = {}  # (spec name, kind) -> resident layers and their host arrays
 
 
 def logits_for(spec, routing: str, T: int, seed: int):
+    """The router logits a call is given, or None: the layer's own router GEMV."""
     from anedvd_amd import synth
+    if routing == "router":
+        return None
     if routing == "zipf":
         lg = synth.zipf_logits(spec, T, seed=seed)
     elif routing == "uniform":
@@ -212,9 +224,12 @@ def free_layers():
 
 
 def parity_of(got: np.ndarray, want: np.ndarray, n: int) -> dict:
+    """rel-L2 and max-abs error of `got` against the oracle's `want`, with the
+    reference's largest magnitude beside max-abs (its scale)."""
     from anedvd_amd import moe
     return {"tokens_checked": n, "rel_l2": moe.rel_l2(got, want),
-            "max_abs": float(np.abs(got.astype(np.float64) - want).max())}
+            "max_abs": float(np.abs(got.astype(np.float64) - want).max()),
+            "ref_max_abs": float(np.abs(want).max())}
 
 
 def sample_rows(T: int, n: int) -> np.ndarray:
@@ -223,8 +238,9 @@ def sample_rows(T: int, n: int) -> np.ndarray:
 
 def run_config(name: str, ctx, warmup: int, steps: int, with_parity: bool) -> dict:
     """One workload beside the headline: a layer call (route + dispatch + expert
-    products + shared expert + combine, router logits given), rotated over device
-    copies of the layer, or a chained stack of distinct layers.  Reports tokens/s,
+    products + shared expert + combine; the router GEMV too where the workload does
+    not give logits), rotated over device copies of the layer, or a chained stack of
+    distinct layers each routing its own input.  Reports tokens/s,
     the algorithmic HBM bytes/s and useful MFMA-path FLOP/s against the peaks, and
     the oracle's agreement on sampled tokens of the same inputs."""
     from anedvd_amd import moe, synth
@@ -238,44 +254,63 @@ def run_config(name: str, ctx, warmup: int, steps: int, with_parity: bool) -> di
     r = {"name": name, "workload": spec.name, "tokens": T, "routing": c["routing"]}
     if stack:
         Ls, layers = resident_stack(ctx, spec, stack)
-        lgs = np.stack([logits_for(spec, c["routing"], T, seed=1 + i) for i in range(stack)])
-        _, st = layers[0].forward(h, lgs[0], stats=True)
-        d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lgs), ctx.alloc(T * spec.hidden * 4)
+        lgl = [logits_for(spec, c["routing"], T, seed=1 + i) for i in range(stack)]
+        routed = lgl[0] is None
+        _, st = layers[0].forward(h, lgl[0], stats=True)
+        d_h, d_out = ctx.to_device(h), ctx.alloc(T * spec.hidden * 4)
+        d_lg = None if routed else ctx.to_device(np.stack(lgl))
         passes = max(2, steps // stack)
         ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, stack, stack * passes, chain=True)
         _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 0, stack, stages=True, chain=True)
         got = ctx.from_device(d_out, (T, spec.hidden), np.float32)  # one whole pass from d_h
         for p in (d_h, d_lg, d_out):
-            ctx.free(p)
+            if p:
+                ctx.free(p)
         n_calls = stack * passes
         if with_parity:
-            x = h[rows].copy()
+            # Layer by layer on the GPU (host calls over all T tokens: the kernels of the
+            # timed call), each layer checked against the oracle on the GPU's own input
+            # rows.  A layer that routes its own x picks its experts from that x, so both
+            # sides see the same x and the router's bit-exact logits: the check is one
+            # layer's arithmetic.  (A chained oracle would drift to another expert choice
+            # wherever two logits tie within the stack's accumulated rounding.)
+            x, worst = h.copy(), None
             for i in range(stack):
-                x = x + O.OracleLayer(spec, Ls[i]).forward(x, lgs[i][rows], fast=True)
-            r["parity"] = parity_of(got[rows], x, len(rows))
+                proj = layers[i].forward(x, lgl[i])
+                want = O.OracleLayer(spec, Ls[i]).forward(x[rows], None if routed else lgl[i][rows], fast=True)
+                p_i = parity_of(proj[rows], want, len(rows))
+                if worst is None or p_i["rel_l2"] > worst["rel_l2"]:
+                    worst = dict(p_i, layer=i)
+                x = x + proj
+            r["parity"] = dict(worst, check="each layer on the GPU's own input rows; the worst layer",
+                               chained_vs_layer_by_layer_max_abs=float(np.abs(got[rows] - x[rows]).max()))
         r.update({"stack_layers": stack, "layers": f"{stack} distinct layers, chained x += proj",
                   "stack_ms": round(ms / passes, 4), "stack_tokens_per_s": round(T / (ms / passes / 1e3), 1)})
         L = Ls[0]
-        lg = lgs[0]
+        lg = lgl[0]
         solo = None
     else:
         L, layers = resident_copies(ctx, spec, c["copies"])
         lg = logits_for(spec, c["routing"], T, seed=1)
+        routed = lg is None
         out_host, st = layers[0].forward(h, lg, stats=True)
-        d_h, d_lg, d_out = ctx.to_device(h), ctx.to_device(lg), ctx.alloc(T * spec.hidden * 4)
+        d_h, d_out = ctx.to_device(h), ctx.alloc(T * spec.hidden * 4)
+        d_lg = None if routed else ctx.to_device(lg)
         n_calls = max(steps, 2 * c["copies"]) // c["copies"] * c["copies"]
         ms, _ = moe.time_forward(layers, d_h, T, d_lg, d_out, max(warmup, c["copies"]), n_calls)
         _, stages = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, n_calls, stages=True)
         _, solo = moe.time_forward(layers, d_h, T, d_lg, d_out, 1, n_calls, solo=True)
         for p in (d_h, d_lg, d_out):
-            ctx.free(p)
+            if p:
+                ctx.free(p)
         if with_parity:
-            want = O.OracleLayer(spec, L).forward(h[rows], lg[rows], fast=True)
+            want = O.OracleLayer(spec, L).forward(h[rows], None if routed else lg[rows], fast=True)
             r["parity"] = parity_of(out_host[rows], want, len(rows))
         r["layer_copies_rotated"] = c["copies"]
+    r["router_in_call"] = routed
     t = ms / 1e3 / n_calls  # one layer call
-    flops = spec.call_flops(T, with_router=False)
-    lbytes = spec.call_bytes(st["touched_experts"], T, with_router=False)
+    flops = spec.call_flops(T, with_router=routed)
+    lbytes = spec.call_bytes(st["touched_experts"], T, with_router=routed)
     r.update({"touched_experts": st["touched_experts"], "max_group": st["max_group"],
               "path": "grouped GEMM" if st["path"] else "decode MFMA kernels",
               "ms_per_call": round(ms / n_calls, 4), "tokens_per_s": round(T / t, 1),
@@ -292,8 +327,9 @@ def run_config(name: str, ctx, warmup: int, steps: int, with_parity: bool) -> di
         f"{r['TFLOPs']} TFLOP/s ({100 * r['mfma_frac']:.1f}% of fp16 MFMA peak), {r['layer_GBps']} GB/s "
         f"({100 * r['hbm_frac']:.1f}% of HBM), touched {r['touched_experts']}, max group {r['max_group']}"
         + (f", {stack}-layer stack {r['stack_ms']:.3f} ms" if stack else "")
-        + (f", parity rel-L2 {r['parity']['rel_l2']:.2e} on {r['parity']['tokens_checked']} tokens"
-           if "parity" in r else "")
+        + (f", parity rel-L2 {r['parity']['rel_l2']:.2e}, max-abs {r['parity']['max_abs']:.3g} of |ref| "
+           f"{r['parity']['ref_max_abs']:.3g} on {r['parity']['tokens_checked']} tokens" if "parity" in r else "")
+        + (", router GEMV in the call" if routed else ", logits given")
         + f", event stages {r['stage_ms']} (setup {time.perf_counter() - t0:.1f} s)")
     return r
 
@@ -413,7 +449,7 @@ def main():
         want = O.OracleLayer(spec, L).forward(h[rows], lg[rows], fast=True)
         parity = parity_of(out_gpu[rows], want, len(rows))
         log(f"[bench] headline vs oracle on {len(rows)} tokens: rel-L2 {parity['rel_l2']:.2e}, "
-            f"max-abs {parity['max_abs']:.2e}")
+            f"max-abs {parity['max_abs']:.2e} of |ref| {parity['ref_max_abs']:.3g}")
 
     cpu = None
     if args.cpu:

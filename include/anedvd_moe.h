@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define ANEDVD_MOE_ABI_VERSION 4
+#define ANEDVD_MOE_ABI_VERSION 5
 
 /* ggml tensor type ids as stored in GGUF (gguf.zig:30-46). */
 enum anedvd_ggml_type {
@@ -231,6 +231,19 @@ int anedvd_moe_layer_route(anedvd_moe_layer *layer, const float *h, size_t n_tok
  * routed instead. */
 int anedvd_moe_layer_forward(anedvd_moe_layer *layer, const float *h, size_t n_tokens,
                              const float *logits, float *out, anedvd_moe_stats *stats);
+
+/* The engine's routing recorder (Engine.route_counts / route_tokens,
+ * engine.zig:245-250, 726-731, 1190-1195): adds to counts[e], for the layer's
+ * n_experts routed experts, how many of the last forward call's tokens chose
+ * expert e (each token adds its k choices, as the engine's loop does; merged
+ * shared-expert pieces are not counted), and the call's token count to
+ * *n_tokens when n_tokens is non-NULL.  Pointing `counts` at route_counts +
+ * layer * E keeps the engine's [layer][E] table through the drop-in.  It reads
+ * the per-expert offsets the call's dispatch left on the device, so it refers to
+ * the last forward call on the layer's context, whichever entry point made it;
+ * if that call was another layer's, or there was none, it returns
+ * ANEDVD_E_INVALID_ARG and adds nothing.  Synchronous (host memory). */
+int anedvd_moe_layer_route_counts(anedvd_moe_layer *layer, uint32_t *counts, uint32_t *n_tokens);
 
 /* Same with device pointers, stream-ordered on the context's stream, no host
  * synchronisation (stats are not filled). */

@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(moe.LIB_PATH)
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.anedvd_moe_abi_version() == 4
+    assert lib.anedvd_moe_abi_version() == 5
 
 
 def test_open_without_a_device_fails_cleanly():

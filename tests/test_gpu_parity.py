@@ -478,6 +478,43 @@ def test_forward_grouped_small_groups(ctx, types):
     assert st["small_groups"] == sum(1 for n in SMALL_SIZES if n <= 16)
 
 
+def test_route_counts_match_the_routing(ctx):
+    """Engine.route_counts through the drop-in (engine.zig:726-731, 1190-1195): after
+    a forward call the layer's per-expert choices of that call are added to the
+    caller's counts, k per token, and the call's tokens to route_tokens.  Checked
+    against the oracle's routing (the router GEMV of the call, bit-exact), over two
+    calls (host and device entry points) that accumulate, on a layer with merged
+    shared pieces (not counted), and refused for a layer whose call was not the last."""
+    spec = W.TINY_Q8_0
+    L = synth.make_layer(spec, seed=5)
+    layer = moe.MoeLayer(ctx, spec, L)
+    h = synth.activations(spec, 16, seed=5)
+    _, _, oidx = O.OracleLayer(spec, L).route(h, 16)
+    want = np.bincount(oidx.ravel(), minlength=spec.n_experts).astype(np.uint32)
+    layer.forward(h)
+    counts, n = layer.route_counts()
+    assert np.array_equal(counts, want) and n == 16
+    d_h, d_out = ctx.to_device(h), ctx.alloc(16 * spec.hidden * 4)
+    layer.forward_device(d_h, 16, None, d_out)
+    counts, n = layer.route_counts(counts)
+    assert np.array_equal(counts, 2 * want) and n == 16
+    for p in (d_h, d_out):
+        ctx.free(p)
+    spec2 = SMALL_SHARED[0]  # the shared expert merged as pieces after the routed experts
+    lg = _logits_for_groups(SMALL_SIZES, seed=41)
+    L2 = synth.make_layer(spec2, seed=41)
+    other = moe.MoeLayer(ctx, spec2, L2)
+    other.forward(synth.activations(spec2, lg.shape[0], seed=41), lg)
+    c2, n2 = other.route_counts()
+    assert np.array_equal(c2, np.array(SMALL_SIZES, dtype=np.uint32)) and n2 == lg.shape[0]
+    before = counts.copy()
+    with pytest.raises(moe.MoeError) as ei:
+        layer.route_counts(counts)  # the last call on the context was the other layer's
+    assert ei.value.name == "InvalidArgument" and np.array_equal(counts, before)
+    other.free()
+    layer.free()
+
+
 @pytest.mark.parametrize("spec", SMALL_SHARED, ids=lambda s: s.name)
 def test_forward_small_groups_with_shared_expert(ctx, spec):
     """Small groups beside a shared expert merged as pieces (large groups of their

@@ -4,8 +4,7 @@ two calls in a row on each layer, the second smaller than the first (the static
 scratch keeps the first call's contents), on the decode kernels, the grouped
 GEMM (with Zipf routing also its groups of a few tokens, run in the grouped
 launches) and a separately run shared expert (the context's second stream); and a
-call whose scratch
-exceeds the array is refused."""
+call whose scratch exceeds the array is refused."""
 import dataclasses
 import re
 
