@@ -340,18 +340,16 @@ __device__ inline void route_token(const float (&v)[4], int t, int E, int k, int
 // workgroup of NTH threads:
 //   1. per-expert counts (LDS atomics; order-free), then an exclusive scan over
 //      experts gives offsets[E+1] and the ascending list of active experts;
-//   2. entries are ranked within their expert through a bitmap: each entry sets
-//      bit (entry - chunk start) of its expert's row; the count of earlier
-//      entries of the same expert before a word, plus the popcount of the lower
-//      bits of the entry's own word, is its rank.  When there are no more
-//      entries than threads and E rows of ceil(P/32) words fit in LDS, one pass
-//      does it all (row prefixes per expert, three barriers).  Larger calls up to
-//      16384 entries rank by segments instead (dispatch_segments: no atomics, the
-//      ids loaded once); beyond that the entries go in chunks of C, and a
-//      block-wide scan of the popcounts of the flattened bitmap gives the counts.
-//      (launch_dispatch sends calls of more than kDispBlock entries to
-//      k_dispatch_multi, one workgroup per block of entries; the routed-and-
-//      dispatched launch takes at most 16 tokens.)
+//   2. entries are ranked within their expert.  When E rows of ceil(P/32) bitmap
+//      words fit in LDS, through the bitmap: each entry sets bit (entry) of its
+//      expert's row; the count of earlier entries of the same expert before a
+//      word, plus the popcount of the lower bits of the entry's own word, is its
+//      rank, and one pass does it all (row prefixes per expert, three barriers).
+//      Otherwise (more than 128 experts and more than 512 entries) by segments
+//      (dispatch_segments: no atomics, the ids loaded once).  A workgroup takes at
+//      most NTH = kDispBlock entries: launch_dispatch sends larger calls to
+//      k_dispatch_multi, one workgroup per block of entries, and the routed-and-
+//      dispatched launch takes at most 16 tokens.
 // Outputs: offsets[E+1]; rows/slots[T*k] grouped by expert, tokens ascending;
 // inv[t*k+s] = position of (t, s) or -1 for an expert id >= E; active[0..n) =
 // experts with tokens, ascending; meta[0] = n, meta[1] = largest group,
@@ -374,7 +372,6 @@ struct DispLds {
         };
         int32_t perm[2 * kDispWords + 1];  // dispatch_segments: the entry at each position
     };
-    int32_t wsum[16];
     int32_t bad;
 };
 
@@ -664,75 +661,10 @@ __device__ __forceinline__ void dispatch_block(const uint32_t *__restrict__ idx,
         }
         return;
     }
-    if (P <= (NTH / 64) * 64 * kSegBatches) {
-        dispatch_segments<NTH>(idx, P, k, E, offsets, rows, slots, inv, active, meta, chunks, chunk, n_routed, lo, s);
-        return;
-    }
-    for (int e = tid; e < E; e += NTH) {
-        s.cnt[e] = 0;
-        s.base[e] = 0;
-    }
-    if (tid == 0) s.bad = 0;
-    __syncthreads();
-    int bad = 0;
-    for (int i = tid; i < P; i += NTH) {
-        const uint32_t e = idx[i];
-        if (e < (uint32_t)E) atomicAdd(&s.cnt[e], 1);
-        else bad++;
-    }
-    if (bad) atomicAdd(&s.bad, bad);
-    __syncthreads();
-    if (wv == 0) dispatch_offsets(E, lane, offsets, active, meta, chunks, chunk, n_routed, lo, s);
-    // bitmap words per expert per chunk of entries
-    const int W = max(1, kDispWords / E);
-    const int C = 32 * W, NW = W * E;
-    const int per = (NW + NTH - 1) / NTH;  // words scanned per thread
-    for (int c0 = 0; c0 < P; c0 += C) {
-        const int c1 = min(P, c0 + C);
-        for (int w = tid; w < NW; w += NTH) s.bits[w] = 0;
-        __syncthreads();
-        for (int i = c0 + tid; i < c1; i += NTH) {
-            const uint32_t e = idx[i];
-            if (e < (uint32_t)E) atomicOr(&s.bits[e * W + ((i - c0) >> 5)], 1u << ((i - c0) & 31));
-        }
-        __syncthreads();
-        // exclusive scan of popcounts over the flattened bitmap
-        int loc = 0;
-        for (int q = 0; q < per; q++) {
-            const int w = tid * per + q;
-            if (w < NW) loc += __popc(s.bits[w]);
-        }
-        const int incl = wave_incl_scan(loc, lane);
-        if (lane == 63) s.wsum[wv] = incl;
-        __syncthreads();
-        int run = incl - loc;
-        for (int q = 0; q < wv; q++) run += s.wsum[q];
-        for (int q = 0; q < per; q++) {
-            const int w = tid * per + q;
-            if (w < NW) {
-                s.pre[w] = run;
-                run += __popc(s.bits[w]);
-            }
-        }
-        if (tid == NTH - 1) s.pre[NW] = run;
-        __syncthreads();
-        for (int i = c0 + tid; i < c1; i += NTH) {
-            const uint32_t e = idx[i];
-            if (e >= (uint32_t)E) {
-                inv[i] = -1;
-                continue;
-            }
-            const int r = i - c0, w = e * W + (r >> 5);
-            const int pos = s.off[e] + s.base[e] + (s.pre[w] - s.pre[e * W]) +
-                            __popc(s.bits[w] & ((1u << (r & 31)) - 1u));
-            rows[pos] = i / k;
-            slots[pos] = i % k;
-            inv[i] = pos;
-        }
-        __syncthreads();
-        for (int e = tid; e < E; e += NTH) s.base[e] += s.pre[(e + 1) * W] - s.pre[e * W];
-        __syncthreads();
-    }
+    // larger workgroup calls (P <= kDispBlock entries: launch_dispatch sends more to
+    // k_dispatch_multi; the fused route + dispatch takes at most 16 tokens) rank by segments
+    static_assert((NTH / 64) * 64 * kSegBatches >= NTH, "the segments take every entry a workgroup is given");
+    dispatch_segments<NTH>(idx, P, k, E, offsets, rows, slots, inv, active, meta, chunks, chunk, n_routed, lo, s);
 }
 
 // --------------------------------------------------- activation conversion

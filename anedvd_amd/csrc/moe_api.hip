@@ -449,7 +449,10 @@ int anedvd_moe_open(int device, anedvd_moe_ctx **out)
         return ANEDVD_E_NO_DEVICE;
     }
     ANEDVD_HIP(hipSetDevice(device));
-    ANEDVD_TRY(scratch_setup(device));  // this device's no-allocation scratch, once per device
+    // This device's no-allocation scratch, looked up once per device.  A failure
+    // here only concerns anedvd_moe_layer_forward_device_noalloc, which looks again
+    // and reports it; every other entry point works without the array.
+    (void)scratch_setup(device);
     anedvd_moe_ctx *c = new anedvd_moe_ctx();
     c->device = device;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
@@ -1059,9 +1062,11 @@ int anedvd_moe_layer_forward_device_noalloc(anedvd_moe_layer *L, const float *d_
         return ANEDVD_E_INVALID_ARG;
     }
     uint8_t *base = (uint8_t *)scratch_of(L->ctx->device);
-    if (!base) {
-        set_error("layer_forward_device_noalloc: no scratch for device %d", L->ctx->device);
-        return ANEDVD_E_NO_DEVICE;
+    if (!base) {  // the lookup at open failed: once more here (no allocation), reporting why
+        ANEDVD_HIP(hipSetDevice(L->ctx->device));
+        const int rc = scratch_setup(L->ctx->device);
+        if (rc != ANEDVD_OK) return rc == ANEDVD_E_HIP ? ANEDVD_E_NO_DEVICE : rc;
+        base = (uint8_t *)scratch_of(L->ctx->device);
     }
     Fwd f;
     fwd_layout(L, (int)T, ks, &f, base, false);

@@ -151,12 +151,15 @@ def test_moe_route_special_values(ctx, E, reps):
             assert np.array_equal(bits(p[t]), bits(op)), (t, k, norm)
 
 
-@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (16, 8, 2), (64, 128, 8), (512, 128, 8), (2048, 8, 2), (1024, 64, 6),
-                                   (1000, 256, 16), (4096, 128, 8)])
+@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (16, 8, 2), (64, 128, 8), (128, 128, 8), (96, 256, 8), (128, 256, 8),
+                                   (512, 128, 8), (2048, 8, 2), (1024, 64, 6), (1000, 256, 16), (4096, 128, 8)])
 def test_dispatch_bit_exact(ctx, T, E, k):
-    """Stable counting sort, against the oracle: the one-pass bitmap (decode sizes),
-    the per-wavefront segments (up to 16384 entries; 512x8 of 128, 1024x6 of 64,
-    1000x16 of 256) and the chunked bitmap beyond (4096x8 of 128)."""
+    """Stable counting sort, against the oracle, on every path: up to 1024 entries
+    one workgroup ranks them, with the one-pass bitmap while E rows of ceil(P/32)
+    words fit in LDS (64x8 and 128x8 of 128) and by per-wavefront segments beyond
+    (96x8 and 128x8 of 256: a 128-token prefill chunk of a 256-expert model); larger
+    calls go to k_dispatch_multi, one workgroup per 1024-entry block (512x8 of 128,
+    2048x2 of 8, 1024x6 of 64, 1000x16 of 256, 4096x8 of 128)."""
     lg = synth.normal(11, T, T * E).astype(np.float32).reshape(T, E)
     idx = np.stack([O.moe_route(lg[t], k, True)[1] for t in range(T)])
     got = ctx.dispatch(idx, T, k, E)
@@ -171,6 +174,22 @@ def test_dispatch_rejects_bad_expert_ids(ctx, T, k, E):
     idx[T // 2, k - 1] = E + 1
     with pytest.raises(moe.MoeError):
         ctx.dispatch(idx, T, k, E)
+
+
+def test_forward_256_experts_segment_dispatch(ctx):
+    """A whole forward call whose dispatch ranks by segments (256 experts, top-8,
+    a 128-token chunk: 1024 entries, 256 rows of 32 bitmap words do not fit in LDS),
+    against the oracle."""
+    spec = dataclasses.replace(W.QWEN3_30B_A3B_Q8_0, name="e256-top8", hidden=256, inter=256, n_experts=256)
+    L = synth.make_layer(spec, seed=17)
+    h = synth.activations(spec, 128, seed=17)
+    layer = moe.MoeLayer(ctx, spec, L)
+    got = layer.forward(h)
+    layer.free()
+    want = O.OracleLayer(spec, L).forward(h, fast=True)
+    err = moe.rel_l2(got, want)
+    print(f"\n256 experts, 128 tokens: rel-L2 {err:.3e}, max-abs {np.abs(got - want).max():.3e}")
+    assert err <= REL_L2_TOL
 
 
 @pytest.mark.parametrize("spec,T", [(W.TINY_Q8_0, 16), (W.QWEN3_30B_A3B_Q8_0, 64)])

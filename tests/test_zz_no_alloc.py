@@ -4,7 +4,8 @@ two calls in a row on each layer, the second smaller than the first (the static
 scratch keeps the first call's contents), on the decode kernels, the grouped
 GEMM (with Zipf routing also its groups of a few tokens, run in the grouped
 launches) and a separately run shared expert (the context's second stream); and a
-call whose scratch exceeds the array is refused."""
+call whose scratch exceeds the array is refused; the no-allocation call also runs
+first on a fresh context, before its workspace ever grows."""
 import dataclasses
 import re
 
@@ -57,6 +58,27 @@ def test_noalloc_forward_matches_forward_device(ctx, spec, sizes, routing):
         got = run(ctx, layer, spec, T, 30 + i, noalloc=True, routing=routing)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (spec.name, T, routing)
     layer.free()
+
+
+def test_noalloc_first_on_a_fresh_context():
+    """The no-allocation call made first on a context whose workspace was never grown
+    (a call that fell back to the context's workspace would find none), then the
+    allocating call on the same inputs: the same bits."""
+    spec = W.QWEN3_30B_A3B_Q8_0
+    c = moe.MoeContext(0)
+    layer = moe.MoeLayer(c, spec, synth.make_layer(spec, seed=4))
+    T = 32
+    h = synth.activations(spec, T, seed=4)
+    d_h, d_out = c.to_device(h), c.alloc(T * spec.hidden * 4)
+    layer.forward_device_noalloc(d_h, T, None, d_out)  # router GEMV in the call as well
+    got = c.from_device(d_out, (T, spec.hidden), np.float32)
+    layer.forward_device(d_h, T, None, d_out)
+    want = c.from_device(d_out, (T, spec.hidden), np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for p in (d_h, d_out):
+        c.free(p)
+    layer.free()
+    c.close()
 
 
 def test_noalloc_refuses_calls_beyond_its_scratch(ctx):
