@@ -383,7 +383,7 @@ struct PfArgs {
     int kk;       // slots per token row of ypart
     int sub;      // workgroups per work-list chunk: d.chunk / (16 MT)
     int ks;       // down: K shares (planes of ypart)
-    int contig;   // pf_item's contiguous order
+    int contig;   // pf_item's order: 0 round robin, 1 contiguous XCD ranges, 2 rows split over the XCDs
     int nsmall;   // capacity of the small groups' list (d.chunks_s): workgroups per row group after the grouped ones
 };
 
@@ -400,9 +400,19 @@ struct PfArgs {
 // Otherwise work items go round robin, which spreads unequal groups evenly over
 // the XCDs (contiguous ranges measured 23 % slower on the Zipf-routed Qwen3
 // 512-token prefill).
-__device__ inline void pf_item(const Dispatch &d, int sub, int b, int nw8, int contig, int &w, int &rest)
+// With contig 2 (contiguous order whose R row groups -- times K shares -- divide
+// by 8) the rows are split over the XCDs instead: XCD x takes rest values
+// [x R/8, (x + 1) R/8) of every work item, item-major, so every XCD gets the same
+// work however unequal the experts' groups are, each weight row is still read by
+// one XCD (the chunks of an expert, consecutive in the list, share it in that L2),
+// and each chunk's activations are read by all 8 at about the same time.
+__device__ inline void pf_item(const Dispatch &d, int sub, int b, int nw8, int contig, int R, int &w, int &rest)
 {
-    if (contig) {
+    if (contig == 2) {
+        const int rx = R >> 3, x = b & 7, j = b >> 3;
+        w = j / rx;
+        rest = x * rx + j % rx;
+    } else if (contig) {
         const int per = nw8 >> 3, x = b & 7, j = b >> 3;
         rest = j / per;
         if (sub == 1 && d.xper == per) {  // the dispatch's XCD ranges: whole experts where they fit
@@ -419,6 +429,12 @@ __device__ inline void pf_item(const Dispatch &d, int sub, int b, int nw8, int c
 }
 
 __host__ __device__ inline int pf_nw8(int nw) { return (nw + 7) & ~7; }
+
+// Split the rows over the XCDs (pf_item's contig 2) where a contiguous order's
+// row groups allow it.
+#ifndef ANEDVD_PF_RSPLIT
+#define ANEDVD_PF_RSPLIT 1
+#endif
 
 // Work item w of the grid's nchunk * sub: part w % sub (16 MT tokens) of the
 // work-list chunk w / sub.  False past the list's end or the chunk's tokens.
@@ -557,7 +573,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
             return;
         }
     }
-    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, w, rbg);
+    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, a.I / (2 * kRowBlock), w, rbg);
     if (w >= nw || !pf_chunk<MT>(a.d, w, a.sub, e, p0, nt)) return;  // uniform over the workgroup
     const int wv = wave_id(), lane = threadIdx.x & 63;
     const int t0 = 2 * (wv & 1), rb = 2 * rbg + (wv >> 1);
@@ -670,7 +686,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_dn_waves
             return;
         }
     }
-    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, w, rest);
+    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, a.H / (4 * kRowBlock) * a.ks, w, rest);
     if (w >= nw || !pf_chunk<MT>(a.d, w, a.sub, e, p0, nt)) return;
     const int rbg = rest / a.ks, kq = rest - rbg * a.ks;
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
@@ -849,7 +865,8 @@ int launch_grouped_gateup(const QMat &gate, const QMat &up, const ActQ &x, int H
     a.nchunk = nchunk;
     a.use_gelu = use_gelu;
     a.ks = 1;
-    a.contig = contig;
+    // rows split over the XCDs: Mixtral 2048 tokens' gate/up 928-950 -> 906-917 us
+    a.contig = contig && ANEDVD_PF_RSPLIT && (I / (2 * kRowBlock)) % 8 == 0 ? 2 : contig;
     a.nsmall = nsmall;
     if (!(a.sub = pf_sub(d, mt))) return ANEDVD_E_INVALID_ARG;
     return launch_pf_type(gate.type, a, mt, true, st);
@@ -873,7 +890,7 @@ int launch_grouped_down(const QMat &down, const ActQ &act, int H, int I, const D
     a.P = P;
     a.nchunk = nchunk;
     a.ks = ks;
-    a.contig = contig;
+    a.contig = contig;  // (split rows: Mixtral 2048 tokens' down 605-609 -> 629-633 us)
     a.nsmall = nsmall;
     if (!(a.sub = pf_sub(d, mt))) return ANEDVD_E_INVALID_ARG;
     return launch_pf_type(down.type, a, mt, false, st);
