@@ -434,7 +434,7 @@ def main():
     roofline = {"bound": "hbm", "kernel": "k_mm_gateup<MQ8_0> (fused Q8_0 dequant + gate/up + SwiGLU on MFMA)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": read_traffic("pmc_k_mm_gateup_q8_0_decode_b64.md"),
+                "traffic": read_traffic("pmc_k_mm_q8_0_decode_b1_b8_b32_b64.md"),
                 "bytes_per_launch": gu_bytes, "avg_launch_ms": gu_ms}
     for l in layers:
         l.free()
