@@ -155,6 +155,28 @@ __device__ inline void x_barrier()
 #define ANEDVD_PF_DMA_WD 2
 #endif
 
+// B operands one half-step ahead (decoders whose scales change every step, kSpu
+// 1): a step's MFMAs of block j = 0 run while the wavefront dequantises block 1,
+// and those of block 1 while it dequantises the next step's block 0, so the
+// dequantising VALU work issues in the shadow of the wavefront's own MFMAs
+// instead of before them.  Weights then go three steps ahead: the compiler's wait
+// for the next step's weights (issued three steps earlier) only covers loads at
+// least a step old.
+//
+// Taken for Q4_0 at 128-token workgroups (Mixtral 2048 tokens, one box, A/B:
+// gate/up 910-928 -> 883-887 us, down 622-642 -> 602-609 us; 244 and 256 VGPRs,
+// still two wavefronts per SIMD).  Q8_0's larger weight slots would take its
+// 128-token down kernel to 289 VGPRs (one wavefront per SIMD) and its gate/up
+// kernel is at 256 already.
+#ifndef ANEDVD_PF_PIPE
+#define ANEDVD_PF_PIPE 1
+#endif
+template <class F, int MT>
+constexpr bool pf_pipe()
+{
+    return ANEDVD_PF_PIPE && MT == 8 && std::is_same<F, FQ4_0>::value;
+}
+
 // pf_loop with the activations in the direct-to-LDS ring (steps [s0w, s0w + steps)
 // of the weights; the stager's offsets already point at step s0w).  Per step s the
 // wavefront issues the weight loads of step s + D, then the activation loads of
@@ -170,8 +192,10 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int 
     constexpr int U = 4, DA = kXDepth;
     static_assert(U % F::kSpu == 0, "a scale unit must fit an unrolled block");
     // (larger weight slots stay one step ahead: two more of them would not fit)
+    constexpr bool kP = pf_pipe<F, MT>();
+    static_assert(!kP || F::kSpu == 1, "B operands ahead only where every step has its own scales");
     constexpr int DW = sizeof(typename F::Raw) <= X::kRawCap ? ANEDVD_PF_DMA_WD : 1;
-    constexpr int D = F::kDepth > DW ? F::kDepth : DW;
+    constexpr int D = kP ? 3 : F::kDepth > DW ? F::kDepth : DW;
     constexpr int R = D == 1 ? 2 : 4;
     static_assert(D >= 1 && D <= 3, "at most three steps ahead");
     const int n = lane & 15, g = lane >> 4;
@@ -193,6 +217,11 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int 
     x_barrier();
     // the lane's operand offsets in a slot (halves): row n of a token tile, piece 2 g + j
     const int ao0 = n * 64 + (((2 * g) ^ x_sw(n)) << 3), ao1 = n * 64 + (((2 * g + 1) ^ x_sw(n)) << 3);
+    half8 bc[kPfTiles], bn[kPfTiles];  // with kP: block 0 of the current step, block 1
+    if constexpr (kP) {
+#pragma unroll
+        for (int tt = 0; tt < kPfTiles; tt++) bc[tt] = F::bop(w[0], st, 0, tt, 0, lane);
+    }
     // Step s = s0 + k of an unrolled block (k a constant).  With kPeel, the blocks
     // whose steps all lie DA or more before the end (kTail false) issue every
     // prefetch unguarded with constant wait counts, and only the remaining blocks
@@ -210,6 +239,41 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int 
         const int ss = k % F::kSpu;
         const half_t *a = slot(k);
         F::begin(w[k % R], st, ss, lane);
+        if constexpr (kP) {
+            // block 0 against bc while block 1 is dequantised into bn, then block 1
+            // against bn while the next step's block 0 is dequantised into bc
+            // (tile t's operand after token tile group mt = (t + 1) G - 1, G = max(MTL / 4, 1))
+            constexpr int G = MTL >= 2 * kPfTiles ? MTL / kPfTiles : 1;
+            const bool nxt = !kTail || s + 1 < steps;  // uniform
+            // Each token tile's A fragment is read two groups ahead of its MFMAs
+            // (fragment i: tile i % MTL of block i / MTL); scheduling barriers keep
+            // every group's reads, MFMAs and dequantisation in their own region, so
+            // the reads stay ahead and the VALU work shares a region with MFMAs.
+            auto afrag = [&](int i) { return *(const half8 *)(a + (i % MTL) * 16 * 64 + (i < MTL ? ao0 : ao1)); };
+            half8 p0 = afrag(0), p1 = afrag(1);
+#pragma unroll
+            for (int i = 0; i < 2 * MTL; i++) {
+                const int j = i / MTL, mt = i % MTL;
+                const half8 cur = p0;
+                p0 = p1;
+                if (i + 2 < 2 * MTL) p1 = afrag(i + 2);
+#pragma unroll
+                for (int tt = 0; tt < kPfTiles; tt++)
+                    acc[tt][mt] = mfma(cur, j ? bn[tt] : bc[tt], acc[tt][mt]);
+                if (mt % G == G - 1 && mt / G < kPfTiles) {
+                    if (j == 0) bn[mt / G] = F::bop(w[k % R], st, ss, mt / G, 1, lane);
+                    else if (nxt) bc[mt / G] = F::bop(w[(k + 1) % R], st, 0, mt / G, 0, lane);
+                }
+                if (mt == MTL - 1) {  // operands the groups did not reach (MTL < 4)
+#pragma unroll
+                    for (int tt = MTL / G; tt < kPfTiles; tt++) {
+                        if (j == 0) bn[tt] = F::bop(w[k % R], st, ss, tt, 1, lane);
+                        else if (nxt) bc[tt] = F::bop(w[(k + 1) % R], st, 0, tt, 0, lane);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
         half8 av[2][MT];
         if constexpr (F::kHoistA) {
 #pragma unroll
@@ -229,6 +293,7 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int 
 #pragma unroll
                 for (int tt = 0; tt < kPfTiles; tt++) acc[tt][mt] = mfma(av[j][mt], b[tt], acc[tt][mt]);
             }
+        }
         }
         if constexpr (!kTail) {
             x_wait<F, X>(2);
@@ -784,7 +849,9 @@ static int pf_sub(const Dispatch &d, int mt)
     return d.chunk / (16 * mt);
 }
 
-template <class F, int MT>
+// G decodes the gate/up weights, D the down weights (the same format, read the
+// way each kernel holds it).
+template <class G, class D, int MT>
 static int launch_pf(const PfArgs &a, bool gateup, hipStream_t st)
 {
     if (a.nsmall && (MT != 4 || a.ks != 1 || !a.d.chunks_s)) {
@@ -793,10 +860,10 @@ static int launch_pf(const PfArgs &a, bool gateup, hipStream_t st)
     }
     if (gateup) {
         const size_t wgs = ((size_t)pf_nw8(a.nchunk * a.sub) + a.nsmall) * (a.I / (2 * kRowBlock));
-        hipLaunchKernelGGL((k_pf_gateup<F, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_pf_gateup<G, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     } else {
         const size_t wgs = ((size_t)pf_nw8(a.nchunk * a.sub) * a.ks + a.nsmall) * (a.H / (4 * kRowBlock));
-        hipLaunchKernelGGL((k_pf_down<F, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_pf_down<D, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     }
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
@@ -805,12 +872,12 @@ static int launch_pf(const PfArgs &a, bool gateup, hipStream_t st)
 // 64-token chunks (mt = 4), or 128-token ones (mt = 8) for the decoders that keep
 // two wavefronts per SIMD with twice the accumulators: Q8_0, Q4_0, F16 and the
 // other 32-element formats (the super-block formats would drop to one).
-template <class F, bool WIDE>
+template <class G, class D, bool WIDE>
 static int launch_pf_mt(const PfArgs &a, int mt, bool gateup, hipStream_t st)
 {
-    if (mt == 4) return launch_pf<F, 4>(a, gateup, st);
+    if (mt == 4) return launch_pf<G, D, 4>(a, gateup, st);
     if constexpr (WIDE)
-        if (mt == 8) return launch_pf<F, 8>(a, gateup, st);
+        if (mt == 8) return launch_pf<G, D, 8>(a, gateup, st);
     set_error("grouped GEMM: no %d-token chunk kernel for this type", 16 * mt);
     return ANEDVD_E_INVALID_ARG;
 }
@@ -828,18 +895,17 @@ static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStr
 {
     switch (type) {
     case ANEDVD_Q8_0:
-    case ANEDVD_Q8_1: return launch_pf_mt<FQ8_0, true>(a, mt, gateup, st);  // one tile layout
-    case ANEDVD_F16: return launch_pf_mt<FF16, true>(a, mt, gateup, st);
-    case ANEDVD_Q4_0: return launch_pf_mt<FQ4_0, true>(a, mt, gateup, st);
-    case ANEDVD_Q4_1: return launch_pf_mt<FQ4_1, true>(a, mt, gateup, st);
-    case ANEDVD_Q5_0: return launch_pf_mt<FQ5_0, true>(a, mt, gateup, st);
-    case ANEDVD_Q5_1: return launch_pf_mt<FQ5_1, true>(a, mt, gateup, st);
-    case ANEDVD_Q2_K: return launch_pf_mt<FQ2_K, false>(a, mt, gateup, st);
-    case ANEDVD_Q3_K: return launch_pf_mt<FQ3_K, false>(a, mt, gateup, st);
-    case ANEDVD_Q4_K: return launch_pf_mt<FQ4_K, false>(a, mt, gateup, st);
-    case ANEDVD_Q5_K: return launch_pf_mt<FQ5_K, false>(a, mt, gateup, st);
-    case ANEDVD_Q6_K:
-        return gateup ? launch_pf_mt<FQ6_K, false>(a, mt, gateup, st) : launch_pf_mt<FQ6_KDown, false>(a, mt, gateup, st);
+    case ANEDVD_Q8_1: return launch_pf_mt<FQ8_0, FQ8_0, true>(a, mt, gateup, st);  // one tile layout
+    case ANEDVD_F16: return launch_pf_mt<FF16, FF16, true>(a, mt, gateup, st);
+    case ANEDVD_Q4_0: return launch_pf_mt<FQ4_0, FQ4_0, true>(a, mt, gateup, st);
+    case ANEDVD_Q4_1: return launch_pf_mt<FQ4_1, FQ4_1, true>(a, mt, gateup, st);
+    case ANEDVD_Q5_0: return launch_pf_mt<FQ5_0, FQ5_0, true>(a, mt, gateup, st);
+    case ANEDVD_Q5_1: return launch_pf_mt<FQ5_1, FQ5_1, true>(a, mt, gateup, st);
+    case ANEDVD_Q2_K: return launch_pf_mt<FQ2_K, FQ2_K, false>(a, mt, gateup, st);
+    case ANEDVD_Q3_K: return launch_pf_mt<FQ3_K, FQ3_K, false>(a, mt, gateup, st);
+    case ANEDVD_Q4_K: return launch_pf_mt<FQ4_K, FQ4_K, false>(a, mt, gateup, st);
+    case ANEDVD_Q5_K: return launch_pf_mt<FQ5_K, FQ5_K, false>(a, mt, gateup, st);
+    case ANEDVD_Q6_K: return launch_pf_mt<FQ6_K, FQ6_KDown, false>(a, mt, gateup, st);
     default:
         set_error("grouped GEMM: ggml type %d has no kernel", type);
         return ANEDVD_E_UNSUPPORTED_TYPE;
