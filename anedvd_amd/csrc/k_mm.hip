@@ -1064,7 +1064,7 @@ MmPlan plan_mm(int gate_type, int down_type, int H, int I, int P, int max_u, int
         const long wide_wgs = (long)((P + 127) / 128) * (I / 128);
         const bool wide = mean >= ANEDVD_PF_WIDE_MIN && wide_wgs >= 256;
         p.mt_gu = wide && grouped_wide(gate_type) ? 8 : 4;
-        p.mt_dn = wide && grouped_wide(down_type) ? 8 : 4;
+        p.mt_dn = wide && grouped_wide_down(down_type) ? 8 : 4;
         // A long down K (>= 128 steps) splits in two when that shortens the grid's
         // rounds of resident workgroups (two per CU) by 10 %: a partial last round
         // is then half as long, for one more plane for the combine to add.

@@ -77,7 +77,10 @@ template <int MT>
 struct DmaAct {
     static constexpr int kInst = MT / 2;
     static constexpr int kIssue = kInst + 1;  // the pieces, then the descales
-    static constexpr int kRawCap = MT == 8 ? 72 : 80;  // Q8_0 and Q5_1 at 128 tokens: one step (two waves per SIMD)
+    // The 80-byte slots (Q8_0, Q5_0, Q5_1) stay one step ahead: two waves per SIMD
+    // at 128 tokens, three at 64 (the Q8_0 kernel at 64 tokens: 166 VGPRs against
+    // 202 with its weights two steps ahead).
+    static constexpr int kRawCap = 72;
     rsrc_t q, ds;
     int off[kInst];     // load i: the lane's position's piece (bytes)
     int doff;           // the descale of row 8 (w kInst + j / 8) + j % 8, j = min(lane, 8 kInst - 1) (bytes)
@@ -890,6 +893,12 @@ bool grouped_wide(int type)
     default: return false;
     }
 }
+
+// The down kernel keeps 64-token workgroups for Q8_0 even where gate/up takes 128:
+// at three wavefronts per SIMD (weights one step ahead) DeepSeek-V2-Lite's
+// 1024-token down launch measured 99 us against 109-110 us at 128 tokens and two
+// (one box, A/B).
+bool grouped_wide_down(int type) { return grouped_wide(type) && type != ANEDVD_Q8_0 && type != ANEDVD_Q8_1; }
 
 static int launch_pf_type(int type, const PfArgs &a, int mt, bool gateup, hipStream_t st)
 {

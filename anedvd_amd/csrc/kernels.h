@@ -120,6 +120,7 @@ int launch_expert_down(const QMat &down, const ActQ &act, int H, int I, const Di
 // k_pf.hip -- the grouped GEMM for prefill-sized groups (chunks of 16 mt tokens)
 bool grouped_supported(int H, int I);
 bool grouped_wide(int type);  // the type has a 128-token-chunk grouped kernel
+bool grouped_wide_down(int type);  // ... and its down product takes it
 // A workgroup takes 16 mt tokens of a work-list chunk of d.chunk tokens.
 // contig: XCD-contiguous workgroup order (experts averaging two or more chunks).
 // nsmall > 0 (mt 4, K not split): the same launch also runs the groups of the

@@ -402,8 +402,9 @@ def _logits_for_groups(sizes, seed):
 def test_forward_grouped_every_live_tile_count(ctx, types):
     """Groups of 128 + r tokens, r giving a last chunk with 1 to 8 live 16-token
     tiles: the 128-token workgroups of the types that have them (Q8_0, Q4_0, F16,
-    the 32-element formats; every count 1..8) and the 64-token workgroups of the
-    others (counts 1..4, whole and empty halves of 128-token chunks)."""
+    the 32-element formats; every count 1..8; Q8_0's down product keeps 64-token
+    ones) and the 64-token workgroups of the others (counts 1..4, whole and empty
+    halves of 128-token chunks)."""
     sizes = [128 + r for r in (5, 20, 40, 60, 70, 90, 100, 121)]
     lg = _logits_for_groups(sizes, seed=23)
     spec = dataclasses.replace(W.MIXTRAL_8X7B_Q4_0, name="live-tiles", hidden=256, inter=4096,
@@ -411,8 +412,9 @@ def test_forward_grouped_every_live_tile_count(ctx, types):
     _, _, err, st = _forward_case(ctx, spec, lg.shape[0], seed=23, logits=lg)
     assert err <= REL_L2_TOL
     assert st["path"] == 1 and st["max_group"] == max(sizes)
-    wide = [t in (W.Q8_0, W.Q8_1, W.F16, W.Q4_0, W.Q4_1, W.Q5_0, W.Q5_1) for t in types]
-    assert st["chunk"] == (128 if wide[0] or wide[2] else 64)  # gate/up and down pick their widths apart
+    wide_gu = types[0] in (W.Q8_0, W.Q8_1, W.F16, W.Q4_0, W.Q4_1, W.Q5_0, W.Q5_1)
+    wide_dn = types[2] in (W.F16, W.Q4_0, W.Q4_1, W.Q5_0, W.Q5_1)
+    assert st["chunk"] == (128 if wide_gu or wide_dn else 64)  # gate/up and down pick their widths apart
 
 
 @pytest.mark.parametrize("types", [(W.Q4_0, W.Q4_0, W.Q4_0), (W.Q4_K, W.Q4_K, W.Q6_K), (W.Q8_0, W.Q8_0, W.Q5_K)],
