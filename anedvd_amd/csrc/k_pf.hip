@@ -467,7 +467,9 @@ struct PfArgs {
 // read by two L2s (gate/up fabric reads 2.13 -> 1.63 GB, 984 -> 946 us).
 // Otherwise work items go round robin, which spreads unequal groups evenly over
 // the XCDs (contiguous ranges measured 23 % slower on the Zipf-routed Qwen3
-// 512-token prefill).
+// 512-token prefill); with two work items per chunk (sub 2, nw8 then a multiple of
+// 16) the round robin deals chunks, so both halves of a chunk run on one XCD and
+// read the expert's slice through one L2.
 // With contig 2 (contiguous order whose R row groups -- times K shares -- divide
 // by 8) the rows are split over the XCDs instead: XCD x takes rest values
 // [x R/8, (x + 1) R/8) of every work item, item-major, so every XCD gets the same
@@ -490,13 +492,18 @@ __device__ inline void pf_item(const Dispatch &d, int sub, int b, int nw8, int c
         } else {
             w = x * per + j % per;
         }
+    } else if (sub == 2) {
+        const int i = b % nw8, x = i & 7, q = i >> 3;
+        w = 16 * (q >> 1) + 2 * x + (q & 1);
+        rest = b / nw8;
     } else {
         w = b % nw8;
         rest = b / nw8;
     }
 }
 
-__host__ __device__ inline int pf_nw8(int nw) { return (nw + 7) & ~7; }
+// Work items nw padded for pf_item: a multiple of 8, of 16 with two per chunk.
+__host__ __device__ inline int pf_nw8(int nw, int sub) { return sub == 2 ? (nw + 15) & ~15 : (nw + 7) & ~7; }
 
 // Split the rows over the XCDs (pf_item's contig 2) where a contiguous order's
 // row groups allow it.
@@ -635,13 +642,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_gu_waves
     int e, p0, nt, w, rbg;
     const int nw = a.nchunk * a.sub;
     if constexpr (MT == 4) {
-        const int nbig = pf_nw8(nw) * (a.I / (2 * kRowBlock));
+        const int nbig = pf_nw8(nw, a.sub) * (a.I / (2 * kRowBlock));
         if ((int)blockIdx.x >= nbig) {
             pf_small_gateup<F>(a, (int)blockIdx.x - nbig, dvs, &gmax[0][0]);
             return;
         }
     }
-    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, a.I / (2 * kRowBlock), w, rbg);
+    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw, a.sub), a.contig, a.I / (2 * kRowBlock), w, rbg);
     if (w >= nw || !pf_chunk<MT>(a.d, w, a.sub, e, p0, nt)) return;  // uniform over the workgroup
     const int wv = wave_id(), lane = threadIdx.x & 63;
     const int t0 = 2 * (wv & 1), rb = 2 * rbg + (wv >> 1);
@@ -748,13 +755,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf_dn_waves
     int e, p0, nt, w, rest;
     const int nw = a.nchunk * a.sub;
     if constexpr (MT == 4) {
-        const int nbig = pf_nw8(nw) * (a.H / (4 * kRowBlock)) * a.ks;
+        const int nbig = pf_nw8(nw, a.sub) * (a.H / (4 * kRowBlock)) * a.ks;
         if ((int)blockIdx.x >= nbig) {
             pf_small_down<F>(a, (int)blockIdx.x - nbig, ref, orow, &ref4[0][0]);
             return;
         }
     }
-    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw), a.contig, a.H / (4 * kRowBlock) * a.ks, w, rest);
+    pf_item(a.d, a.sub, (int)blockIdx.x, pf_nw8(nw, a.sub), a.contig, a.H / (4 * kRowBlock) * a.ks, w, rest);
     if (w >= nw || !pf_chunk<MT>(a.d, w, a.sub, e, p0, nt)) return;
     const int rbg = rest / a.ks, kq = rest - rbg * a.ks;
     const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
@@ -862,10 +869,10 @@ static int launch_pf(const PfArgs &a, bool gateup, hipStream_t st)
         return ANEDVD_E_INVALID_ARG;
     }
     if (gateup) {
-        const size_t wgs = ((size_t)pf_nw8(a.nchunk * a.sub) + a.nsmall) * (a.I / (2 * kRowBlock));
+        const size_t wgs = ((size_t)pf_nw8(a.nchunk * a.sub, a.sub) + a.nsmall) * (a.I / (2 * kRowBlock));
         hipLaunchKernelGGL((k_pf_gateup<G, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     } else {
-        const size_t wgs = ((size_t)pf_nw8(a.nchunk * a.sub) * a.ks + a.nsmall) * (a.H / (4 * kRowBlock));
+        const size_t wgs = ((size_t)pf_nw8(a.nchunk * a.sub, a.sub) * a.ks + a.nsmall) * (a.H / (4 * kRowBlock));
         hipLaunchKernelGGL((k_pf_down<D, MT>), dim3((unsigned)wgs), dim3(256), 0, st, a);
     }
     ANEDVD_HIP(hipGetLastError());
