@@ -15,7 +15,9 @@
 //     activations (a power of two per 64-column group) rescaled in LDS to their
 //     row's largest descale before use, so nothing is rescaled inside the K loop;
 //   - gate/up: a wavefront holds gate and up of the same 32 rows, so SiLU(g) * u
-//     and the activation format's scale form in registers.
+//     and the activation format's scale form in registers;
+//   - groups of at most 16 tokens (skewed routing) run in the same launches, one
+//     16-token tile per workgroup, their activations read straight from memory.
 #include <type_traits>
 
 #include "common.h"
