@@ -68,7 +68,9 @@ struct Tiles2 {
 
 // ------------------------------------------------------------------ decoders
 //
-// A decoder loads one step of a wavefront's four row tiles: load();
+// A decoder loads one step of a wavefront's four row tiles: load() (kUnit 1 or 0:
+// the caller knows at compile time whether step s starts a scale unit, which
+// then loads the unit's scales; -1: decided from s);
 // takes what stays valid for a whole scale unit on the unit's first step: begin();
 // and yields the f16 B operand of (tile tt, block j) at step `ss` of the unit:
 // bop().  Lane l = 16 g + n holds row n of the tile and the 8 columns 32 j + 8 g + i.
@@ -83,7 +85,7 @@ struct FF16 {
         u32x4 q[kPfTiles][2];
     };
     struct State {};
-    template <class TS>
+    template <int kUnit = -1, class TS>
     __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
         const int qo = lane_plane_off(ts.src(0), rb, s, 32);
@@ -108,7 +110,7 @@ struct FQ8_0 {
         uint32_t s[kPfTiles];
     };
     struct State {};
-    template <class TS>
+    template <int kUnit = -1, class TS>
     __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
         const int qo = lane_plane_off(ts.src(0), rb, s, 16), so = row_plane_off(ts.src(0), rb, s, 4);
@@ -136,7 +138,7 @@ struct FQ4_0 {
         uint32_t s[kPfTiles];
     };
     struct State {};
-    template <class TS>
+    template <int kUnit = -1, class TS>
     __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
         const int qo = lane_plane_off(ts.src(0), rb, s, 8), so = row_plane_off(ts.src(0), rb, s, 4);
@@ -170,7 +172,7 @@ struct FQLegacy {
         u32x2 s[kPfTiles];  // (d0 | m0 << 16, d1 | m1 << 16) with a min, else (d0 | d1 << 16, -)
     };
     struct State {};
-    template <class TS>
+    template <int kUnit = -1, class TS>
     __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
         const Planes &p = ts.src(0);
@@ -230,7 +232,7 @@ struct FQ4_K {
     struct State {
         uint32_t dm[kPfTiles][8];  // f16 d1 | f16 (-m1) << 16 per (tile, sub-block)
     };
-    template <class TS>
+    template <int kUnit = -1, class TS>
     __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
         const Planes &p = ts.src(0);
@@ -238,7 +240,7 @@ struct FQ4_K {
 #pragma unroll
         for (int tt = 0; tt < kPfTiles; tt++)
             r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kPfAux);
-        if ((s & 3) == 0) {
+        if (kUnit > 0 || (kUnit < 0 && (s & 3) == 0)) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
@@ -297,7 +299,7 @@ struct FQ5_K {
         u32x4 sc[kPfTiles];  // d, dmin, scales: loaded on a unit's first step
     };
     using State = FQ4_K::State;
-    template <class TS>
+    template <int kUnit = -1, class TS>
     __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
         const Planes &p = ts.src(0);
@@ -307,7 +309,7 @@ struct FQ5_K {
             r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kPfAux);
             r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, ho + 128 * ts.idx(tt), kPfAux);
         }
-        if ((s & 3) == 0) {
+        if (kUnit > 0 || (kUnit < 0 && (s & 3) == 0)) {
             const int so = row_plane_off(p, rb, s >> 2, 16);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++)
@@ -351,7 +353,7 @@ struct FQ23K {
     struct State {
         half_t dl[kPfTiles][8], ml[kPfTiles][8];  // [tt][2 ss + j] of the lane's sub-block 4 ss + 2 j + g / 2
     };
-    template <class TS>
+    template <int kUnit = -1, class TS>
     __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
         const Planes &p = ts.src(0);
@@ -364,7 +366,7 @@ struct FQ23K {
                 r.h[tt] = __builtin_amdgcn_raw_buffer_load_b16(ts.src(tt).h, 2 * lane, lane_plane_off(p, rb, s, 2) + 128 * ti,
                                                                kPfAux);
         }
-        if ((s & 3) == 0) {
+        if (kUnit > 0 || (kUnit < 0 && (s & 3) == 0)) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, kThree ? 2 : 4);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++) {
@@ -431,7 +433,7 @@ struct FQ6_K {
     struct State {
         uint32_t dsc[kPfTiles][4];  // f16 pairs; [tt][k / 2] half k % 2 (k = 2 ss + j): d * sc of the lane's sub-block 2 k + g / 2
     };
-    template <class TS>
+    template <int kUnit = -1, class TS>
     __device__ static inline void load(Raw &r, const TS &ts, int rb, int s, int lane)
     {
         const Planes &p = ts.src(0);
@@ -441,7 +443,7 @@ struct FQ6_K {
             r.q[tt] = __builtin_amdgcn_raw_buffer_load_b64(ts.src(tt).q, 8 * lane, qo + 512 * ts.idx(tt), kPfAux);
             r.h[tt] = __builtin_amdgcn_raw_buffer_load_b32(ts.src(tt).h, 4 * lane, ho + 256 * ts.idx(tt), kPfAux);
         }
-        if ((s & 3) == 0) {
+        if (kUnit > 0 || (kUnit < 0 && (s & 3) == 0)) {
             const int so = row_plane_off(p, rb, s >> 2, 16), dof = row_plane_off(p, rb, s >> 2, 2);
 #pragma unroll
             for (int tt = 0; tt < kPfTiles; tt++) {

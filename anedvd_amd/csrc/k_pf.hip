@@ -182,6 +182,14 @@ constexpr bool pf_pipe()
     return ANEDVD_PF_PIPE && MT == 8 && std::is_same<F, FQ4_0>::value;
 }
 
+// The decoder's kUnit for the step at offset v of a four-step block: whether it
+// starts a scale unit (kCt), or -1 to leave it to the decoder.
+template <class F, bool kCt>
+constexpr int pf_unit(int v)
+{
+    return kCt ? (int)(v % F::kSpu == 0) : -1;
+}
+
 // pf_loop with the activations in the direct-to-LDS ring (steps [s0w, s0w + steps)
 // of the weights; the stager's offsets already point at step s0w).  Per step s the
 // wavefront issues the weight loads of step s + D, then the activation loads of
@@ -198,6 +206,13 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int 
     static_assert(U % F::kSpu == 0, "a scale unit must fit an unrolled block");
     // (larger weight slots stay one step ahead: two more of them would not fit)
     constexpr bool kP = pf_pipe<F, MT>();
+    // Whether a step starts a scale unit is known here at compile time (blocks of
+    // four steps from a multiple of four).  The down kernels pass it to the decoder,
+    // so only the slot that holds a unit's first step carries its scales: the Q6_K
+    // kernel's 52-byte-per-lane spill went, and the Qwen3 Q4_K_M 512-token down
+    // launch took 53-56 us against 63.  The gate/up kernels leave it to the decoder
+    // (the Q4_K kernel spilled more with it: 77 against 69 us).
+    constexpr bool kCtUnit = !std::is_same<X, DmaX<MT>>::value;
     static_assert(!kP || F::kSpu == 1, "B operands ahead only where every step has its own scales");
     constexpr int DW = sizeof(typename F::Raw) <= X::kRawCap ? ANEDVD_PF_DMA_WD : 1;
     constexpr int D = kP ? 3 : F::kDepth > DW ? F::kDepth : DW;
@@ -209,10 +224,23 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int 
     auto slot = [&](int b) { return b == 0 ? xs0 : b == 1 ? xs1 : b == 2 ? xs2 : xs3; };  // b a constant
     typename F::Raw w[R];
     typename F::State st;
+    // the steady state's order: weights of v + D, activations of v + DA (v = -DA .. -1)
+    if constexpr (kCtUnit) {
+        auto pro = [&](auto ic) {
+            constexpr int v = decltype(ic)::value - DA;
+            if constexpr (v + D >= 0) F::template load<pf_unit<F, true>(v + D)>(w[(v + D) % R], W, rb, ws(v + D), lane);
+            if (v + DA < steps) x.issue(slot((v + DA) & 3), v + DA, (v + DA) & 3);
+        };
+        static_assert(DA == 3, "the prologue issues three steps");
+        pro(std::integral_constant<int, 0>{});
+        pro(std::integral_constant<int, 1>{});
+        pro(std::integral_constant<int, 2>{});
+    } else {
 #pragma unroll
-    for (int v = -DA; v < 0; v++) {  // the steady state's order: weights of v + D, activations of v + DA
-        if (v + D >= 0) F::load(w[(v + D) % R], W, rb, ws(v + D), lane);
-        if (v + DA < steps) x.issue(slot((v + DA) & 3), v + DA, (v + DA) & 3);
+        for (int v = -DA; v < 0; v++) {
+            if (v + D >= 0) F::load(w[(v + D) % R], W, rb, ws(v + D), lane);
+            if (v + DA < steps) x.issue(slot((v + DA) & 3), v + DA, (v + DA) & 3);
+        }
     }
     // step 0's activations: younger than them are the weight loads of the
     // virtual steps -2 and -1 that exist (min(D, 2) calls) and the activation
@@ -238,7 +266,7 @@ __device__ inline void pf_loop_dma(const TS &W, int rb, int s0w, int steps, int 
         constexpr int k = decltype(kc)::value;
         constexpr bool kTail = decltype(tailc)::value;
         const int s = s0 + k;
-        F::load(w[(k + D) % R], W, rb, kTail ? ws(s + D) : s0w + s + D, lane);
+        F::template load<pf_unit<F, kCtUnit>(k + D)>(w[(k + D) % R], W, rb, kTail ? ws(s + D) : s0w + s + D, lane);
         if (!kTail || s + DA < steps) x.issue(slot((k + DA) & 3), s + DA, (k + DA) & 3);
         __builtin_amdgcn_sched_barrier(0);
         const int ss = k % F::kSpu;
