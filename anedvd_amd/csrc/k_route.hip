@@ -719,6 +719,9 @@ struct RouteArgs {
     int kk;              // slots per token row of probs/idx: k routed + n_sh shared pieces
     int n_sh;            // shared expert pieces (experts E .. E+n_sh-1), written by the conversion
     const uint16_t *sh_lin;  // shared gate vector [H] f16, or null (scale 1)
+    // With `rwt` (fused route and dispatch only) the routing workgroup forms the
+    // logits itself from x: the router lane-major (rwt) and as stored (rw).
+    const uint16_t *rwt, *rw;
 };
 
 constexpr int kRouteWaves = 4;      // tokens per routing workgroup, one per wavefront
@@ -769,6 +772,51 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a)
     route_token(v, t, a.E, a.k, a.kk, a.norm, a.probs, a.idx, lane, c_exp2_tab, rows[wv]);
 }
 
+// The router logits of a few tokens inside the routing workgroup (T E 8 <= its
+// threads): the tokens' x staged in LDS as k_router stages them (in xs, the
+// dispatch's LDS, idle until the routing is done), thread (t, e, l) runs chain l of
+// (token t, expert e) -- the same adds in the same order as k_router, so the same
+// bits -- and lane 0 of each eight adds the chains in order, then the scalar tail,
+// into lg[t][e].  No second launch and no trip of the logits through memory.
+__device__ inline void router_chains(const RouteArgs &a, float (*lg)[kMaxExperts], float *xs)
+{
+    const int J = a.H >> 3, H8 = J * 8, JP = router_stride(J);  // xs: [T][8][JP]
+    for (int i = threadIdx.x; i < a.T * H8; i += kDispThreads) {
+        const int t = i / H8, c = i - t * H8;
+        xs[(t * 8 + (c & 7)) * JP + (c >> 3)] = a.x[(size_t)t * a.H + c];
+    }
+    __syncthreads();
+    const int n = a.T * a.E * 8;
+    if ((int)(threadIdx.x & ~63u) >= n) return;  // a wavefront with no chain (uniform; the caller's barrier follows)
+    const int ch = min((int)threadIdx.x, n - 1);  // lanes past the chains repeat the last (not stored)
+    const int t = ch / (a.E * 8), e = (ch >> 3) % a.E, l = ch & 7;
+    const uint16_t *wr = a.rwt + ((size_t)e * 8 + l) * J;
+    const float *xr = xs + (t * 8 + l) * JP;
+    float acc = 0.0f;
+    int j = 0;
+    if ((J & 7) == 0) {
+        // 8 j's per 16-byte load, the next one issued before this one's adds
+        const uint4 *w16 = (const uint4 *)wr;
+        uint4 cur = w16[0];
+        for (; j < J; j += 8) {
+            const uint4 nxt = w16[min(j + 8, J - 8) >> 3];
+            const uint32_t ww[4] = {cur.x, cur.y, cur.z, cur.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                acc = __fadd_rn(acc, __fmul_rn(xr[j + q], f16_bits_to_f32((uint16_t)(ww[q >> 1] >> (16 * (q & 1))))));
+            cur = nxt;
+        }
+    }
+    for (; j < J; j++) acc = __fadd_rn(acc, __fmul_rn(xr[j], f16_bits_to_f32(wr[j])));
+    float sum = __shfl(acc, (threadIdx.x & ~7), 64);
+    for (int q = 1; q < 8; q++) sum = __fadd_rn(sum, __shfl(acc, (threadIdx.x & ~7) + q, 64));
+    if ((int)threadIdx.x < n && l == 0) {
+        const uint16_t *row = a.rw + (size_t)e * a.H;
+        for (int i = H8; i < a.H; i++) sum = __fadd_rn(sum, __fmul_rn(f16_bits_to_f32(row[i]), a.x[(size_t)t * a.H + i]));
+        lg[t][e] = sum;
+    }
+}
+
 // Up to kFusedTokens tokens routed and dispatched in one launch.  Block 0's
 // wavefront w routes token w; the ids also go to LDS (the shared
 // slots' ids are fixed: E + j), and after a barrier the same workgroup dispatches
@@ -789,9 +837,15 @@ __global__ __launch_bounds__(kDispThreads) void k_route_dispatch(RouteArgs a, Di
     __shared__ __attribute__((aligned(16))) float rows[kW][kMaxExperts];
     __shared__ uint32_t ids[kFusedIds];
     __shared__ DispLds s;
+    if (a.rwt) {
+        static_assert(sizeof(DispLds) % 4 == 0 && alignof(DispLds) >= 4, "x staged in the dispatch's LDS");
+        router_chains(a, rows, reinterpret_cast<float *>(&s));
+        __syncthreads();
+    }
     if (wv < a.T) {  // T <= kW: one token per wavefront
         float v[4];
-        route_logits(a.logits, wv, a.T, a.E, lane, v);
+        if (a.rwt) route_logits(rows[wv], 0, 1, a.E, lane, v);
+        else route_logits(a.logits, wv, a.T, a.E, lane, v);
         exp_table_ready(exp_table_warm(lane));
         route_token(v, wv, a.E, a.k, a.kk, a.norm, a.probs, a.idx, lane, c_exp2_tab, rows[wv], ids);
     }
@@ -971,10 +1025,20 @@ bool route_fusable(int T, int)
     return T > 0 && T <= kFusedTokens;
 }
 
+bool route_router_fusable(int T, int E, int H)
+{
+    return route_fusable(T, E) && T * E * 8 <= kDispThreads && E <= kMaxExperts &&
+           (size_t)T * 8 * router_stride(H >> 3) * 4 <= sizeof(DispLds);
+}
+
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                               const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
-                              const SharedSlots &sh)
+                              const SharedSlots &sh, const uint16_t *d_rwt, const uint16_t *d_rw)
 {
+    if (!d_logits && (!d_rwt || !d_rw || !d_x || !route_router_fusable(T, E, H))) {
+        set_error("route: no logits, and the router cannot be fused into this call (%d tokens, %d experts)", T, E);
+        return ANEDVD_E_INVALID_ARG;
+    }
     if (!route_fusable(T, E)) {
         ANEDVD_TRY(launch_route(d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, st, sh));
         return launch_dispatch(d_idx, T, k + sh.n, E + sh.n, d, st);
@@ -989,7 +1053,11 @@ int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int no
         set_error("route: %d shared pieces need the activations and at most 64 pieces", sh.n);
         return ANEDVD_E_INVALID_ARG;
     }
-    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, 1, k + sh.n, sh.n, sh.lin};
+    RouteArgs a{d_logits, T, E, k, norm, d_probs, d_idx, d_x, H, xq, 1, k + sh.n, sh.n, sh.lin, nullptr, nullptr};
+    if (!d_logits) {
+        a.rwt = d_rwt;
+        a.rw = d_rw;
+    }
     const unsigned blocks = 1 + (d_x ? (unsigned)((T + kDispThreads / 64 - 1) / (kDispThreads / 64)) : 0u);
     hipLaunchKernelGGL(k_route_dispatch, dim3(blocks), dim3(kDispThreads), 0, st, a, d);
     ANEDVD_HIP(hipGetLastError());

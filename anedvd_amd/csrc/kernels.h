@@ -76,9 +76,14 @@ int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &
 // launch (one wavefront per token, the conversion beside it), then the
 // one-workgroup dispatch launch.
 bool route_fusable(int T, int E);
+// route_router_fusable(T, E, H): the fused launch can also form the router logits
+// (a chain per thread); then d_logits is null and d_rwt / d_rw the router
+// (lane-major, as stored), and d_x the call's activations.
+bool route_router_fusable(int T, int E, int H);
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                               const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
-                              const SharedSlots &sh = {});
+                              const SharedSlots &sh = {}, const uint16_t *d_rwt = nullptr,
+                              const uint16_t *d_rw = nullptr);
 int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st);
 
 // k_mm.hip -- expert products on MFMA

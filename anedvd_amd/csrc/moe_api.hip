@@ -335,15 +335,19 @@ int forward_device(anedvd_moe_layer *L, const float *d_h, int T, const float *d_
         if (ev) (void)hipEventRecord(ev[i], st);
     };
     mark(0);
+    // The router GEMV runs in the routing launch itself when the call is a few
+    // tokens (a chain per thread of the routing workgroup), else in its own launch.
     const float *logits = d_logits;
-    if (!logits) {
+    const bool fuse_router = !logits && route_router_fusable(T, E, H);
+    if (!logits && !fuse_router) {
         ANEDVD_TRY(launch_router(L->router_t, L->router, d_h, T, E, H, f.logits, st));
         logits = f.logits;
     }
     SharedSlots sh;
     sh.n = (int)L->n_sh;
     sh.lin = L->sgate_lin;
-    ANEDVD_TRY(launch_route_and_dispatch(logits, T, E, k, L->norm, f.probs, f.idx, d_h, H, f.xq, f.d, st, sh));
+    ANEDVD_TRY(launch_route_and_dispatch(logits, T, E, k, L->norm, f.probs, f.idx, d_h, H, f.xq, f.d, st, sh,
+                                         fuse_router ? L->router_t : nullptr, fuse_router ? L->router : nullptr));
     mark(1);
     // A shared expert that is not merged into the routed launches needs only x
     // (converted by the route launch): it runs on the context's second stream beside

@@ -499,6 +499,37 @@ def test_forward_grouped_small_groups(ctx, types):
     assert st["small_groups"] == sum(1 for n in SMALL_SIZES if n <= 16)
 
 
+ROUTER_IN_ROUTING = [
+    (dataclasses.replace(W.MIXTRAL_8X7B_Q4_0, name="mixtral-router", inter=256), (1, 2, 16)),
+    (dataclasses.replace(W.DEEPSEEK_V2_LITE_Q8_0, name="deepseek-router", inter=256, shared_inter=512), (1, 2)),
+    (dataclasses.replace(W.QWEN3_30B_A3B_Q8_0, name="qwen3-router", inter=256), (1,)),
+    (W.TINY_Q8_0, (1, 5, 16)),
+]
+
+
+@pytest.mark.parametrize("spec,Ts", ROUTER_IN_ROUTING, ids=lambda v: v.name if hasattr(v, "name") else str(v))
+def test_router_in_the_routing_launch_is_bit_exact(ctx, spec, Ts):
+    """A call of a few tokens without logits forms the router logits inside the
+    routing launch (a chain per thread, T E 8 <= 1024) instead of the router
+    GEMV launch: its output must equal, bit for bit, the same call given the
+    oracle's logits (cpu.matmulF16's order, which the router GEMV matches bit for
+    bit), so every logit bit is the same.  Shapes of Mixtral (H 4096, 8 experts),
+    DeepSeek-V2-Lite (64 experts and merged shared pieces), Qwen3 (128 experts at
+    one token) and the tiny layer (H 512: the largest T)."""
+    L = synth.make_layer(spec, seed=61)
+    layer = moe.MoeLayer(ctx, spec, L)
+    ol = O.OracleLayer(spec, L)
+    for T in Ts:
+        h = synth.activations(spec, T, seed=61 + T)
+        lg = ol.route(h, T)[0]
+        fused = layer.forward(h)
+        given = layer.forward(h, lg)
+        assert np.array_equal(bits(fused), bits(given)), T
+        err = moe.rel_l2(fused, ol.forward(h, lg, fast=True))
+        assert err <= REL_L2_TOL, (T, err)
+    layer.free()
+
+
 def test_route_counts_match_the_routing(ctx):
     """Engine.route_counts through the drop-in (engine.zig:726-731, 1190-1195): after
     a forward call the layer's per-expert choices of that call are added to the
