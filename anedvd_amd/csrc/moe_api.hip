@@ -1259,10 +1259,11 @@ int anedvd_moe_time_forward(anedvd_moe_layer *const *layers, size_t n_layers, co
     }
     if (kernel_ms && (flags & ANEDVD_TIME_EXPERT_SOLO)) {
         // The routed expert products alone: `iters` back-to-back launches of the
-        // gate/up (then the down) kernels over the rotated layers (with the small
-        // groups' launch after each grouped one, serially), reading the
+        // gate/up (then the down) kernels over the rotated layers, reading the
         // dispatch, activations and gate/up output the last call left in place (the
-        // calls above routed the same inputs).  Events bracket each loop only.
+        // calls above routed the same inputs).  Events bracket each loop only.  Then
+        // the router GEMV kernel alone (a call of a few tokens forms its logits in
+        // the routing launch instead; this times the separate kernel).
         const int H = layers[0]->H, I = layers[0]->I, P = (int)T * (int)(layers[0]->k + layers[0]->n_sh);
         hipEvent_t a = nullptr, b = nullptr;
         ANEDVD_HIP(hipEventCreate(&a));
