@@ -14,6 +14,7 @@
 #include "common.h"
 #include "expf_exact.h"
 #include "kernels.h"
+#include "mma.h"
 
 namespace anedvd {
 
@@ -32,41 +33,90 @@ __device__ inline void exp_table_ready(uint64_t warm) { asm volatile("" ::"v"(wa
 // cpu.matmulF16's order fixes, for each (token, expert), eight sequential chains:
 // chain l adds x[8j+l] * f32(w[8j+l]) for j = 0, 1, ... (multiply and add rounded
 // separately); the eight chain sums are then added l = 0..7 in order, then the
-// scalar tail i >= H8 = H & ~7.  The chains cannot be split, so the kernel gives
-// every chain its own lane and makes each lane's operands one contiguous stream:
-// the router is stored lane-major, wt[(8 e + l) J + j] = w[e][8 j + l] with
-// J = H / 8 (router_layout), read 8 j's per 16-byte load; the token's x is staged
-// in LDS the same way, xs[l JP + j] = x[8 j + l], the row stride JP (>= J, four
-// times an odd number) putting the eight chains' 16-byte reads on distinct banks.
-// Each lane runs TT tokens' chains at once (independent adds interleave), and the
-// eight lanes of an expert sit in one DPP row for the ordered sum.
+// scalar tail i >= H8 = H & ~7.  The chains cannot be split, so every chain runs
+// in one lane: lane (g, l) of a block runs chain l of EX experts (g, g + 32) for
+// TT tokens, the eight lanes of an expert in one DPP row for the ordered sum.
 //
-// Block: 256 threads = 32 experts x 8 lanes.  Grid: (ceil(E/32), ceil(T/TT)).
-__global__ void k_router_layout(const uint16_t *__restrict__ w, int E, int H, uint16_t *__restrict__ wt)
+// The router is stored once per layer as f32 (f16 -> f32 is exact, so the products
+// are the reference's, and the kernel converts nothing), interleaved so that a
+// wavefront's loads of one 8-j block are one contiguous run: experts in groups of
+// 64, and wt[((grp NB + jb) 64 + ei) 64 + 8 l + q] = w[64 grp + ei][8 (8 jb + q) + l]
+// (NB = ceil(J / 8) blocks of eight j's, J = H / 8; zero past E and past J).  A lane
+// reads its 8 j's of one block in two 16-byte loads through a buffer descriptor
+// with a scalar per-block offset.  The token's x is staged in LDS as xs[l JP + j]
+// = x[8 j + l], the row stride JP (>= J, four times an odd number) putting the
+// eight chains' 16-byte reads on distinct banks.
+//
+// What bounds it (Qwen3 512 and DeepSeek-V2-Lite 1024 tokens, 134 M products):
+// at TT = EX = 1 the 16-byte weight loads cost 4 bytes per product through the
+// L1 and the staged x 4 bytes of LDS; TT = 2 halves the first, EX = 2 the second,
+// leaving the multiply and add (2 VALU per product) as the largest term.
+__host__ __device__ inline int router_stride(int J) { return ((J + 3) / 4 | 1) * 4; }
+constexpr int kRouterGroup = 64;  // experts per layout group
+
+__host__ __device__ inline size_t router_blocks(int H) { return (size_t)(((H >> 3) + 7) / 8); }
+
+size_t router_layout_floats(int E, int H)
 {
-    const int J = H >> 3;
-    const size_t n = (size_t)E * 8 * J;
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const size_t e = i / (8 * (size_t)J), r = i % (8 * (size_t)J);
-    const int l = (int)(r / J), j = (int)(r % J);
-    wt[i] = w[e * H + 8 * (size_t)j + l];
+    return (size_t)((E + kRouterGroup - 1) / kRouterGroup) * router_blocks(H) * kRouterGroup * 64;
 }
 
-__host__ __device__ inline int router_stride(int J) { return ((J + 3) / 4 | 1) * 4; }
+__global__ void k_router_layout(const uint16_t *__restrict__ w, int E, int H, float *__restrict__ wt, size_t n)
+{
+    const int J = H >> 3, NB = (int)router_blocks(H);
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int q = (int)(i & 7), l = (int)(i >> 3) & 7;
+    const size_t r = i >> 6;  // (grp NB + jb) 64 + ei
+    const int ei = (int)(r % kRouterGroup);
+    const size_t r2 = r / kRouterGroup;
+    const int jb = (int)(r2 % NB), grp = (int)(r2 / NB);
+    const int e = kRouterGroup * grp + ei, j = 8 * jb + q;
+    wt[i] = (e < E && j < J) ? f16_bits_to_f32(w[(size_t)e * H + 8 * (size_t)j + l]) : 0.0f;
+}
 
-template <int TT>
-__global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ wt, const uint16_t *__restrict__ w,
+// Block: 256 threads = 32 lane groups x 8 chains, 32 EX experts.  Grid:
+// (ceil(E / (32 EX)), ceil(T / TT)).
+template <int TT, int EX>
+__global__ __launch_bounds__(256) void k_router(const float *__restrict__ wt, const uint16_t *__restrict__ w,
                                                 const float *__restrict__ x, int T, int E, int H,
                                                 float *__restrict__ logits)
 {
+    static_assert(EX == 1 || EX == 2, "a block's experts lie in one layout group");
     extern __shared__ float xs[];  // [TT][8][JP]
-    const int J = H >> 3, H8 = J * 8, JP = router_stride(J);
+    const int J = H >> 3, H8 = J * 8, JP = router_stride(J), NB = (int)router_blocks(H), NBF = J / 8;
     const int t0 = blockIdx.y * TT;
     const int nt = min(TT, T - t0);
+    const int e0 = blockIdx.x * 32 * EX;  // the block's first expert
+    // The block's experts: layout group e0 / 64, from expert e0 % 64 of it (0, or 32
+    // when EX = 1); a block of the group is 64 x 256 bytes.
+    const rsrc_t rs = make_rsrc(wt + ((size_t)(e0 / kRouterGroup) * NB * kRouterGroup + e0 % kRouterGroup) * 64,
+                                (size_t)NB * kRouterGroup * 256);
+    // The first 8 kWarmBlocks blocks (kWarmBlocks per XCD, workgroup b on XCD b mod 8)
+    // pull the router slice of their experts into their XCD's L2 before staging x,
+    // each a kWarmBlocks-th of it: a layer's router is cold when its call starts, and
+    // otherwise every block waits on the same misses at each 8-j block.  One dword per
+    // 128-byte line, up to kWarm lines per thread, folded after the staging (whose
+    // waits cover them) so they hold no register in the main loop.
+    constexpr int kWarm = 4, kWarmBlocks = 16;
+    uint32_t warm = 0;
+    const int lin = blockIdx.x + blockIdx.y * gridDim.x;
+    if (lin < 8 * kWarmBlocks) {
+        const int lpb = 2 * min(32 * EX, E - e0);  // lines per 8-j block
+        const int L = NB * lpb, per = (L + kWarmBlocks - 1) / kWarmBlocks, i0 = (lin / 8) * per;
+        uint32_t wv[kWarm];
+#pragma unroll
+        for (int k = 0; k < kWarm; k++) {
+            const int d = (int)threadIdx.x + 256 * k, i = i0 + d, jb = i / lpb;
+            wv[k] = d < per && i < L ? __builtin_amdgcn_raw_buffer_load_b32(rs, (i % lpb) * 128, jb * kRouterGroup * 256, 0)
+                                     : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < kWarm; k++) warm ^= wv[k];
+    }
     // Staging: kB loads per token in flight per thread before their LDS writes (one
     // load, wait and write per element measured 37 us for Mixtral's 2048 tokens).
-    constexpr int kB = 16;
+    constexpr int kB = 8;
     for (int i0 = threadIdx.x; i0 < H8; i0 += kB * blockDim.x) {
         float v[TT][kB];
 #pragma unroll
@@ -84,96 +134,134 @@ __global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ wt,
                 if (t < nt && i < H8) xs[(t * 8 + (i & 7)) * JP + (i >> 3)] = v[t][b];
             }
     }
+    asm volatile("" ::"v"(warm));
     __syncthreads();
 
-    const int l = threadIdx.x & 7;
-    const int e = blockIdx.x * 32 + (threadIdx.x >> 3);
-    // A wavefront holds experts 8w .. 8w + 7 of the block; one with none below E
+    const int l = threadIdx.x & 7, g = threadIdx.x >> 3;
+    // A wavefront holds lane groups 8w .. 8w + 7; one whose first expert is past E
     // leaves (no barrier follows): with E = 8 three of the four would otherwise run
     // every chain on a stand-in expert.
-    if (blockIdx.x * 32 + 8 * (int)(threadIdx.x >> 6) >= E) return;
-    const bool live = e < E;
-    const uint16_t *wr = wt + ((size_t)(live ? e : 0) * 8 + l) * J;
-    float acc[TT];
+    if (e0 + 8 * (int)(threadIdx.x >> 6) >= E) return;
+    const int vo = threadIdx.x * 32;
+    auto wl = [&](int jb, int m, int h) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo + 16 * h,
+                                                                                 jb * kRouterGroup * 256 + m * 8192, 0));
+    };
+    float acc[TT][EX];
 #pragma unroll
-    for (int t = 0; t < TT; t++) acc[t] = 0.0f;
-    int j = 0;
-    if (J >= 8 && (J & 7) == 0) {
-        // 8 j's per 16-byte load, the next block's load issued before this one's adds
-        // (eight blocks in flight instead measured slower: the loop is bound by its
-        // adds, eight ordered chains per (token, expert), not by the loads)
-        const uint4 *w16 = (const uint4 *)wr;
-        uint4 cur = w16[0];
-        for (; j < J; j += 8) {
-            const uint4 nxt = w16[min(j + 8, J - 8) >> 3];
-            const uint32_t ww[4] = {cur.x, cur.y, cur.z, cur.w};
-            float xv[TT][8];
+    for (int t = 0; t < TT; t++)
 #pragma unroll
-            for (int t = 0; t < TT; t++) {
-                const float4 a = *(const float4 *)&xs[(t * 8 + l) * JP + j];
-                const float4 b = *(const float4 *)&xs[(t * 8 + l) * JP + j + 4];
+        for (int m = 0; m < EX; m++) acc[t][m] = 0.0f;
+    float xv[TT][8];
+    float4 cur[EX][2];
+#pragma unroll
+    for (int m = 0; m < EX; m++) {
+        cur[m][0] = wl(0, m, 0);
+        cur[m][1] = wl(0, m, 1);
+    }
+    // x of block jb (its first nq j's) from LDS
+    auto ldx = [&](int jb, int nq) {
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const float *xr = &xs[(t * 8 + l) * JP + 8 * jb];
+            if (nq == 8) {
+                const float4 a = *(const float4 *)xr, b = *(const float4 *)(xr + 4);
                 xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
                 xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
-            }
+            } else {
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const float wv = f16_bits_to_f32((uint16_t)(ww[q >> 1] >> (16 * (q & 1))));
-#pragma unroll
-                for (int t = 0; t < TT; t++) acc[t] = __fadd_rn(acc[t], __fmul_rn(xv[t][q], wv));
+                for (int q = 0; q < 8; q++) xv[t][q] = q < nq ? xr[q] : 0.0f;
             }
-            cur = nxt;
         }
-    } else {
-        for (; j < J; j++) {
-            const float wv = f16_bits_to_f32(wr[j]);
+    };
+    // the first nq j's of the block in `cur` against xv
+    auto step = [&](int nq) {
 #pragma unroll
-            for (int t = 0; t < TT; t++) acc[t] = __fadd_rn(acc[t], __fmul_rn(xs[(t * 8 + l) * JP + j], wv));
+        for (int q = 0; q < 8; q++) {
+            if (q >= nq) break;
+#pragma unroll
+            for (int m = 0; m < EX; m++) {
+                const float4 h = cur[m][q >> 2];
+                const float wf = (q & 3) == 0 ? h.x : (q & 3) == 1 ? h.y : (q & 3) == 2 ? h.z : h.w;
+#pragma unroll
+                for (int t = 0; t < TT; t++) acc[t][m] = __fadd_rn(acc[t][m], __fmul_rn(xv[t][q], wf));
+            }
+        }
+    };
+    // Full blocks, the next block's weights loaded before this one's adds (past the
+    // last block they lie outside the descriptor's range and read 0, no request).
+    for (int jb = 0; jb < NBF; jb++) {
+        float4 nxt[EX][2];
+#pragma unroll
+        for (int m = 0; m < EX; m++) {
+            nxt[m][0] = wl(jb + 1, m, 0);
+            nxt[m][1] = wl(jb + 1, m, 1);
+        }
+        ldx(jb, 8);
+        step(8);
+#pragma unroll
+        for (int m = 0; m < EX; m++) {
+            cur[m][0] = nxt[m][0];
+            cur[m][1] = nxt[m][1];
         }
     }
+    if (NB > NBF) {  // the last block's first J - 8 NBF j's
+        ldx(NBF, J - 8 * NBF);
+        step(J - 8 * NBF);
+    }
     // Ordered lane sum: lane 0 + lane 1 + ... + lane 7, then the scalar tail.
-    const uint16_t *row = w + (size_t)(live ? e : 0) * H;
 #pragma unroll
-    for (int t = 0; t < TT; t++) {
-        float sum = __shfl(acc[t], (threadIdx.x & ~7), 64);
-        for (int q = 1; q < 8; q++) sum = __fadd_rn(sum, __shfl(acc[t], (threadIdx.x & ~7) + q, 64));
-        if (live && l == 0 && t < nt) {
-            for (int i = H8; i < H; i++)
-                sum = __fadd_rn(sum, __fmul_rn(f16_bits_to_f32(row[i]), x[(size_t)(t0 + t) * H + i]));
-            logits[(size_t)(t0 + t) * E + e] = sum;
+    for (int m = 0; m < EX; m++) {
+        const int e = e0 + 32 * m + g;
+        const bool live = e < E;
+        const uint16_t *row = w + (size_t)(live ? e : 0) * H;
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            float sum = __shfl(acc[t][m], (threadIdx.x & ~7), 64);
+            for (int q = 1; q < 8; q++) sum = __fadd_rn(sum, __shfl(acc[t][m], (threadIdx.x & ~7) + q, 64));
+            if (live && l == 0 && t < nt) {
+                for (int i = H8; i < H; i++)
+                    sum = __fadd_rn(sum, __fmul_rn(f16_bits_to_f32(row[i]), x[(size_t)(t0 + t) * H + i]));
+                logits[(size_t)(t0 + t) * E + e] = sum;
+            }
         }
     }
 }
 
-int launch_router_layout(const uint16_t *d_w, int E, int H, uint16_t *d_wt, hipStream_t st)
+int launch_router_layout(const uint16_t *d_w, int E, int H, float *d_wt, hipStream_t st)
 {
-    const size_t n = (size_t)E * (H & ~7);
+    const size_t n = router_layout_floats(E, H);
     if (!n) return ANEDVD_OK;
-    hipLaunchKernelGGL(k_router_layout, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, d_w, E, H, d_wt);
+    hipLaunchKernelGGL(k_router_layout, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, d_w, E, H, d_wt, n);
     ANEDVD_HIP(hipGetLastError());
     return ANEDVD_OK;
 }
 
-int launch_router(const uint16_t *d_wt, const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits,
+int launch_router(const float *d_wt, const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits,
                   hipStream_t st)
 {
     if (T <= 0) return ANEDVD_OK;
-    // Tokens per block: enough blocks to spread over the CUs, the staged
-    // activations within 64 KiB of LDS.
-    const dim3 block(256);
-    const int eb = (E + 31) / 32;
-    auto go = [&](auto tt) -> int {
-        constexpr int TT = decltype(tt)::value;
+    if (router_blocks(H) * kRouterGroup * 256 > (size_t)INT32_MAX) {
+        set_error("router: hidden size %d too large", H);
+        return ANEDVD_E_INVALID_ARG;
+    }
+    // Two tokens and two experts per lane once the grid still has about two
+    // wavefronts per SIMD that way (Qwen3 512 tokens, DeepSeek-V2-Lite 1024: 11.5
+    // and 11.8 us against 13.1 and 13.4 at one expert, 19.9 and 20.6 at one token
+    // and one expert); one of each below (64 tokens of 128 experts: 5.1 against
+    // 6.3 us at two tokens), and one expert for E < 64 (Mixtral's E = 8).
+    const bool big = E >= 64 && (long)T * E >= 65536;
+    auto go = [&](auto tt, auto ex) -> int {
+        constexpr int TT = decltype(tt)::value, EX = decltype(ex)::value;
         const size_t lds = (size_t)TT * 8 * router_stride(H >> 3) * 4;
         if (lds > 65536) return -1;
-        hipLaunchKernelGGL(k_router<TT>, dim3(eb, (T + TT - 1) / TT), block, lds, st, d_wt, d_w, d_x, T, E, H,
-                           d_logits);
+        hipLaunchKernelGGL((k_router<TT, EX>), dim3((E + 32 * EX - 1) / (32 * EX), (T + TT - 1) / TT), dim3(256), lds,
+                           st, d_wt, d_w, d_x, T, E, H, d_logits);
         return 0;
     };
-    const long blocks1 = (long)eb * T;
     int rc = -1;
-    if (blocks1 >= 1024) rc = go(std::integral_constant<int, 4>{});
-    if (rc && blocks1 >= 512) rc = go(std::integral_constant<int, 2>{});
-    if (rc) rc = go(std::integral_constant<int, 1>{});
+    if (big) rc = go(std::integral_constant<int, 2>{}, std::integral_constant<int, 2>{});
+    if (rc) rc = go(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
     if (rc) {
         set_error("router: hidden size %d too large for the staged router", H);
         return ANEDVD_E_INVALID_ARG;
@@ -407,9 +495,10 @@ __device__ inline ListOpts list_opts(const Dispatch &d) { return ListOpts{d.chun
 // Wavefront 0 of the dispatch: offsets[E+1], the active experts, the chunk list
 // and meta from the per-expert counts in s.cnt (4 experts per lane, E <= 256);
 // s.off gets the offsets.
+template <class S>
 __device__ __forceinline__ void dispatch_offsets(int E, int lane, int32_t *__restrict__ offsets, int32_t *__restrict__ active,
                                  int32_t *__restrict__ meta, uint64_t *__restrict__ chunks, int chunk, int n_routed,
-                                 ListOpts lo, DispLds &s, bool write = true)
+                                 ListOpts lo, S &s, bool write = true)
 {
     uint64_t *__restrict__ chunks_s = lo.chunks_s;
     const int small = lo.small;
@@ -720,8 +809,10 @@ struct RouteArgs {
     int n_sh;            // shared expert pieces (experts E .. E+n_sh-1), written by the conversion
     const uint16_t *sh_lin;  // shared gate vector [H] f16, or null (scale 1)
     // With `rwt` (fused route and dispatch only) the routing workgroup forms the
-    // logits itself from x: the router lane-major (rwt) and as stored (rw).
-    const uint16_t *rwt, *rw;
+    // logits itself from x: the router in the router kernel's layout (rwt) and as
+    // stored (rw).
+    const float *rwt;
+    const uint16_t *rw;
 };
 
 constexpr int kRouteWaves = 4;      // tokens per routing workgroup, one per wavefront
@@ -781,6 +872,7 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a)
 __device__ inline void router_chains(const RouteArgs &a, float (*lg)[kMaxExperts], float *xs)
 {
     const int J = a.H >> 3, H8 = J * 8, JP = router_stride(J);  // xs: [T][8][JP]
+    const int NB = (int)router_blocks(a.H), NBF = J / 8;
     for (int i = threadIdx.x; i < a.T * H8; i += kDispThreads) {
         const int t = i / H8, c = i - t * H8;
         xs[(t * 8 + (c & 7)) * JP + (c >> 3)] = a.x[(size_t)t * a.H + c];
@@ -790,24 +882,29 @@ __device__ inline void router_chains(const RouteArgs &a, float (*lg)[kMaxExperts
     if ((int)(threadIdx.x & ~63u) >= n) return;  // a wavefront with no chain (uniform; the caller's barrier follows)
     const int ch = min((int)threadIdx.x, n - 1);  // lanes past the chains repeat the last (not stored)
     const int t = ch / (a.E * 8), e = (ch >> 3) % a.E, l = ch & 7;
-    const uint16_t *wr = a.rwt + ((size_t)e * 8 + l) * J;
+    // chain l of expert e in the router layout: block jb's 8 j's at wr + jb 64 64
+    const float *wr = a.rwt + ((size_t)(e / kRouterGroup) * NB * kRouterGroup + e % kRouterGroup) * 64 + 8 * l;
+    const size_t bstride = (size_t)kRouterGroup * 64;
     const float *xr = xs + (t * 8 + l) * JP;
     float acc = 0.0f;
-    int j = 0;
-    if ((J & 7) == 0) {
-        // 8 j's per 16-byte load, the next one issued before this one's adds
-        const uint4 *w16 = (const uint4 *)wr;
-        uint4 cur = w16[0];
-        for (; j < J; j += 8) {
-            const uint4 nxt = w16[min(j + 8, J - 8) >> 3];
-            const uint32_t ww[4] = {cur.x, cur.y, cur.z, cur.w};
+    if (NB > 0) {
+        // 8 j's per two 16-byte loads, the next block's issued before this one's adds
+        float4 c0 = *(const float4 *)wr, c1 = *(const float4 *)(wr + 4);
+        auto add = [&](int jb, int nq) {
+            const float wf[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
             for (int q = 0; q < 8; q++)
-                acc = __fadd_rn(acc, __fmul_rn(xr[j + q], f16_bits_to_f32((uint16_t)(ww[q >> 1] >> (16 * (q & 1))))));
-            cur = nxt;
+                if (q < nq) acc = __fadd_rn(acc, __fmul_rn(xr[8 * jb + q], wf[q]));
+        };
+        for (int jb = 0; jb < NBF; jb++) {
+            const float *nw = wr + (size_t)min(jb + 1, NB - 1) * bstride;
+            const float4 n0 = *(const float4 *)nw, n1 = *(const float4 *)(nw + 4);
+            add(jb, 8);
+            c0 = n0;
+            c1 = n1;
         }
+        if (NB > NBF) add(NBF, J - 8 * NBF);
     }
-    for (; j < J; j++) acc = __fadd_rn(acc, __fmul_rn(xr[j], f16_bits_to_f32(wr[j])));
     float sum = __shfl(acc, (threadIdx.x & ~7), 64);
     for (int q = 1; q < 8; q++) sum = __fadd_rn(sum, __shfl(acc, (threadIdx.x & ~7) + q, 64));
     if ((int)threadIdx.x < n && l == 0) {
@@ -866,14 +963,32 @@ __global__ __launch_bounds__(kDispThreads) void k_dispatch(const uint32_t *__res
 
 // Dispatch of more entries than one workgroup ranks at once, by kDispBlock-entry
 // blocks, one workgroup each and no communication between them.  Every workgroup
-// counts all P entries per expert (the totals give the offsets) and, apart, the
-// entries before its block; then it ranks its own block's entries the way
-// dispatch_segments does (each wavefront 64 entries, same-id lanes found with
-// nine ballots, a prefix over the wavefronts): position = offset[e] + entries of
-// e in earlier blocks + earlier in this block.  Workgroup 0 also writes the
-// offsets, the active experts, the chunk list and meta.  The order is the
-// single-workgroup dispatch's: entries ascending within an expert.
+// counts all P entries per expert (the totals give the offsets), apart those of
+// the blocks before its own (their sum is its base per expert), and ranks its own
+// block's entries the way dispatch_segments does (each wavefront 64 entries,
+// same-id lanes found with nine ballots, a prefix over the wavefronts): position =
+// offset[e] + entries of e in earlier blocks + earlier in this block.  Workgroup 0
+// also writes the offsets, the active experts, the chunk list and meta.  The order
+// is the single-workgroup dispatch's: entries ascending within an expert.
+//
+// The counting: wavefront w takes the batches of 64 entries at 1024 q + 64 w (so
+// its batch of this block is the one it ranks), every batch's ids loaded before the
+// first barrier (one memory round trip); each entry adds one to its expert in the
+// wavefront's own LDS row (before / this / after the block) with one LDS atomic per
+// batch, no contention between wavefronts, and the rows are summed per expert
+// once.  The nine-ballot match runs on the block's own batch only: on every batch
+// it took 6.7 us of the 10.6 us DeepSeek-V2-Lite 1024-token dispatch (8192 entries,
+// each workgroup's VALU on one CU).
 constexpr int kDispBlock = kDispThreads;  // entries per workgroup: one per thread
+constexpr int kDispWaves = kDispThreads / 64;
+
+struct MultiLds {
+    int32_t cnt[kMaxExperts];   // all entries of e
+    int32_t off[kMaxExperts];   // offsets (dispatch_offsets)
+    int32_t base[kMaxExperts];  // entries of e in blocks before this one
+    int32_t bef[kDispWaves][kMaxExperts], own[kDispWaves][kMaxExperts], aft[kDispWaves][kMaxExperts];
+    int32_t bad;
+};
 
 // Lanes of the wavefront holding the same 9-bit id as this lane (ids >= E and
 // padding all share 0x1FF, which no expert has).
@@ -892,73 +1007,76 @@ __device__ inline uint64_t same_id_lanes(uint32_t e)
 __global__ __launch_bounds__(kDispThreads) void k_dispatch_multi(const uint32_t *__restrict__ idx, int P, int k, int E,
                                                                  Dispatch d)
 {
-    constexpr int NW = kDispThreads / 64;
-    static_assert(NW * kMaxExperts <= kDispWords, "per-wavefront counts live in the bitmap's words");
-    __shared__ DispLds s;
+    constexpr int NW = kDispWaves, kB = 8;
+    constexpr int kIt = 64 * NW * kB;  // entries per round of batches
+    __shared__ MultiLds s;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int i0 = (int)blockIdx.x * kDispBlock;  // this block's first entry (a multiple of 64)
-    int32_t *wcnt = reinterpret_cast<int32_t *>(s.bits);  // [NW][kMaxExperts]: this block's counts per wavefront
-    for (int e = tid; e < E; e += kDispThreads) {
-        s.cnt[e] = 0;   // all entries of e
-        s.base[e] = 0;  // entries of e before this block
-    }
-    for (int i = tid; i < NW * kMaxExperts; i += kDispThreads) wcnt[i] = 0;
-    if (tid == 0) s.bad = 0;
-    const int i = i0 + 64 * wv + lane;  // this thread's entry of the block
-    uint32_t e = i < P ? idx[i] : 0x1FFu;
-    __syncthreads();
-    // 1. counts over all entries, 64 at a time per wavefront (eight batches' ids
-    // loaded at once); a group's lowest lane adds its size
-    constexpr int kB = 8;
-    int bad = 0;
-    for (int r0 = 64 * wv; r0 < P; r0 += 64 * NW * kB) {  // uniform per wavefront
-        uint32_t ids[kB];
+    const int blk = blockIdx.x, i0 = blk * kDispBlock;  // this block's first entry
+    const uint64_t below_mask = (1ull << lane) - 1ull;
+    uint32_t ids[kB];
+    auto load = [&](int r) {
 #pragma unroll
         for (int q = 0; q < kB; q++) {
-            const int j = r0 + 64 * NW * q + lane;
+            const int j = r + 1024 * q + 64 * wv + lane;
             ids[q] = j < P ? idx[j] : 0x1FFu;
         }
+    };
+    load(0);
+    for (int i = tid; i < NW * kMaxExperts; i += kDispThreads) {
+        (&s.bef[0][0])[i] = 0;
+        (&s.own[0][0])[i] = 0;
+        (&s.aft[0][0])[i] = 0;
+    }
+    if (tid == 0) s.bad = 0;
+    __syncthreads();
+    int bad = 0, below = 0;
+    uint32_t mine = 0x1FFu;  // this thread's entry of the block (0x1FF: none or id >= E)
+    for (int r = 0; r < P; r += kIt) {
+        if (r) load(r);
 #pragma unroll
         for (int q = 0; q < kB; q++) {
-            const int b0 = r0 + 64 * NW * q;
+            const int b0 = r + 1024 * q + 64 * wv, bq = b0 >> 10;  // the batch's first entry and its block
             if (b0 >= P) break;  // uniform
             uint32_t x = ids[q];
             if (x >= (uint32_t)E) {
                 bad += b0 + lane < P;
                 x = 0x1FFu;
             }
-            const uint64_t same = same_id_lanes(x);
-            if (x < (uint32_t)E && __popcll(same & ((1ull << lane) - 1ull)) == 0) {
-                const int c = __popcll(same);
-                atomicAdd(&s.cnt[x], c);
-                if (b0 < i0) atomicAdd(&s.base[x], c);
+            if (bq == blk) {  // this block's batch: ranks within the wavefront
+                mine = x;
+                below = __popcll(same_id_lanes(x) & below_mask);
             }
+            int32_t *row = bq < blk ? s.bef[wv] : bq == blk ? s.own[wv] : s.aft[wv];
+            if (x < (uint32_t)E) atomicAdd(&row[x], 1);  // the wavefront's own row
         }
     }
     if (bad) atomicAdd(&s.bad, bad);
-    // 2. this block's entries: wavefront w the 64 from i0 + 64 w, ranked within the wavefront
-    if (e >= (uint32_t)E) e = 0x1FFu;
-    const uint64_t same = same_id_lanes(e);
-    const int below = __popcll(same & ((1ull << lane) - 1ull));
-    if (e < (uint32_t)E && below == 0) wcnt[wv * kMaxExperts + e] = __popcll(same);
     __syncthreads();
-    // 3. the wavefronts' exclusive prefix per expert, and the offsets
+    // per expert: the totals, the base, and the wavefronts' exclusive prefix of this
+    // block's counts in place
     for (int x = tid; x < E; x += kDispThreads) {
-        int run = 0;
+        int b = 0, a = 0, run = 0;
+#pragma unroll
         for (int w = 0; w < NW; w++) {
-            const int v = wcnt[w * kMaxExperts + x];
-            wcnt[w * kMaxExperts + x] = run;
+            b += s.bef[w][x];
+            a += s.aft[w][x];
+            const int v = s.own[w][x];
+            s.own[w][x] = run;
             run += v;
         }
+        s.base[x] = b;
+        s.cnt[x] = b + run + a;
     }
-    if (wv == NW - 1) dispatch_offsets(E, lane, d.offsets, d.active, d.meta, d.chunks, d.chunk, d.n_routed, list_opts(d),
-                                      s, blockIdx.x == 0);
     __syncthreads();
-    // 4. positions
+    if (wv == NW - 1) dispatch_offsets(E, lane, d.offsets, d.active, d.meta, d.chunks, d.chunk, d.n_routed, list_opts(d),
+                                      s, blk == 0);
+    __syncthreads();
+    // positions of this block's entries
+    const int i = i0 + 64 * wv + lane;
     if (i < P) {
         int pos = -1;
-        if (e < (uint32_t)E) {
-            pos = s.off[e] + s.base[e] + wcnt[wv * kMaxExperts + e] + below;
+        if (mine < (uint32_t)E) {
+            pos = s.off[mine] + s.base[mine] + s.own[wv][mine] + below;
             d.rows[pos] = i / k;
             d.slots[pos] = i % k;
         }
@@ -1033,7 +1151,7 @@ bool route_router_fusable(int T, int E, int H)
 
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                               const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
-                              const SharedSlots &sh, const uint16_t *d_rwt, const uint16_t *d_rw)
+                              const SharedSlots &sh, const float *d_rwt, const uint16_t *d_rw)
 {
     if (!d_logits && (!d_rwt || !d_rw || !d_x || !route_router_fusable(T, E, H))) {
         set_error("route: no logits, and the router cannot be fused into this call (%d tokens, %d experts)", T, E);

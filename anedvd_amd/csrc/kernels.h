@@ -55,10 +55,12 @@ int launch_f16_to_f32(const uint16_t *d_src, float *d_dst, size_t n, hipStream_t
 constexpr int kMaxRouteExperts = 256;  // experts the route and dispatch kernels take (ids fit a byte)
 constexpr int kMaxRouteSlots = 32;     // slots per token
 // cpu.matmulF16 of T rows of x against the [E][H] f16 router: d_wt is the router
-// in the kernel's lane-major layout (launch_router_layout, E * (H & ~7) halves),
-// d_w the [E][H] matrix itself (read only for a tail of H % 8 columns).
-int launch_router_layout(const uint16_t *d_w, int E, int H, uint16_t *d_wt, hipStream_t st);
-int launch_router(const uint16_t *d_wt, const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits,
+// in the kernel's layout (launch_router_layout: f32, interleaved for the chains,
+// router_layout_floats(E, H) floats), d_w the [E][H] matrix itself (read only for
+// a tail of H % 8 columns).
+size_t router_layout_floats(int E, int H);
+int launch_router_layout(const uint16_t *d_w, int E, int H, float *d_wt, hipStream_t st);
+int launch_router(const float *d_wt, const uint16_t *d_w, const float *d_x, int T, int E, int H, float *d_logits,
                   hipStream_t st);
 // cpu.moeRoute for T rows of logits; with d_x non-null the same launch also
 // converts x [T][H] to the GEMV activation format `xq`.
@@ -77,12 +79,12 @@ int launch_dispatch(const uint32_t *d_idx, int T, int k, int E, const Dispatch &
 // one-workgroup dispatch launch.
 bool route_fusable(int T, int E);
 // route_router_fusable(T, E, H): the fused launch can also form the router logits
-// (a chain per thread); then d_logits is null and d_rwt / d_rw the router
-// (lane-major, as stored), and d_x the call's activations.
+// (a chain per thread); then d_logits is null and d_rwt / d_rw the router (in
+// launch_router_layout's layout, as stored), and d_x the call's activations.
 bool route_router_fusable(int T, int E, int H);
 int launch_route_and_dispatch(const float *d_logits, int T, int E, int k, int norm, float *d_probs, uint32_t *d_idx,
                               const float *d_x, int H, const ActQ &xq, const Dispatch &d, hipStream_t st,
-                              const SharedSlots &sh = {}, const uint16_t *d_rwt = nullptr,
+                              const SharedSlots &sh = {}, const float *d_rwt = nullptr,
                               const uint16_t *d_rw = nullptr);
 int launch_act_prep(const float *d_x, int rows, int K, const ActQ &xq, hipStream_t st);
 

@@ -57,7 +57,7 @@ struct anedvd_moe_layer {
     int norm = 0, gelu = 0;
     QMat gate{}, up{}, down{};
     uint16_t *router = nullptr;    // [E][H] f16
-    uint16_t *router_t = nullptr;  // the router kernel's lane-major copy (launch_router_layout)
+    float *router_t = nullptr;  // the router kernel's f32 interleaved copy (launch_router_layout)
     uint32_t Is = 0;
     uint32_t n_sh = 0;  // shared expert merged as n_sh expert-width pieces after the E routed experts
     QMat sgate{}, sup{}, sdown{};  // the shared expert when it is not merged
@@ -550,8 +550,8 @@ int anedvd_moe_layer_create(anedvd_moe_ctx *ctx, const anedvd_moe_layer_desc *d,
                        sdn, nsh);
     if (!rc) {
         // the router as given ([E][H], for a tail of H % 8 columns) and in the router
-        // kernel's lane-major layout
-        const size_t rb = (size_t)E * H * 2, rtb = (size_t)E * (H & ~7) * 2;
+        // kernel's layout (f32, interleaved for its chains)
+        const size_t rb = (size_t)E * H * 2, rtb = router_layout_floats(E, H) * 4;
         if (hipMalloc(&L->router, rb) != hipSuccess || hipMalloc(&L->router_t, rtb) != hipSuccess ||
             hipMemcpy(L->router, d->router, rb, hipMemcpyHostToDevice) != hipSuccess) {
             set_error("router upload failed");
@@ -728,10 +728,11 @@ int anedvd_matmul_f16(anedvd_moe_ctx *ctx, float *out, const uint16_t *w, const 
     if (!n_vec) return ANEDVD_OK;
     ANEDVD_HIP(hipSetDevice(ctx->device));
     const size_t wb = out_dim * in_dim * 2, xb = n_vec * in_dim * 4, ob = n_vec * out_dim * 4;
-    ANEDVD_TRY(ensure(ctx->io, 2 * wb + xb + ob + 1024, ctx->stream));
+    const size_t nwt = router_layout_floats((int)out_dim, (int)in_dim);
+    ANEDVD_TRY(ensure(ctx->io, wb + nwt * 4 + xb + ob + 1024, ctx->stream));
     Carve c{(uint8_t *)ctx->io.base};
     uint16_t *dw = c.take<uint16_t>(out_dim * in_dim);
-    uint16_t *dwt = c.take<uint16_t>(out_dim * in_dim);
+    float *dwt = c.take<float>(nwt);
     float *dx = c.take<float>(n_vec * in_dim);
     float *dout = c.take<float>(n_vec * out_dim);
     ANEDVD_HIP(hipMemcpyAsync(dw, w, wb, hipMemcpyHostToDevice, ctx->stream));
