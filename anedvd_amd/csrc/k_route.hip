@@ -766,23 +766,46 @@ __device__ __forceinline__ void act_prep_wave(const float *__restrict__ x, int r
 {
     if (w >= (size_t)rows) return;
     const float *xr = x + w * K;
-    const int G = K / 64;
+    const int G = K / 64, R = K / 8;  // 64-column groups, 8-element runs
     half_t *q = xq.q + w * K;
-    constexpr int B = 64;  // groups held in registers: one round trip for K <= 4096
-    if (G <= B) {
-        float v[B];
-#pragma unroll
-        for (int b = 0; b < B; b++) v[b] = b < G ? xr[64 * b + lane] : 0.0f;
+    // Run r (elements 8r .. 8r + 7) of group r / 8 lands at 16 (a & 3) + 8 (a >> 2),
+    // a = r % 8, within its group in mma_pos order: eight contiguous halves.  Lane l
+    // takes runs l, l + 64, ...: two 16-byte loads and one 16-byte store each, the
+    // whole row in registers for K <= 64 kB 8 (one memory round trip).
+    constexpr int kB = 8;
+    if (R <= 64 * kB) {
+        float4 v[kB][2];
         float m = 0.0f;
 #pragma unroll
-        for (int b = 0; b < B; b++) m = fmaxf(m, fabsf(v[b]));
+        for (int b = 0; b < kB; b++) {
+            const int r = lane + 64 * b;
+            if (r < R) {
+                v[b][0] = *(const float4 *)(xr + 8 * r);
+                v[b][1] = *(const float4 *)(xr + 8 * r + 4);
+            } else {
+                v[b][0] = v[b][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kB; b++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[b][h].x), fabsf(v[b][h].y)), fmaxf(fabsf(v[b][h].z), fabsf(v[b][h].w))));
         const float sc = pow2_scale(wave_max(m)), inv = 1.0f / sc;
 #pragma unroll
-        for (int b = 0; b < B; b++)
-            if (b < G) {
-                q[64 * b + mma_pos(lane)] = (half_t)(v[b] * sc);
-                if (lane == 0) xq.ds[(size_t)b * xq.ld + w] = inv;
+        for (int b = 0; b < kB; b++) {
+            const int r = lane + 64 * b;
+            if (r < R) {
+                const int a = r & 7;
+                half8 o;
+                o[0] = (_Float16)(v[b][0].x * sc); o[1] = (_Float16)(v[b][0].y * sc);
+                o[2] = (_Float16)(v[b][0].z * sc); o[3] = (_Float16)(v[b][0].w * sc);
+                o[4] = (_Float16)(v[b][1].x * sc); o[5] = (_Float16)(v[b][1].y * sc);
+                o[6] = (_Float16)(v[b][1].z * sc); o[7] = (_Float16)(v[b][1].w * sc);
+                *(half8 *)(q + 64 * (r >> 3) + 16 * (a & 3) + 8 * (a >> 2)) = o;
             }
+        }
+        for (int g = lane; g < G; g += 64) xq.ds[(size_t)g * xq.ld + w] = inv;
         return;
     }
     float m = 0.0f;
