@@ -76,18 +76,20 @@ __global__ void k_router_layout(const uint16_t *__restrict__ w, int E, int H, fl
 }
 
 // Block: 256 threads = 32 lane groups x 8 chains, 32 EX experts.  Grid:
-// (ceil(E / (32 EX)), ceil(T / TT)).
+// (ceil(E / (32 EX)), ceil(T / TT)), or the two swapped (`tx`, tokens on x) when the
+// token blocks pass the 65536 limit of the grid's y.
 template <int TT, int EX>
 __global__ __launch_bounds__(256) void k_router(const float *__restrict__ wt, const uint16_t *__restrict__ w,
                                                 const float *__restrict__ x, int T, int E, int H,
-                                                float *__restrict__ logits)
+                                                float *__restrict__ logits, int tx)
 {
+    const int tb = tx ? blockIdx.x : blockIdx.y, eb = tx ? blockIdx.y : blockIdx.x;
     static_assert(EX == 1 || EX == 2, "a block's experts lie in one layout group");
     extern __shared__ float xs[];  // [TT][8][JP]
     const int J = H >> 3, H8 = J * 8, JP = router_stride(J), NB = (int)router_blocks(H), NBF = J / 8;
-    const int t0 = blockIdx.y * TT;
+    const int t0 = tb * TT;
     const int nt = min(TT, T - t0);
-    const int e0 = blockIdx.x * 32 * EX;  // the block's first expert
+    const int e0 = eb * 32 * EX;  // the block's first expert
     // The block's experts: layout group e0 / 64, from expert e0 % 64 of it (0, or 32
     // when EX = 1); a block of the group is 64 x 256 bytes.
     const rsrc_t rs = make_rsrc(wt + ((size_t)(e0 / kRouterGroup) * NB * kRouterGroup + e0 % kRouterGroup) * 64,
@@ -255,13 +257,20 @@ int launch_router(const float *d_wt, const uint16_t *d_w, const float *d_x, int 
         constexpr int TT = decltype(tt)::value, EX = decltype(ex)::value;
         const size_t lds = (size_t)TT * 8 * router_stride(H >> 3) * 4;
         if (lds > 65536) return -1;
-        hipLaunchKernelGGL((k_router<TT, EX>), dim3((E + 32 * EX - 1) / (32 * EX), (T + TT - 1) / TT), dim3(256), lds,
-                           st, d_wt, d_w, d_x, T, E, H, d_logits);
+        const unsigned nt = (unsigned)((T + TT - 1) / TT), ne = (unsigned)((E + 32 * EX - 1) / (32 * EX));
+        if (ne > 65536u && nt > 65536u) return -2;
+        const int tx = nt > 65536u;
+        hipLaunchKernelGGL((k_router<TT, EX>), tx ? dim3(nt, ne) : dim3(ne, nt), dim3(256), lds, st, d_wt, d_w, d_x, T, E,
+                           H, d_logits, tx);
         return 0;
     };
     int rc = -1;
     if (big) rc = go(std::integral_constant<int, 2>{}, std::integral_constant<int, 2>{});
     if (rc) rc = go(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    if (rc == -2) {
+        set_error("router: %d tokens x %d experts is too many for one launch", T, E);
+        return ANEDVD_E_INVALID_ARG;
+    }
     if (rc) {
         set_error("router: hidden size %d too large for the staged router", H);
         return ANEDVD_E_INVALID_ARG;
