@@ -88,15 +88,16 @@ def test_resident_experts_bit_exact(ctx, types):
 @pytest.mark.parametrize("out_dim,in_dim,n", [(128, 2048, 1), (128, 2048, 64), (8, 512, 16), (64, 2048, 3),
                                               (7, 300, 5), (8, 4096, 2), (64, 2048, 1024), (128, 2048, 512),
                                               (100, 1003, 700), (8, 4096, 300), (70, 5, 3), (64, 2048, 1025),
-                                              (100, 1003, 5), (8, 64, 70000)])
+                                              (100, 1003, 5), (8, 64, 70000), (256, 1024, 300)])
 def test_matmul_f16_bit_exact(ctx, out_dim, in_dim, n):
     """The router GEMV (cpu.matmulF16's chains) at the shapes of both launch forms:
     a token and an expert per lane, and two of each (>= 64 experts and >= 65536
     token-expert pairs: (64, 2048, 1024), (128, 2048, 512), and (100, 1003, 700) with
     a partial second expert half and a partial last 8-j block plus a scalar tail; an
     odd token count, whose last workgroup has one token), a hidden size below one
-    block (70, 5, 3), and more token blocks than a grid's y dimension takes (8, 64,
-    70000: tokens run on x)."""
+    block (70, 5, 3), more token blocks than a grid's y dimension takes (8, 64,
+    70000: tokens run on x), and four 64-expert groups at two experts per lane (256,
+    1024, 300)."""
     w = (synth.normal(1, out_dim, out_dim * in_dim) * 0.02).astype(np.float16).reshape(out_dim, in_dim)
     x = synth.normal(2, in_dim, n * in_dim).astype(np.float32).reshape(n, in_dim)
     got = ctx.matmul_f16(w, x)
