@@ -1247,7 +1247,10 @@ int launch_combine(const float *ypart, const int32_t *inv, const float *probs, i
         return ANEDVD_E_INVALID_ARG;
     }
     const size_t threads = (size_t)T * (H / 4);
-    if (threads >= 65536) {  // enough (token, column) threads to fill the GPU: slots in order per thread
+    // From 32768 (token, column) threads on, one thread per column group with its
+    // slots in order: the Qwen3 B=64 step (32768) 119.1-119.4 -> 117.7 us against the
+    // slot-parallel kernel; at B=32 (16384) the slot-parallel one is as fast or faster.
+    if (threads >= 32768) {
         const dim3 grid((unsigned)((threads + 255) / 256));
         if (k <= 2)  // as many slot loads per pass as there are slots (Mixtral: 2, not 8 clamped copies)
             hipLaunchKernelGGL(k_combine_rows<2>, grid, dim3(256), 0, st, ypart, inv, probs, T, k, H, KS, P, shared,
